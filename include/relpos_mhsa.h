@@ -1,0 +1,263 @@
+/*
+ * relpos_mhsa.h - C ABI of the MI355X (gfx950) FastConformer rel-pos MHSA path.
+ *
+ * Drop-in boundary for the attention sublayer of animaslabs/mlx-nemo-rs
+ * (crate mlx-voice 0.3.0). Each entry point names the reference interface it
+ * replaces (paths relative to the reference repository):
+ *
+ *   RelPositionMultiHeadAttention   src/asr/modules/encoders/attention.rs:328-893
+ *   RelPositionalEncoding           src/asr/modules/encoders/attention.rs:19-194
+ *   AttentionContext                src/asr/modules/encoders/attention.rs:208-273
+ *   key_padding_mask                src/asr/modules/encoders/attention.rs:275-294
+ *   LinearLayer / QuantizationConfig src/core/quantization.rs:17-162, 289-349
+ *   streaming mask + cache          src/asr/modules/encoders/conformer.rs:97-323, 840-1047
+ *   MHSA sublayer (pre-LN+residual) src/asr/modules/encoders/conformer.rs:1747-1780
+ *
+ * Conventions
+ *  - Plain C types only. Activations, caches and outputs are DEVICE pointers
+ *    owned by the caller, in the layer's dtype (fp32 or bf16), row-major,
+ *    16-byte aligned. Weights are passed as HOST pointers and uploaded into a
+ *    kernel-native layout owned by the layer handle.
+ *  - Lengths and fill levels are HOST arrays, as in the reference
+ *    (conformer.rs:852-857), so no call waits on the GPU.
+ *  - Calls are asynchronous on the given HIP stream (hipStream_t passed as
+ *    void*; NULL = the null stream). Weight uploads and debug exports are
+ *    synchronous.
+ *  - A handle is not reentrant (the reference takes &mut self,
+ *    attention.rs:446, 606); different handles may be used from different
+ *    threads.
+ *  - Every function returns a status; on failure mhsa_last_error() gives a
+ *    thread-local message. No exceptions or aborts cross the ABI.
+ */
+#ifndef RELPOS_MHSA_H
+#define RELPOS_MHSA_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes (reference: Result<T, Error>, src/core/error.rs:7-12) */
+#define MHSA_OK 0
+#define MHSA_ENOMEM 12
+#define MHSA_EINVAL 22       /* bad shape / argument (Error::Model, MLX shape errors) */
+#define MHSA_ENOTSUP 95      /* unsupported mode (e.g. bits != 8, group != 64) */
+#define MHSA_ENOENT 2        /* strict load: a tensor is missing (loading.rs:107-116) */
+#define MHSA_EHIP 1000       /* HIP runtime error; the message names it */
+
+/* dtypes (mlx_rs::Dtype subset) */
+#define MHSA_F32 0
+#define MHSA_BF16 1
+#define MHSA_F16 2
+#define MHSA_U32 3
+
+/* projections of one layer (attention.rs:333-342) */
+#define MHSA_LINEAR_Q 0
+#define MHSA_LINEAR_K 1
+#define MHSA_LINEAR_V 2
+#define MHSA_LINEAR_OUT 3
+#define MHSA_LINEAR_POS 4
+
+typedef struct mhsa_layer mhsa_layer;
+typedef struct mhsa_stream mhsa_stream;
+
+/* AttentionContext (attention.rs:211-227): left/right context in frames,
+ * -1 = unlimited; chunked = 1 for the "chunked_limited" style. A context with
+ * left < 0 and right < 0 means full attention (AttentionContext::new -> None). */
+typedef struct {
+  int32_t left;
+  int32_t right;
+  int32_t chunked;
+} mhsa_context;
+
+/* Streaming attention mask, built in-kernel from the parameters
+ * create_attention_mask takes (conformer.rs:97-221):
+ *  present      0 = the encoder has no att_context_size: no mask at all
+ *  ctx          att_context_size and style
+ *  filled_host  [B] cache fill per session (NULL = the stream's own count);
+ *               the reference uses session 0's fill for every session
+ *               (conformer.rs:883-887), this is the per-session superset
+ *  valid_host   [B] valid query rows per session (NULL = all); rows past it
+ *               see no key and yield zeros, as the reference's bool path */
+typedef struct {
+  int32_t present;
+  mhsa_context ctx;
+  const int32_t* filled_host;
+  const int32_t* valid_host;
+} mhsa_stream_mask;
+
+/* Named host tensor for mhsa_load_weights (the Weights map, loading.rs:81). */
+typedef struct {
+  const char* name;
+  int32_t dtype;     /* MHSA_F32 / MHSA_BF16 / MHSA_F16 / MHSA_U32 */
+  int32_t ndim;
+  int64_t shape[4];
+  const void* data;  /* host pointer, row-major */
+} mhsa_tensor;
+
+/* ---- errors / library -------------------------------------------------- */
+
+/* Thread-local message of the last failing call (error.rs Display). */
+const char* mhsa_last_error(void);
+/* ABI version (major * 100 + minor). */
+int32_t mhsa_version(void);
+
+/* ---- layer lifecycle ---------------------------------------------------- */
+
+/* RelPositionMultiHeadAttention::new(d_model, n_heads, use_bias)
+ * (attention.rs:367-406). Weights start at zero, dtype fp32. Kernels support
+ * head_dim 64 or 128 and d_model a multiple of 128. */
+int32_t mhsa_create(int32_t d_model, int32_t n_heads, int32_t use_bias, mhsa_layer** out);
+void mhsa_destroy(mhsa_layer* layer);
+/* set_dtype (attention.rs:409-423): MHSA_F32 or MHSA_BF16. Drops the
+ * streaming position memo, as the reference does (attention.rs:421). */
+int32_t mhsa_set_dtype(mhsa_layer* layer, int32_t dtype);
+int32_t mhsa_get_dtype(const mhsa_layer* layer);
+/* head_dim(), n_heads() (attention.rs:426-433) */
+int32_t mhsa_head_dim(const mhsa_layer* layer);
+int32_t mhsa_n_heads(const mhsa_layer* layer);
+int32_t mhsa_d_model(const mhsa_layer* layer);
+/* pub cache_drop_size (attention.rs:349-350), set by setup_streaming
+ * (conformer.rs:812-817) */
+int32_t mhsa_set_cache_drop_size(mhsa_layer* layer, int32_t cache_drop_size);
+
+/* ---- weights ------------------------------------------------------------ */
+
+/* LinearLayer::standard(weight [out,in], bias [out] | NULL)
+ * (quantization.rs:62-65). data_dtype: MHSA_F32 / MHSA_BF16 / MHSA_F16.
+ * linear_pos never takes a bias (attention.rs:385). */
+int32_t mhsa_load_linear_standard(mhsa_layer* layer, int32_t which, int32_t data_dtype, const void* weight,
+                                  const void* bias);
+/* LinearLayer::quantized (quantization.rs:67-82): MLX affine layout
+ * weight u32 [out, in*bits/32], scales and biases f16 [out, in/group],
+ * bias f16 [out] | NULL. Only bits = 8, group_size = 64 are supported
+ * (the reference's default, quantization.rs:307). */
+int32_t mhsa_load_linear_quantized(mhsa_layer* layer, int32_t which, const uint32_t* weight,
+                                   const uint16_t* scales_f16, const uint16_t* biases_f16,
+                                   const uint16_t* bias_f16, int32_t bits, int32_t group_size);
+/* pos_bias_u / pos_bias_v [n_heads, head_dim] (attention.rs:344-347, 388-389). */
+int32_t mhsa_load_pos_bias(mhsa_layer* layer, int32_t data_dtype, const void* pos_bias_u, const void* pos_bias_v);
+/* load_weights(weights, prefix, quant) (attention.rs:863-893): resolves
+ * {prefix}.linear_{q,k,v,out,pos}.{weight,bias,scales,biases} and
+ * {prefix}.pos_bias_{u,v}; a layer is quantized iff .scales and .biases exist
+ * (quantization.rs:299-304), with (quant_bits, quant_group) or (8, 64) when
+ * quant_bits <= 0 (quantization.rs:307). strict != 0 fails with MHSA_ENOENT on
+ * the first missing tensor (loading.rs:107-116); otherwise missing tensors
+ * keep their values. */
+int32_t mhsa_load_weights(mhsa_layer* layer, const mhsa_tensor* tensors, int32_t n_tensors, const char* prefix,
+                          int32_t strict, int32_t quant_bits, int32_t quant_group);
+
+/* ---- offline forward ---------------------------------------------------- */
+
+/* forward(x, pos_emb, context, key_mask) (attention.rs:446-573).
+ *  x        [batch, seq_len, d_model] device, layer dtype
+ *  pos_emb  [pos_len, d_model] device, layer dtype: the table
+ *           get_encoding(seq_len) gives (pos_len = 2*seq_len-1), or a centred
+ *           band of 2W+1 rows (distances W..-W) when `context` hides every
+ *           pair farther apart than W (a local window)
+ *  ctx      NULL = full attention
+ *  key_lengths_host [batch] valid frames per item (key_padding_mask,
+ *           attention.rs:280-294; values clamped to >= 1), NULL = no padding
+ *  out      [batch, seq_len, d_model] device, layer dtype
+ * Only the position rows the context can reach are projected. */
+int32_t mhsa_forward(mhsa_layer* layer, const void* x, int32_t batch, int32_t seq_len, const void* pos_emb,
+                     int32_t pos_len, const mhsa_context* ctx, const int32_t* key_lengths_host, void* out,
+                     void* hip_stream);
+
+/* x <- x + forward(LayerNorm(x)) : the MHSA sublayer of ConformerBlock
+ * (conformer.rs:1747-1780). ln_gamma / ln_beta [d_model] HOST fp32 arrays
+ * (NULL = 1 / 0), eps as nn::LayerNorm (1e-5). */
+int32_t mhsa_sublayer_forward(mhsa_layer* layer, void* x_inout, int32_t batch, int32_t seq_len,
+                              const float* ln_gamma_host, const float* ln_beta_host, float eps,
+                              const void* pos_emb, int32_t pos_len, const mhsa_context* ctx,
+                              const int32_t* key_lengths_host, void* hip_stream);
+
+/* ---- cache-aware streaming ---------------------------------------------- */
+
+/* Streaming state of one layer for `batch` sessions: the attention cache of
+ * `cache_size` frames (EncoderCache::last_channel slice, streaming/core.rs:
+ * 117-166) kept as an HBM ring of C + chunk_len rows holding the cached
+ * normalised inputs h and their projected K and V, plus each session's
+ * fill. Zero-filled at creation, like EncoderCache::new. Only fp32 layers. */
+int32_t mhsa_stream_create(mhsa_layer* layer, int32_t batch, int32_t cache_size, int32_t chunk_len,
+                           mhsa_stream** out);
+void mhsa_stream_destroy(mhsa_stream* stream);
+/* Replace the cache with `cache` [batch, cache_size, d_model] (device, fp32,
+ * oldest frame first) and set the fill levels (filled_host [batch], NULL = 0).
+ * K/V of the cached rows are projected here. */
+int32_t mhsa_stream_load_cache(mhsa_stream* stream, const void* cache, const int32_t* filled_host,
+                               void* hip_stream);
+/* Copy the cache out in the reference layout [batch, cache_size, d_model]. */
+int32_t mhsa_stream_read_cache(const mhsa_stream* stream, void* cache_out, void* hip_stream);
+/* Current fill level of each session [batch] (host). */
+int32_t mhsa_stream_fill(const mhsa_stream* stream, int32_t* filled_out_host);
+
+/* forward_with_cache(x, pos_emb, cache, _, att_mask) (attention.rs:606-816)
+ * followed by the encoder's cache pad/truncate and fill update
+ * (conformer.rs:983-999, 1025-1036).
+ *  x       [batch, chunk_len, d_model] device fp32 (the normalised input h)
+ *  pos_emb [2*(cache_size+chunk_len)-1, d_model] device fp32; its projection
+ *          is memoised per pos_len as the reference does (attention.rs:749-761)
+ *  mask    NULL = no mask (att_context_size absent)
+ *  out     [batch, chunk_len, d_model] device fp32
+ * Afterwards the cache holds [cache[q_keep:]; x[:q_keep]] (q_keep =
+ * chunk_len - cache_drop_size) and fill = min(fill + q_keep, cache_size). */
+int32_t mhsa_forward_with_cache(mhsa_layer* layer, mhsa_stream* stream, const void* x, const void* pos_emb,
+                                int32_t pos_len, const mhsa_stream_mask* mask, void* out, void* hip_stream);
+
+/* ---- helpers ------------------------------------------------------------ */
+
+/* RelPositionalEncoding::new(d_model, max_len).get_encoding(seq_len)
+ * (attention.rs:59-103, 131-177) into a HOST fp32 buffer
+ * [2*seq_len-1, d_model]; seq_len > max_len regenerates the table. */
+int32_t mhsa_pos_encoding(int32_t d_model, int32_t max_len, int32_t seq_len, float* out_host);
+
+/* ---- per-kernel timing --------------------------------------------------- */
+
+/* No counterpart in the reference (it times whole calls with wall clocks,
+ * examples/eval.rs:181-183, 289-295). When enabled, every kernel the layer
+ * launches is bracketed by HIP events on the launch stream; totals accumulate
+ * per kernel tag (gemm_qkv, gemm_pos, attention, gemm_out, layer_norm,
+ * gemm_q, gemm_kv, ring_write). Reading waits for the recorded events. */
+int32_t mhsa_profile_enable(mhsa_layer* layer, int32_t enable);
+int32_t mhsa_profile_reset(mhsa_layer* layer);
+/* Number of distinct tags recorded so far (flushes pending events). */
+int32_t mhsa_profile_count(mhsa_layer* layer);
+/* Entry idx: tag name (valid until the next reset), total ms and launches. */
+int32_t mhsa_profile_entry(mhsa_layer* layer, int32_t idx, const char** name, double* total_ms, int32_t* launches);
+
+/* ---- debug exports (bit-exact checks) ----------------------------------- */
+
+/* Dequantised weight [out, in] of a quantized projection, as the GEMM loader
+ * produces it in the current dtype, widened to fp32 (device output). */
+int32_t mhsa_debug_dequantize(mhsa_layer* layer, int32_t which, float* out_dev, void* hip_stream);
+/* One projection alone, LinearLayer::forward (quantization.rs:126-162):
+ * out [rows, d_model] = x [rows, d_model] W^T (+ bias), device, layer dtype,
+ * through the same GEMM kernels the forward pass uses. */
+int32_t mhsa_debug_linear(mhsa_layer* layer, int32_t which, const void* x, int32_t rows, void* out_dev,
+                          void* hip_stream);
+/* Visibility map [batch, seq_len, seq_len] (1 = visible) the offline kernel
+ * applies for (ctx, key lengths) (device output). */
+int32_t mhsa_debug_offline_mask(int32_t batch, int32_t seq_len, const mhsa_context* ctx,
+                                const int32_t* key_lengths_host, uint8_t* out_dev, void* hip_stream);
+/* Visibility map [batch, chunk_len, cache_size + chunk_len] the streaming
+ * kernel applies (device output); filled_host must be given. */
+int32_t mhsa_debug_stream_mask(int32_t batch, int32_t cache_size, int32_t chunk_len, const mhsa_stream_mask* mask,
+                               uint8_t* out_dev, void* hip_stream);
+/* Position-table row read for every (query i, key j) pair [rows, total_len]
+ * (device output): the closed form of rel_shift + truncation
+ * (attention.rs:831-855) as the kernel evaluates it. */
+int32_t mhsa_debug_rel_shift_index(int32_t rows, int32_t total_len, int32_t* out_dev, void* hip_stream);
+/* Scaled position scores cast(s) * rel_shift(q_v P^T)[..., :seq_len]
+ * [batch, n_heads, seq_len, seq_len] fp32 (device), computed by the fused
+ * kernel's MFMA + LDS remap path, for a full-attention offline call. */
+int32_t mhsa_debug_position_scores(mhsa_layer* layer, const void* x, int32_t batch, int32_t seq_len,
+                                   const void* pos_emb, int32_t pos_len, float* out_dev, void* hip_stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RELPOS_MHSA_H */

@@ -1,0 +1,365 @@
+// Fused Transformer-XL relative-position attention for one head slice.
+//
+// Replaces, per query block, the reference's
+//   q_u = q + pos_bias_u, q_v = q + pos_bias_v        (attention.rs:501-508)
+//   bd = rel_shift(q_v P^T)[..., :L]                  (attention.rs:524-532, 818-855)
+//   mask = context mask + key padding mask            (attention.rs:229-294, 536-543)
+//   softmax(s q_u K^T + cast(s) bd + mask) V          (attention.rs:296-318)
+// and the streaming bool-mask path where a fully hidden row yields zeros
+// (attention.rs:774-790), with no [rows, 2L-1] score matrix in memory.
+//
+// Work split (gfx950, 64-wide waves): a workgroup owns QB = 16*NW queries of
+// one (batch, head); each wave owns 16 queries. Keys advance in tiles of NK
+// (64 for bf16, 32 for fp32) staged in LDS together with V^T and the band of
+// QB+NK position rows the tile's (query, key) pairs can reach. Per tile and
+// wave:
+//   S^T  = K  . Qu^T   (NK x 16)       MFMA, K as the A operand
+//   B'^T = P' . Qv^T   ((NK+16) x 16)  MFMA over the wave's position band
+//   rel_shift: bd(j, i) = B'^T(j + 15 - i, i), an index remap through LDS
+//   online fp32 softmax per query column, then O^T += V^T . Pr^T (MFMA)
+// Scores stay in fp32 registers; probabilities are rounded to the compute
+// dtype for the PV MFMA. Key tiles that no query of the block can see are
+// skipped, so a +-w local window costs O(T w) instead of O(T^2).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace mhsa {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ bool ctx_visible(const AttnParams& p, int ia, int j) {
+  if (!p.has_ctx) return true;
+  if (p.chunked && p.right >= 0) {
+    const int chunk = p.right + 1;
+    const int lc = p.left >= 0 ? p.left / chunk : 10000;
+    const int d = ia / chunk - j / chunk;
+    return d >= 0 && d <= lc;
+  }
+  bool vis = p.left < 0 || j - ia >= -p.left;
+  if (!p.chunked && p.right >= 0) vis = vis && j - ia <= p.right;
+  return vis;
+}
+
+__device__ __forceinline__ bool pair_visible(const AttnParams& p, int bl, int i, int j) {
+  return i < p.q_valid[bl] && j >= p.key_lo[bl] && j < p.key_hi[bl] && ctx_visible(p, p.qoff + i, j);
+}
+
+__device__ __forceinline__ int key_row(const AttnParams& p, int j) {
+  return p.ring_len ? (p.ring_head + j) % p.ring_len : j;
+}
+
+// Keys [jbeg, jend) that can be visible to some query in [i0, i_end).
+__device__ __forceinline__ void key_range(const AttnParams& p, int bl, int i0, int i_end, int& jbeg,
+                                          int& jend) {
+  const int row_end = min(i_end, p.q_valid[bl]);
+  jbeg = max(p.key_lo[bl], 0);
+  jend = min(p.key_hi[bl], p.L);
+  if (row_end <= i0) {
+    jend = jbeg;
+    return;
+  }
+  if (!p.has_ctx) return;
+  const int a0 = p.qoff + i0, a1 = p.qoff + row_end - 1;
+  if (p.chunked && p.right >= 0) {
+    const int chunk = p.right + 1;
+    const int lc = p.left >= 0 ? p.left / chunk : 10000;
+    const long lo = ((long)(a0 / chunk) - lc) * chunk;
+    jbeg = max(jbeg, (int)max(lo, 0L));
+    jend = min(jend, (a1 / chunk + 1) * chunk);
+  } else {
+    if (p.left >= 0) jbeg = max(jbeg, a0 - p.left);
+    if (!p.chunked && p.right >= 0) jend = min(jend, a1 + p.right + 1);
+  }
+}
+
+template <typename T, int DK, int NW>
+struct Cfg {
+  static constexpr int NT = 64 * NW;
+  static constexpr int QB = 16 * NW;
+  static constexpr int NK = sizeof(T) == 2 ? 64 : 32;
+  static constexpr int RB = DK * (int)sizeof(T);           // bytes per K/P row
+  static constexpr int KP = RB + 16;                       // LDS pitch of K and P rows
+  static constexpr int VP = NK * (int)sizeof(T) + 16;      // LDS pitch of V^T rows
+  static constexpr int PR = QB + NK;                       // position rows staged per tile
+  static constexpr int RMP = NK + 20;                      // remap row pitch (floats)
+  static constexpr int K_OFF = 0;
+  static constexpr int V_OFF = K_OFF + NK * KP;
+  static constexpr int P_OFF = V_OFF + DK * VP;
+  static constexpr int R_OFF = P_OFF + PR * KP;
+  static constexpr int LDS = R_OFF + NW * 16 * RMP * 4;
+  static constexpr int NKF = DK / Frag<T>::KSTEP;          // fragments along d_k
+  static constexpr int NU = NK / 16;                       // 16-key sub-tiles
+  static constexpr int NB = NU + 1;                        // 16-row band sub-tiles
+};
+
+template <typename T, int DK, int NW, bool DEBUG>
+__global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
+  using C = Cfg<T, DK, NW>;
+  using F = Frag<T>;
+  using frag_t = typename F::type;
+  constexpr int NT = C::NT, QB = C::QB, NK = C::NK, EPL = F::EPL;
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS];
+  char* Ks = smem + C::K_OFF;
+  char* Vt = smem + C::V_OFF;
+  char* Ps = smem + C::P_OFF;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, ql = lane & 15;
+  const int bl = blockIdx.z, b = p.b0 + bl, h = blockIdx.y;
+  const int i0 = blockIdx.x * QB;
+  const int qi = i0 + 16 * w + ql;  // this lane's query column
+  float* Rm = reinterpret_cast<float*>(smem + C::R_OFF) + w * 16 * C::RMP;
+
+  // Queries with the position biases folded in, rounded like the reference's
+  // bf16 adds; they are the B operand of both score products.
+  frag_t qu[C::NKF], qv[C::NKF];
+  {
+    const T* qrow = reinterpret_cast<const T*>(p.q) + (int64_t)b * p.q_bs + (int64_t)qi * p.q_rs + h * DK;
+    const bool ok = qi < p.T;
+#pragma unroll
+    for (int kf = 0; kf < C::NKF; ++kf) {
+      const int d0 = kf * F::KSTEP + g * EPL;
+      const frag_t raw = load16<frag_t>(qrow + d0, ok);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const float x = (float)raw[e];
+        qu[kf][e] = from_float<T>(ok ? x + p.bias_u[h * DK + d0 + e] : 0.f);
+        qv[kf][e] = from_float<T>(ok ? x + p.bias_v[h * DK + d0 + e] : 0.f);
+      }
+    }
+  }
+
+  floatx4 o[DK / 16];
+#pragma unroll
+  for (int d = 0; d < DK / 16; ++d) o[d] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  int jbeg, jend;
+  key_range(p, bl, i0, min(i0 + QB, p.T), jbeg, jend);
+  const float sc_qk = p.scale * kLog2e, sc_bd = p.scale_bd * kLog2e;
+  const char* kbase = reinterpret_cast<const char*>(p.k) + ((int64_t)b * p.kv_bs + h * DK) * sizeof(T);
+  const char* vbase = reinterpret_cast<const char*>(p.v) + ((int64_t)b * p.kv_bs + h * DK) * sizeof(T);
+  const char* pbase = reinterpret_cast<const char*>(p.p) + (int64_t)h * DK * sizeof(T);
+
+  for (int j0 = (jbeg / NK) * NK; j0 < jend; j0 += NK) {
+    __syncthreads();  // previous tile fully consumed
+    // K rows and V^T (transposed on the way in), zero past the last key.
+    constexpr int CPR = C::RB / 16;
+    for (int c = tid; c < NK * CPR; c += NT) {
+      const int row = c / CPR, cb = (c % CPR) * 16;
+      const int j = j0 + row;
+      const bool ok = j < p.L;
+      const int64_t off = (int64_t)(ok ? key_row(p, j) : 0) * p.kv_rs * sizeof(T) + cb;
+      *reinterpret_cast<uint4*>(Ks + row * C::KP + cb) = load16<uint4>(kbase + off, ok);
+      const frag_t vv = load16<frag_t>(vbase + off, ok);
+      const int d0 = cb / (int)sizeof(T);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e)
+        *reinterpret_cast<T*>(Vt + (d0 + e) * C::VP + row * (int)sizeof(T)) = vv[e];
+    }
+    // Position rows pmin .. pmin + PR - 1 (zero outside the table).
+    const int pmin = p.center - p.qoff - (i0 + QB - 1) + j0;
+    for (int c = tid; c < C::PR * CPR; c += NT) {
+      const int row = c / CPR, cb = (c % CPR) * 16;
+      const int tp = pmin + row;
+      const bool ok = tp >= 0 && tp < p.p_rows;
+      *reinterpret_cast<uint4*>(Ps + row * C::KP + cb) =
+          load16<uint4>(pbase + (int64_t)(ok ? tp : 0) * p.p_rs * sizeof(T) + cb, ok);
+    }
+    __syncthreads();
+
+    // S^T = K Qu^T and the wave's band B'^T = P' Qv^T.
+    floatx4 s[C::NU], bd[C::NB];
+#pragma unroll
+    for (int u = 0; u < C::NU; ++u) s[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < C::NB; ++t) bd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int band0 = QB - 16 - 16 * w;  // first band row of this wave
+#pragma unroll
+    for (int kf = 0; kf < C::NKF; ++kf) {
+      const int cb = kf * 64 + g * 16;
+#pragma unroll
+      for (int u = 0; u < C::NU; ++u) {
+        const frag_t a = *reinterpret_cast<const frag_t*>(Ks + (16 * u + ql) * C::KP + cb);
+        s[u] = mma16(a, qu[kf], s[u]);
+      }
+#pragma unroll
+      for (int t = 0; t < C::NB; ++t) {
+        const frag_t a = *reinterpret_cast<const frag_t*>(Ps + (band0 + 16 * t + ql) * C::KP + cb);
+        bd[t] = mma16(a, qv[kf], bd[t]);
+      }
+    }
+
+    // rel_shift as an LDS remap: band row n of query column ql holds the
+    // pair (i = 16w + ql, j = n - 15 + ql).
+#pragma unroll
+    for (int t = 0; t < C::NB; ++t)
+      *reinterpret_cast<floatx4*>(Rm + ql * C::RMP + 16 * t + 4 * g) = bd[t];
+    __builtin_amdgcn_wave_barrier();
+
+    float sc[C::NU][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < C::NU; ++u) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int jl = 16 * u + 4 * g + r;
+        const int j = j0 + jl;
+        const float bdv = Rm[ql * C::RMP + jl + 15 - ql];
+        if (DEBUG && qi < p.T && j < p.L)
+          p.dbg_bd[(((int64_t)b * p.H + h) * p.T + qi) * p.L + j] = p.scale_bd * bdv;
+        const float v = s[u][r] * sc_qk + bdv * sc_bd;
+        sc[u][r] = pair_visible(p, bl, qi, j) ? v : -INFINITY;
+        tmax = fmaxf(tmax, sc[u][r]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    tmax = col_max(tmax);
+    // Branch-free (the MFMAs below run wave-wide): a column with nothing
+    // visible yet keeps alpha = 0 and all-zero probabilities.
+    const float m_new = fmaxf(m_run, tmax);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m_run - m_use);
+    m_run = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int u = 0; u < C::NU; ++u)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sc[u][r] = exp2f(sc[u][r] - m_use);
+        psum += sc[u][r];
+      }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int d = 0; d < DK / 16; ++d) o[d] *= alpha;
+
+    // O^T += V^T Pr^T. The contraction slots of a fragment map to the keys
+    // this lane already holds in S^T layout: keys 16u + 4g + r.
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int u = 0; u < C::NU; u += 2) {
+        bf16x8 pb;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          pb[r] = (bf16)sc[u][r];
+          pb[4 + r] = (bf16)sc[u + 1][r];
+        }
+#pragma unroll
+        for (int d = 0; d < DK / 16; ++d) {
+          const char* vr = Vt + (16 * d + ql) * C::VP;
+          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vr + (16 * u + 4 * g) * 2);
+          const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vr + (16 * (u + 1) + 4 * g) * 2);
+          const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          o[d] = mma16(a, pb, o[d]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < C::NU; ++u) {
+        const floatx4 pb = {sc[u][0], sc[u][1], sc[u][2], sc[u][3]};
+#pragma unroll
+        for (int d = 0; d < DK / 16; ++d) {
+          const floatx4 a = *reinterpret_cast<const floatx4*>(Vt + (16 * d + ql) * C::VP + (16 * u + 4 * g) * 4);
+          o[d] = mma16(a, pb, o[d]);
+        }
+      }
+    }
+  }
+
+  // Normalise; a query that saw no key outputs zeros.
+  const float l_tot = col_sum(l_run);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (qi < p.T) {
+    T* orow = reinterpret_cast<T*>(p.o) + (int64_t)b * p.o_bs + (int64_t)qi * p.o_rs + h * DK;
+#pragma unroll
+    for (int d = 0; d < DK / 16; ++d) {
+      T vals[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) vals[r] = from_float<T>(o[d][r] * inv);
+      if constexpr (sizeof(T) == 2) {
+        *reinterpret_cast<uint2*>(orow + 16 * d + 4 * g) = *reinterpret_cast<const uint2*>(vals);
+      } else {
+        *reinterpret_cast<uint4*>(orow + 16 * d + 4 * g) = *reinterpret_cast<const uint4*>(vals);
+      }
+    }
+  }
+}
+
+template <typename T, int DK, int NW, bool DEBUG>
+hipError_t launch(const AttnParams& p, int nb, hipStream_t s) {
+  using C = Cfg<T, DK, NW>;
+  dim3 grid((p.T + C::QB - 1) / C::QB, p.H, nb);
+  hipLaunchKernelGGL((attn_kernel<T, DK, NW, DEBUG>), grid, dim3(C::NT), 0, s, p);
+  return hipGetLastError();
+}
+
+template <typename T, int DK>
+hipError_t dispatch_nw(const AttnParams& p, int nb, hipStream_t s) {
+  const bool dbg = p.dbg_bd != nullptr;
+  if (p.T <= 16) return dbg ? launch<T, DK, 1, true>(p, nb, s) : launch<T, DK, 1, false>(p, nb, s);
+  return dbg ? launch<T, DK, 4, true>(p, nb, s) : launch<T, DK, 4, false>(p, nb, s);
+}
+
+bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+__global__ void mask_kernel(const AttnParams p, uint8_t* out) {
+  const int bl = blockIdx.y;
+  const int64_t n = (int64_t)p.T * p.L;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int i = (int)(e / p.L), j = (int)(e % p.L);
+    out[bl * n + e] = pair_visible(p, bl, i, j) ? 1 : 0;
+  }
+}
+
+__global__ void pos_index_kernel(int T, int L, int qoff, int center, int32_t* out) {
+  const int64_t n = (int64_t)T * L;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
+    const int i = (int)(e / L), j = (int)(e % L);
+    // the same expression the attention kernel stages its position band with:
+    // row pmin + (band0 + n) for n = (j - j0) + 15 - (i - i0 - 16w)
+    out[e] = center - (qoff + i) + j;
+  }
+}
+
+}  // namespace
+
+hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStream_t s) {
+  if (nb <= 0 || p.T <= 0) return hipSuccess;
+  if (nb > kMaxBatch || p.L <= 0 || p.H <= 0 || p.p_rows <= 0) return hipErrorInvalidValue;
+  if (!p.q || !p.k || !p.v || !p.p || !p.o || !p.bias_u || !p.bias_v) return hipErrorInvalidValue;
+  if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.p) || !aligned16(p.o))
+    return hipErrorInvalidValue;
+  const int epv = 16 / dtype_size(dt);
+  if (p.q_rs % epv || p.q_bs % epv || p.kv_rs % epv || p.kv_bs % epv || p.p_rs % epv || p.o_rs % epv ||
+      p.o_bs % epv)
+    return hipErrorInvalidValue;
+  if (p.ring_len < 0 || (p.ring_len && p.ring_head < 0)) return hipErrorInvalidValue;
+  if (dt == kF32) {
+    if (head_dim == 64) return dispatch_nw<float, 64>(p, nb, s);
+    if (head_dim == 128) return dispatch_nw<float, 128>(p, nb, s);
+  } else {
+    if (head_dim == 64) return dispatch_nw<bf16, 64>(p, nb, s);
+    if (head_dim == 128) return dispatch_nw<bf16, 128>(p, nb, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t export_mask(const AttnParams& p, int nb, uint8_t* out, hipStream_t s) {
+  if (nb <= 0 || p.T <= 0 || p.L <= 0) return hipSuccess;
+  if (nb > kMaxBatch || !out) return hipErrorInvalidValue;
+  const int64_t n = (int64_t)p.T * p.L;
+  dim3 grid((unsigned)std::min<int64_t>((n + 255) / 256, 4096), nb);
+  hipLaunchKernelGGL(mask_kernel, grid, dim3(256), 0, s, p, out);
+  return hipGetLastError();
+}
+
+hipError_t export_pos_index(int T, int L, int qoff, int center, int32_t* out, hipStream_t s) {
+  if (T <= 0 || L <= 0) return hipSuccess;
+  if (!out) return hipErrorInvalidValue;
+  const int64_t n = (int64_t)T * L;
+  hipLaunchKernelGGL(pos_index_kernel, dim3((unsigned)std::min<int64_t>((n + 255) / 256, 4096)), dim3(256), 0, s,
+                     T, L, qoff, center, out);
+  return hipGetLastError();
+}
+
+}  // namespace mhsa

@@ -1,0 +1,90 @@
+// Launch interface between the host runtime (mhsa_api.hip) and the gfx950
+// kernels (gemm.hip, attention.hip, misc.hip). Every launcher checks the shape
+// assumptions its kernel relies on and returns a hipError_t (or
+// hipErrorInvalidValue when a shape does not fit the kernel).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mhsa {
+
+enum DType : int { kF32 = 0, kBF16 = 1 };
+
+inline int dtype_size(DType d) { return d == kF32 ? 4 : 2; }
+
+// C[out_row(r), n] = epilogue( sum_k A[r, k] * W[n, k] )
+//   dense W: [N, K] in the compute dtype; quantized W: uint32 [N, K/4] holding
+//   one u8 code per byte, with `sb` = [N, K/64] {scale, bias} float pairs.
+//   out_row(r) = (r / seg_rows) * seg_stride + (ring_off + r % seg_rows) % ring_len
+// Epilogue (reference order): y = T(acc); y = T(y + bias[n]); y = T(R[r, n] + y).
+struct GemmParams {
+  const void* A = nullptr;
+  int64_t lda = 0;
+  const void* W = nullptr;
+  const float* sb = nullptr;
+  const float* bias = nullptr;
+  const void* R = nullptr;
+  int64_t ldr = 0;
+  void* C = nullptr;
+  int64_t ldc = 0;
+  int M = 0, N = 0, K = 0;
+  int seg_rows = 0, seg_stride = 0, ring_off = 0, ring_len = 0;
+};
+hipError_t gemm(DType dt, bool quantized, const GemmParams& p, hipStream_t s);
+
+constexpr int kMaxBatch = 64;
+
+// Fused rel-pos attention over one head slice per (query tile, head, batch).
+// Query i of batch b sits at absolute frame qoff + i; key j at frame j and is
+// stored at row (ring_head + j) % ring_len (row j when ring_len == 0). The
+// position row of pair (i, j) is center - (qoff + i) + j (the closed form of
+// the Transformer-XL rel_shift). Key j is visible to query i iff
+// key_lo[b] <= j < key_hi[b], i < q_valid[b], and the context rule holds.
+struct AttnParams {
+  const void* q = nullptr;
+  int64_t q_bs = 0, q_rs = 0;
+  const void* k = nullptr;
+  const void* v = nullptr;
+  int64_t kv_bs = 0, kv_rs = 0;
+  int ring_head = 0, ring_len = 0;
+  const void* p = nullptr;
+  int64_t p_rs = 0;
+  int p_rows = 0, center = 0;
+  const float* bias_u = nullptr;  // [H, dk], values in the compute dtype
+  const float* bias_v = nullptr;
+  void* o = nullptr;
+  int64_t o_bs = 0, o_rs = 0;
+  float* dbg_bd = nullptr;  // debug: scaled position scores [B, H, T, L]
+  int T = 0, L = 0, qoff = 0, H = 0;
+  float scale = 0.f, scale_bd = 0.f;
+  int has_ctx = 0, left = -1, right = -1, chunked = 0;
+  int b0 = 0;
+  int key_lo[kMaxBatch];
+  int key_hi[kMaxBatch];
+  int q_valid[kMaxBatch];
+};
+hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nbatch, hipStream_t s);
+
+// Visibility map [nbatch, T, L] (1 = visible) from the same predicate the
+// attention kernel applies.
+hipError_t export_mask(const AttnParams& p, int nbatch, uint8_t* out, hipStream_t s);
+// Position-row index of every (i, j) pair [T, L], as the attention kernel computes it.
+hipError_t export_pos_index(int T, int L, int qoff, int center, int32_t* out, hipStream_t s);
+
+// y = T(LayerNorm(x) * gamma + beta), statistics in fp32; gamma/beta may be null.
+hipError_t layer_norm(DType dt, const void* x, void* y, const float* gamma, const float* beta,
+                      float eps, int rows, int D, hipStream_t s);
+
+// Ring copies between a contiguous [B, n, D] block and a ring [B, R, ld]
+// (row t of batch b <-> ring row (off + t) % R, columns [0, D)).
+hipError_t ring_write(DType dt, const void* src, void* ring, int B, int n, int D, int R, int64_t ld,
+                      int off, hipStream_t s);
+hipError_t ring_read(DType dt, const void* ring, void* dst, int B, int n, int D, int R, int64_t ld,
+                     int off, hipStream_t s);
+
+// Dequantised weight [N, K] as the GEMM's loader produces it, widened to fp32.
+hipError_t dequant_export(DType dt, const uint32_t* w, const float* sb, float* out, int N, int K,
+                          hipStream_t s);
+
+}  // namespace mhsa

@@ -1,0 +1,1031 @@
+// Host runtime of the rel-pos MHSA library: the C ABI declared in
+// include/relpos_mhsa.h, mirroring RelPositionMultiHeadAttention
+// (attention.rs:328-893), LinearLayer (quantization.rs:36-162) and the
+// encoder's streaming cache bookkeeping (conformer.rs:840-1047).
+//
+// A layer handle keeps fp32 master copies of its parameters and uploads them
+// on first use after a change into kernel-native device layouts for its
+// dtype: q/k/v rows stacked as one [3D, D] operand (one fused GEMM when all
+// three have the same kind), dense weights in the compute dtype, affine u8
+// codes as stored plus {scale, bias} float pairs, biases pre-rounded to the
+// compute dtype.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/relpos_mhsa.h"
+#include "kernels.hpp"
+
+using mhsa::DType;
+
+namespace {
+
+thread_local std::string g_err;
+
+int32_t fail(int32_t code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIPCHK(expr)                                                                               \
+  do {                                                                                             \
+    hipError_t e_ = (expr);                                                                        \
+    if (e_ != hipSuccess) return fail(MHSA_EHIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_), \
+                                      __FILE__, __LINE__);                                         \
+  } while (0)
+
+float bits_to_f32(uint32_t u) {
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+uint32_t f32_to_bits(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  return u;
+}
+// bf16 round-to-nearest-even (no NaNs on this path).
+uint16_t f32_to_bf16(float f) {
+  uint32_t u = f32_to_bits(f);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+float bf16_to_f32(uint16_t b) { return bits_to_f32((uint32_t)b << 16); }
+float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
+float f16_to_f32(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1Fu, man = h & 0x3FFu;
+  if (exp == 0) {
+    if (man == 0) return bits_to_f32(sign);
+    // subnormal: value = man * 2^-24
+    float v = std::ldexp((float)man, -24);
+    return sign ? -v : v;
+  }
+  if (exp == 31) return bits_to_f32(sign | 0x7F800000u | (man << 13));
+  return bits_to_f32(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+float load_host(int32_t dtype, const void* data, size_t i) {
+  switch (dtype) {
+    case MHSA_F32: return static_cast<const float*>(data)[i];
+    case MHSA_BF16: return bf16_to_f32(static_cast<const uint16_t*>(data)[i]);
+    case MHSA_F16: return f16_to_f32(static_cast<const uint16_t*>(data)[i]);
+    default: return 0.f;
+  }
+}
+bool float_dtype(int32_t d) { return d == MHSA_F32 || d == MHSA_BF16 || d == MHSA_F16; }
+
+struct HostLinear {
+  bool quantized = false;
+  std::vector<float> w;          // standard [out, in]
+  std::vector<float> bias;       // [out], empty = none
+  std::vector<uint32_t> codes;   // quantized [out, in/4]
+  std::vector<float> qs, qb;     // quantized scales / biases [out, in/64]
+};
+
+struct DevLinear {
+  bool quantized = false;
+  const void* w = nullptr;   // dense [N, K] (compute dtype) or u32 codes
+  const float* sb = nullptr; // [N, K/64, 2]
+  const float* bias = nullptr;
+};
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t n = 0;
+  ~DevBuf() { release(); }
+  void release() {
+    if (p) (void)hipFree(p);
+    p = nullptr;
+    n = 0;
+  }
+  hipError_t ensure(size_t bytes) {
+    if (bytes <= n) return hipSuccess;
+    release();
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e == hipSuccess) n = bytes;
+    else p = nullptr;
+    return e;
+  }
+};
+
+int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+
+// Per-kernel HIP-event timing on the launch stream (off unless enabled).
+struct Profiler {
+  bool on = false;
+  struct Pair {
+    hipEvent_t a = nullptr, b = nullptr;
+    std::string tag;
+  };
+  std::vector<Pair> pool;
+  size_t used = 0;
+  std::vector<std::string> names;
+  std::vector<double> ms;
+  std::vector<int> count;
+
+  ~Profiler() {
+    for (Pair& p : pool) {
+      if (p.a) (void)hipEventDestroy(p.a);
+      if (p.b) (void)hipEventDestroy(p.b);
+    }
+  }
+  int begin(const char* tag, hipStream_t s) {
+    if (!on) return -1;
+    if (used == pool.size()) {
+      Pair p;
+      if (hipEventCreate(&p.a) != hipSuccess || hipEventCreate(&p.b) != hipSuccess) return -1;
+      pool.push_back(p);
+    }
+    Pair& p = pool[used];
+    p.tag = tag;
+    if (hipEventRecord(p.a, s) != hipSuccess) return -1;
+    return (int)used++;
+  }
+  void end(int idx, hipStream_t s) {
+    if (idx >= 0) (void)hipEventRecord(pool[idx].b, s);
+  }
+  // Wait for the recorded pairs and fold them into the totals.
+  void flush() {
+    for (size_t i = 0; i < used; ++i) {
+      float t = 0.f;
+      if (hipEventSynchronize(pool[i].b) != hipSuccess || hipEventElapsedTime(&t, pool[i].a, pool[i].b) != hipSuccess)
+        continue;
+      size_t k = 0;
+      while (k < names.size() && names[k] != pool[i].tag) ++k;
+      if (k == names.size()) {
+        names.push_back(pool[i].tag);
+        ms.push_back(0.0);
+        count.push_back(0);
+      }
+      ms[k] += t;
+      count[k] += 1;
+    }
+    used = 0;
+  }
+};
+
+}  // namespace
+
+struct mhsa_layer {
+  int D = 0, H = 0, dk = 0;
+  bool use_bias = false;
+  DType dt = mhsa::kF32;
+  int cache_drop = 0;
+  HostLinear lin[5];
+  std::vector<float> pbu, pbv;
+  bool dirty = true;
+  // device parameters
+  DevBuf wbuf;
+  DevLinear dev[5];
+  bool qkv_fused = false;
+  const float* d_pbu = nullptr;
+  const float* d_pbv = nullptr;
+  // scratch
+  DevBuf ws;
+  DevBuf hbuf;                 // sublayer: LayerNorm output
+  DevBuf ln_dev;               // sublayer: LayerNorm gamma, beta
+  std::vector<float> ln_host;  // values currently in ln_dev
+  // streaming position memo (attention.rs:749-761)
+  DevBuf pmemo;
+  int pmemo_len = -1;
+  Profiler prof;
+};
+
+namespace {
+// Brackets the kernels launched in its scope with a profiling event pair.
+struct ProfScope {
+  Profiler& p;
+  hipStream_t s;
+  int idx;
+  ProfScope(mhsa_layer* L, const char* tag, hipStream_t s_) : p(L->prof), s(s_), idx(L->prof.begin(tag, s_)) {}
+  ~ProfScope() { p.end(idx, s); }
+  // Close the current span and open the next one.
+  void next(const char* tag) {
+    p.end(idx, s);
+    idx = p.begin(tag, s);
+  }
+};
+}  // namespace
+
+struct mhsa_stream {
+  mhsa_layer* layer = nullptr;
+  int B = 0, C = 0, Tc = 0, R = 0;
+  int head = 0;
+  std::vector<int32_t> fill;
+  DevBuf ring_h;   // [B, R, D] fp32
+  DevBuf ring_kv;  // [B, R, 2D] fp32 (K columns then V columns)
+  DevBuf ws;
+};
+
+namespace {
+
+DType dtype_of(const mhsa_layer* L) { return L->dt; }
+size_t esz(const mhsa_layer* L) { return (size_t)mhsa::dtype_size(L->dt); }
+
+// Upload the parameters in the layer's dtype (no-op when clean).
+int32_t prepare(mhsa_layer* L) {
+  if (!L->dirty) return MHSA_OK;
+  const int D = L->D;
+  const bool bf = L->dt == mhsa::kBF16;
+  const size_t es = esz(L);
+  auto rnd = [&](float v) { return bf ? round_bf16(v) : v; };
+  const bool q0 = L->lin[0].quantized;
+  L->qkv_fused = L->lin[1].quantized == q0 && L->lin[2].quantized == q0;
+
+  // Layout: [qkv weights][out][pos] then sb blocks, biases, pos biases.
+  const size_t dense_b = (size_t)D * D * es, codes_b = (size_t)D * D, sb_b = (size_t)D * (D / 64) * 2 * 4;
+  std::vector<size_t> woff(5), sboff(5), boff(5);
+  size_t off = 0;
+  for (int i = 0; i < 5; ++i) {
+    woff[i] = off;
+    off += L->lin[i].quantized ? codes_b : dense_b;
+  }
+  for (int i = 0; i < 5; ++i) {
+    off = align_up(off, 256);
+    sboff[i] = off;
+    if (L->lin[i].quantized) off += sb_b;
+  }
+  off = align_up(off, 256);
+  const size_t bias_all = off;  // [3D] q/k/v bias block then out, pos
+  for (int i = 0; i < 5; ++i) boff[i] = bias_all + (size_t)i * D * 4;
+  off = bias_all + (size_t)5 * D * 4;
+  off = align_up(off, 256);
+  const size_t pb_off = off;
+  off += (size_t)2 * D * 4;
+  std::vector<char> host(off, 0);
+
+  bool any_qkv_bias = false;
+  for (int i = 0; i < 5; ++i) {
+    const HostLinear& h = L->lin[i];
+    if (h.quantized) {
+      std::memcpy(host.data() + woff[i], h.codes.data(), codes_b);
+      float* sb = reinterpret_cast<float*>(host.data() + sboff[i]);
+      for (size_t e = 0; e < h.qs.size(); ++e) {
+        sb[2 * e] = rnd(h.qs[e]);
+        sb[2 * e + 1] = rnd(h.qb[e]);
+      }
+    } else if (bf) {
+      uint16_t* w = reinterpret_cast<uint16_t*>(host.data() + woff[i]);
+      for (size_t e = 0; e < h.w.size(); ++e) w[e] = f32_to_bf16(h.w[e]);
+    } else {
+      std::memcpy(host.data() + woff[i], h.w.data(), dense_b);
+    }
+    float* b = reinterpret_cast<float*>(host.data() + boff[i]);
+    for (size_t e = 0; e < h.bias.size(); ++e) b[e] = rnd(h.bias[e]);
+    if (i < 3 && !h.bias.empty()) any_qkv_bias = true;
+  }
+  float* pb = reinterpret_cast<float*>(host.data() + pb_off);
+  for (int e = 0; e < D; ++e) {
+    pb[e] = rnd(L->pbu[e]);
+    pb[D + e] = rnd(L->pbv[e]);
+  }
+  HIPCHK(L->wbuf.ensure(host.size()));
+  HIPCHK(hipMemcpy(L->wbuf.p, host.data(), host.size(), hipMemcpyHostToDevice));
+  char* base = static_cast<char*>(L->wbuf.p);
+  for (int i = 0; i < 5; ++i) {
+    DevLinear& d = L->dev[i];
+    d.quantized = L->lin[i].quantized;
+    d.w = base + woff[i];
+    d.sb = d.quantized ? reinterpret_cast<const float*>(base + sboff[i]) : nullptr;
+    const bool has = !L->lin[i].bias.empty() || (i < 3 && L->qkv_fused && any_qkv_bias);
+    d.bias = has ? reinterpret_cast<const float*>(base + boff[i]) : nullptr;
+  }
+  // With fused q/k/v the three operands must be contiguous rows of one
+  // matrix: true for dense (woff stride D*D*es) and for codes (stride D*D).
+  L->d_pbu = reinterpret_cast<const float*>(base + pb_off);
+  L->d_pbv = L->d_pbu + D;
+  L->dirty = false;
+  L->pmemo_len = -1;
+  return MHSA_OK;
+}
+
+int32_t run_gemm(mhsa_layer* L, const DevLinear& lin, int n_rows_w, const void* A, int64_t lda, int M, void* C,
+                 int64_t ldc, const void* R, int64_t ldr, hipStream_t s, int seg_rows = 0, int seg_stride = 0,
+                 int ring_off = 0, int ring_len = 0) {
+  mhsa::GemmParams p;
+  p.A = A;
+  p.lda = lda;
+  p.W = lin.w;
+  p.sb = lin.sb;
+  p.bias = lin.bias;
+  p.R = R;
+  p.ldr = ldr;
+  p.C = C;
+  p.ldc = ldc;
+  p.M = M;
+  p.N = n_rows_w;
+  p.K = L->D;
+  p.seg_rows = seg_rows > 0 ? seg_rows : std::max(M, 1);
+  p.seg_stride = seg_rows > 0 ? seg_stride : 0;
+  p.ring_off = ring_off;
+  p.ring_len = ring_len > 0 ? ring_len : std::max(M, 1);
+  HIPCHK(mhsa::gemm(dtype_of(L), lin.quantized, p, s));
+  return MHSA_OK;
+}
+
+// q, k, v (and optionally only k, v) projections of `A` [M, D].
+int32_t project_qkv(mhsa_layer* L, const void* A, int M, void* out, int64_t ldo, hipStream_t s) {
+  const size_t es = esz(L);
+  if (L->qkv_fused) return run_gemm(L, L->dev[0], 3 * L->D, A, L->D, M, out, ldo, nullptr, 0, s);
+  for (int i = 0; i < 3; ++i) {
+    int32_t rc = run_gemm(L, L->dev[i], L->D, A, L->D, M, static_cast<char*>(out) + (size_t)i * L->D * es, ldo,
+                          nullptr, 0, s);
+    if (rc) return rc;
+  }
+  return MHSA_OK;
+}
+
+struct DistRange {
+  int dmin, dmax;  // query-minus-key frame distances a visible pair can have
+};
+
+DistRange context_distances(const mhsa_context* ctx, int qoff, int T, int L) {
+  // distances d = (qoff + i) - j over 0 <= i < T, 0 <= j < L
+  DistRange r{qoff - (L - 1), qoff + T - 1};
+  if (!ctx || (ctx->left < 0 && ctx->right < 0)) return r;
+  if (ctx->chunked && ctx->right >= 0) {
+    const int chunk = ctx->right + 1;
+    const long lc = ctx->left >= 0 ? ctx->left / chunk : 10000;
+    r.dmin = std::max(r.dmin, -(chunk - 1));
+    r.dmax = (int)std::min<long>(r.dmax, (lc + 1) * chunk - 1);
+  } else {
+    if (ctx->left >= 0) r.dmax = std::min(r.dmax, ctx->left);
+    if (!ctx->chunked && ctx->right >= 0) r.dmin = std::max(r.dmin, -ctx->right);
+  }
+  return r;
+}
+
+// Resolve the position table: full (2L-1 rows, centre L-1) or a centred band
+// the context never reaches beyond. Returns the first table row to project,
+// the row count, and the centre inside the projected rows.
+int32_t plan_positions(int pos_len, int L, const DistRange& dr, int& row0, int& nrows, int& center) {
+  if (pos_len <= 0 || pos_len % 2 == 0)
+    return fail(MHSA_EINVAL, "pos_emb must have an odd number of rows (2*len-1 or a centred band), got %d", pos_len);
+  if (dr.dmax < dr.dmin) {  // nothing visible: project a single row
+    row0 = 0;
+    nrows = 1;
+    center = 0;
+    return MHSA_OK;
+  }
+  const int c = (pos_len - 1) / 2;
+  if (pos_len > 2 * L - 1)
+    return fail(MHSA_EINVAL, "pos_emb has %d rows; expected %d (2*len-1) or fewer", pos_len, 2 * L - 1);
+  if (pos_len < 2 * L - 1 && std::max(dr.dmax, -dr.dmin) > c)
+    return fail(MHSA_EINVAL,
+                "pos_emb band of %d rows covers distances +-%d but the attention context reaches %d..%d", pos_len,
+                c, dr.dmin, dr.dmax);
+  const int lo = std::max(dr.dmin, -c), hi = std::min(dr.dmax, c);
+  row0 = c - hi;
+  nrows = hi - lo + 1;
+  center = hi;
+  return MHSA_OK;
+}
+
+float scale_f32(int dk) { return 1.0f / std::sqrt((float)dk); }
+
+void fill_attn_common(const mhsa_layer* L, mhsa::AttnParams& a) {
+  a.H = L->H;
+  a.scale = scale_f32(L->dk);
+  a.scale_bd = L->dt == mhsa::kBF16 ? round_bf16(a.scale) : a.scale;  // attention.rs:308-311
+  a.bias_u = L->d_pbu;
+  a.bias_v = L->d_pbv;
+}
+
+void set_ctx(mhsa::AttnParams& a, const mhsa_context* ctx) {
+  a.has_ctx = ctx && (ctx->left >= 0 || ctx->right >= 0);
+  a.left = ctx ? ctx->left : -1;
+  a.right = ctx ? ctx->right : -1;
+  a.chunked = ctx ? ctx->chunked != 0 : 0;
+}
+
+// Launch attention in batch chunks of kMaxBatch; `per_batch` fills the
+// per-item key range / valid rows.
+template <typename Fn>
+int32_t run_attention(const mhsa_layer* L, mhsa::AttnParams a, int B, Fn per_batch, hipStream_t s) {
+  for (int b0 = 0; b0 < B; b0 += mhsa::kMaxBatch) {
+    const int nb = std::min(mhsa::kMaxBatch, B - b0);
+    a.b0 = b0;
+    for (int i = 0; i < nb; ++i) per_batch(b0 + i, a.key_lo[i], a.key_hi[i], a.q_valid[i]);
+    HIPCHK(mhsa::attention(dtype_of(L), L->dk, a, nb, s));
+  }
+  return MHSA_OK;
+}
+
+int32_t check_layer(const mhsa_layer* L) {
+  if (!L) return fail(MHSA_EINVAL, "null layer handle");
+  return MHSA_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Offline forward shared by mhsa_forward, the sublayer and the debug export.
+int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos_emb, int pos_len,
+                     const mhsa_context* ctx, const int32_t* lens, void* out, const void* residual, float* dbg_bd,
+                     hipStream_t s) {
+  if (B <= 0 || T <= 0) return fail(MHSA_EINVAL, "batch and seq_len must be positive (got %d, %d)", B, T);
+  if (!x || !pos_emb || (!out && !dbg_bd)) return fail(MHSA_EINVAL, "null tensor pointer");
+  if (!aligned16(x) || !aligned16(pos_emb) || (out && !aligned16(out)))
+    return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  int32_t rc = prepare(L);
+  if (rc) return rc;
+  const int D = L->D;
+  const size_t es = esz(L);
+  const DistRange dr = context_distances(ctx, 0, T, T);
+  int row0, nrows, center;
+  if ((rc = plan_positions(pos_len, T, dr, row0, nrows, center))) return rc;
+
+  const int64_t M = (int64_t)B * T;
+  const size_t qkv_b = align_up(M * 3 * D * es, 256), p_b = align_up((int64_t)nrows * D * es, 256),
+               ctx_b = align_up(M * D * es, 256);
+  HIPCHK(L->ws.ensure(qkv_b + p_b + ctx_b));
+  char* qkv = static_cast<char*>(L->ws.p);
+  char* P = qkv + qkv_b;
+  char* cx = P + p_b;
+
+  {
+    ProfScope ps(L, "gemm_qkv", s);
+    if ((rc = project_qkv(L, x, (int)M, qkv, 3 * D, s))) return rc;
+  }
+  {
+    ProfScope ps(L, "gemm_pos", s);
+    if ((rc = run_gemm(L, L->dev[4], D, static_cast<const char*>(pos_emb) + (size_t)row0 * D * es, D, nrows, P, D,
+                       nullptr, 0, s)))
+      return rc;
+  }
+
+  mhsa::AttnParams a;
+  fill_attn_common(L, a);
+  a.q = qkv;
+  a.k = qkv + (size_t)D * es;
+  a.v = qkv + (size_t)2 * D * es;
+  a.q_bs = a.kv_bs = (int64_t)T * 3 * D;
+  a.q_rs = a.kv_rs = 3 * D;
+  a.p = P;
+  a.p_rs = D;
+  a.p_rows = nrows;
+  a.center = center;
+  a.o = cx;
+  a.o_bs = (int64_t)T * D;
+  a.o_rs = D;
+  a.dbg_bd = dbg_bd;
+  a.T = T;
+  a.L = T;
+  a.qoff = 0;
+  set_ctx(a, ctx);
+  {
+    ProfScope ps(L, "attention", s);
+    rc = run_attention(
+        L, a, B,
+        [&](int b, int& lo, int& hi, int& qv) {
+          lo = 0;
+          hi = lens ? std::min(std::max(lens[b], 1), T) : T;  // attention.rs:281-285
+          qv = T;
+        },
+        s);
+  }
+  if (rc) return rc;
+  if (!out) return MHSA_OK;
+  ProfScope ps(L, "gemm_out", s);
+  return run_gemm(L, L->dev[3], D, cx, D, (int)M, out, D, residual, D, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mhsa_last_error(void) { return g_err.c_str(); }
+int32_t mhsa_version(void) { return 100; }
+
+int32_t mhsa_create(int32_t d_model, int32_t n_heads, int32_t use_bias, mhsa_layer** out) {
+  if (!out) return fail(MHSA_EINVAL, "null output pointer");
+  *out = nullptr;
+  if (d_model <= 0 || n_heads <= 0 || d_model % n_heads)
+    return fail(MHSA_EINVAL, "d_model %d must be a positive multiple of n_heads %d", d_model, n_heads);
+  const int dk = d_model / n_heads;
+  if (dk != 64 && dk != 128) return fail(MHSA_ENOTSUP, "head_dim %d not supported (64 or 128)", dk);
+  if (d_model % 128) return fail(MHSA_ENOTSUP, "d_model %d must be a multiple of 128", d_model);
+  mhsa_layer* L = new (std::nothrow) mhsa_layer();
+  if (!L) return fail(MHSA_ENOMEM, "out of host memory");
+  L->D = d_model;
+  L->H = n_heads;
+  L->dk = dk;
+  L->use_bias = use_bias != 0;
+  for (int i = 0; i < 5; ++i) {
+    L->lin[i].w.assign((size_t)d_model * d_model, 0.f);
+    if (use_bias && i != MHSA_LINEAR_POS) L->lin[i].bias.assign(d_model, 0.f);
+  }
+  L->pbu.assign(d_model, 0.f);
+  L->pbv.assign(d_model, 0.f);
+  *out = L;
+  return MHSA_OK;
+}
+
+void mhsa_destroy(mhsa_layer* layer) { delete layer; }
+
+int32_t mhsa_set_dtype(mhsa_layer* L, int32_t dtype) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (dtype != MHSA_F32 && dtype != MHSA_BF16) return fail(MHSA_ENOTSUP, "dtype %d not supported (f32, bf16)", dtype);
+  L->dt = dtype == MHSA_F32 ? mhsa::kF32 : mhsa::kBF16;
+  L->dirty = true;
+  L->pmemo_len = -1;
+  return MHSA_OK;
+}
+int32_t mhsa_get_dtype(const mhsa_layer* L) { return L ? (L->dt == mhsa::kF32 ? MHSA_F32 : MHSA_BF16) : -1; }
+int32_t mhsa_head_dim(const mhsa_layer* L) { return L ? L->dk : -1; }
+int32_t mhsa_n_heads(const mhsa_layer* L) { return L ? L->H : -1; }
+int32_t mhsa_d_model(const mhsa_layer* L) { return L ? L->D : -1; }
+int32_t mhsa_set_cache_drop_size(mhsa_layer* L, int32_t n) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (n < 0) return fail(MHSA_EINVAL, "cache_drop_size must be >= 0");
+  L->cache_drop = n;
+  return MHSA_OK;
+}
+
+int32_t mhsa_load_linear_standard(mhsa_layer* L, int32_t which, int32_t dtype, const void* weight, const void* bias) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (which < 0 || which > 4) return fail(MHSA_EINVAL, "unknown projection %d", which);
+  if (!weight || !float_dtype(dtype)) return fail(MHSA_EINVAL, "weight must be f32/bf16/f16 host data");
+  HostLinear& h = L->lin[which];
+  const size_t n = (size_t)L->D * L->D;
+  h.quantized = false;
+  h.codes.clear();
+  h.qs.clear();
+  h.qb.clear();
+  h.w.resize(n);
+  for (size_t i = 0; i < n; ++i) h.w[i] = load_host(dtype, weight, i);
+  h.bias.clear();
+  if (bias) {
+    h.bias.resize(L->D);
+    for (int i = 0; i < L->D; ++i) h.bias[i] = load_host(dtype, bias, i);
+  }
+  L->dirty = true;
+  return MHSA_OK;
+}
+
+int32_t mhsa_load_linear_quantized(mhsa_layer* L, int32_t which, const uint32_t* weight, const uint16_t* scales,
+                                   const uint16_t* biases, const uint16_t* bias, int32_t bits, int32_t group) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (which < 0 || which > 4) return fail(MHSA_EINVAL, "unknown projection %d", which);
+  if (bits != 8 || group != 64)
+    return fail(MHSA_ENOTSUP, "quantization bits=%d group_size=%d not supported (8, 64)", bits, group);
+  if (!weight || !scales || !biases) return fail(MHSA_EINVAL, "null quantized tensor");
+  HostLinear& h = L->lin[which];
+  const int D = L->D, G = D / 64;
+  h.quantized = true;
+  h.w.clear();
+  h.codes.assign(weight, weight + (size_t)D * D / 4);
+  h.qs.resize((size_t)D * G);
+  h.qb.resize((size_t)D * G);
+  for (size_t i = 0; i < h.qs.size(); ++i) {
+    h.qs[i] = f16_to_f32(scales[i]);
+    h.qb[i] = f16_to_f32(biases[i]);
+  }
+  h.bias.clear();
+  if (bias) {
+    h.bias.resize(D);
+    for (int i = 0; i < D; ++i) h.bias[i] = f16_to_f32(bias[i]);
+  }
+  L->dirty = true;
+  return MHSA_OK;
+}
+
+int32_t mhsa_load_pos_bias(mhsa_layer* L, int32_t dtype, const void* u, const void* v) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (!u || !v || !float_dtype(dtype)) return fail(MHSA_EINVAL, "pos biases must be f32/bf16/f16 host data");
+  for (int i = 0; i < L->D; ++i) {
+    L->pbu[i] = load_host(dtype, u, i);
+    L->pbv[i] = load_host(dtype, v, i);
+  }
+  L->dirty = true;
+  return MHSA_OK;
+}
+
+int32_t mhsa_load_weights(mhsa_layer* L, const mhsa_tensor* tensors, int32_t n, const char* prefix, int32_t strict,
+                          int32_t quant_bits, int32_t quant_group) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if ((n > 0 && !tensors) || !prefix) return fail(MHSA_EINVAL, "null tensor list or prefix");
+  auto find = [&](const std::string& key) -> const mhsa_tensor* {
+    for (int i = 0; i < n; ++i)
+      if (tensors[i].name && key == tensors[i].name) return &tensors[i];
+    return nullptr;
+  };
+  auto numel = [](const mhsa_tensor* t) {
+    int64_t e = 1;
+    for (int i = 0; i < t->ndim; ++i) e *= t->shape[i];
+    return e;
+  };
+  const int D = L->D;
+  const char* names[5] = {"linear_q", "linear_k", "linear_v", "linear_out", "linear_pos"};
+  const int bits = quant_bits > 0 ? quant_bits : 8, group = quant_group > 0 ? quant_group : 64;
+  for (int i = 0; i < 5; ++i) {
+    const std::string p = std::string(prefix) + "." + names[i];
+    const mhsa_tensor* w = find(p + ".weight");
+    const mhsa_tensor* sc = find(p + ".scales");
+    const mhsa_tensor* qb = find(p + ".biases");
+    const mhsa_tensor* b = find(p + ".bias");
+    if (w && sc && qb) {  // quantization.rs:299-304
+      if (w->dtype != MHSA_U32 || sc->dtype != MHSA_F16 || qb->dtype != MHSA_F16)
+        return fail(MHSA_EINVAL, "`%s`: quantized tensors must be u32 weight and f16 scales/biases", p.c_str());
+      if (numel(w) != (int64_t)D * D * bits / 32 || numel(sc) != (int64_t)D * D / group || numel(qb) != numel(sc))
+        return fail(MHSA_EINVAL, "`%s`: quantized shapes do not match d_model %d", p.c_str(), D);
+      if (b && (b->dtype != MHSA_F16 || numel(b) != D))
+        return fail(MHSA_EINVAL, "`%s.bias`: expected f16 [%d]", p.c_str(), D);
+      int32_t rc = mhsa_load_linear_quantized(L, i, static_cast<const uint32_t*>(w->data),
+                                              static_cast<const uint16_t*>(sc->data),
+                                              static_cast<const uint16_t*>(qb->data),
+                                              b ? static_cast<const uint16_t*>(b->data) : nullptr, bits, group);
+      if (rc) return rc;
+    } else if (w) {
+      // [O, I] or a pointwise-conv [O, 1, I] (quantization.rs:330-335)
+      const bool shape_ok = (w->ndim == 2 && w->shape[0] == D && w->shape[1] == D) ||
+                            (w->ndim == 3 && w->shape[0] == D && w->shape[1] == 1 && w->shape[2] == D);
+      if (!shape_ok || !float_dtype(w->dtype))
+        return fail(MHSA_EINVAL, "`%s.weight`: expected float [%d, %d]", p.c_str(), D, D);
+      if (b && (!float_dtype(b->dtype) || numel(b) != D))
+        return fail(MHSA_EINVAL, "`%s.bias`: expected float [%d]", p.c_str(), D);
+      if (b && b->dtype != w->dtype) {
+        std::vector<float> bb(D);
+        for (int k = 0; k < D; ++k) bb[k] = load_host(b->dtype, b->data, k);
+        int32_t rc = mhsa_load_linear_standard(L, i, w->dtype, w->data, nullptr);
+        if (rc) return rc;
+        L->lin[i].bias = bb;
+      } else {
+        int32_t rc = mhsa_load_linear_standard(L, i, w->dtype, w->data, b ? b->data : nullptr);
+        if (rc) return rc;
+      }
+    } else if (strict) {
+      return fail(MHSA_ENOENT, "missing weight `%s.weight`", p.c_str());  // loading.rs:107-116
+    }
+  }
+  const mhsa_tensor* tu = find(std::string(prefix) + ".pos_bias_u");
+  const mhsa_tensor* tv = find(std::string(prefix) + ".pos_bias_v");
+  for (const mhsa_tensor* t : {tu, tv}) {
+    if (t && (!float_dtype(t->dtype) || numel(t) != D))
+      return fail(MHSA_EINVAL, "`%s`: expected float [%d, %d]", t->name, L->H, L->dk);
+  }
+  if (strict && (!tu || !tv))
+    return fail(MHSA_ENOENT, "missing weight `%s.%s`", prefix, tu ? "pos_bias_v" : "pos_bias_u");
+  if (tu)
+    for (int k = 0; k < D; ++k) L->pbu[k] = load_host(tu->dtype, tu->data, k);
+  if (tv)
+    for (int k = 0; k < D; ++k) L->pbv[k] = load_host(tv->dtype, tv->data, k);
+  L->dirty = true;
+  return MHSA_OK;
+}
+
+int32_t mhsa_forward(mhsa_layer* L, const void* x, int32_t batch, int32_t seq_len, const void* pos_emb,
+                     int32_t pos_len, const mhsa_context* ctx, const int32_t* lens, void* out, void* hs) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (!out) return fail(MHSA_EINVAL, "null output pointer");
+  return forward_impl(L, x, batch, seq_len, pos_emb, pos_len, ctx, lens, out, nullptr, nullptr,
+                      static_cast<hipStream_t>(hs));
+}
+
+int32_t mhsa_sublayer_forward(mhsa_layer* L, void* x, int32_t batch, int32_t seq_len, const float* gamma,
+                              const float* beta, float eps, const void* pos_emb, int32_t pos_len,
+                              const mhsa_context* ctx, const int32_t* lens, void* hs) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (!x || batch <= 0 || seq_len <= 0) return fail(MHSA_EINVAL, "bad sublayer arguments");
+  if (!aligned16(x)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  const int D = L->D;
+  const int64_t M = (int64_t)batch * seq_len;
+  // LayerNorm affine parameters, uploaded when they change (rounded like the
+  // reference's cast of the norm to the layer dtype)
+  const float* gd = nullptr;
+  const float* bd = nullptr;
+  if (gamma || beta) {
+    std::vector<float> tmp(2 * D);
+    const bool bf = L->dt == mhsa::kBF16;
+    for (int i = 0; i < D; ++i) {
+      const float gv = gamma ? gamma[i] : 1.f, bv = beta ? beta[i] : 0.f;
+      tmp[i] = bf ? round_bf16(gv) : gv;
+      tmp[D + i] = bf ? round_bf16(bv) : bv;
+    }
+    if (tmp != L->ln_host) {
+      HIPCHK(L->ln_dev.ensure(tmp.size() * 4));
+      HIPCHK(hipMemcpy(L->ln_dev.p, tmp.data(), tmp.size() * 4, hipMemcpyHostToDevice));
+      L->ln_host = tmp;
+    }
+    gd = static_cast<const float*>(L->ln_dev.p);
+    bd = gd + D;
+  }
+  HIPCHK(L->hbuf.ensure(align_up(M * D * esz(L), 256)));
+  {
+    ProfScope ps(L, "layer_norm", s);
+    HIPCHK(mhsa::layer_norm(dtype_of(L), x, L->hbuf.p, gd, bd, eps, (int)M, D, s));
+  }
+  return forward_impl(L, L->hbuf.p, batch, seq_len, pos_emb, pos_len, ctx, lens, x, x, nullptr, s);
+}
+
+int32_t mhsa_stream_create(mhsa_layer* L, int32_t batch, int32_t cache_size, int32_t chunk_len, mhsa_stream** out) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (!out) return fail(MHSA_EINVAL, "null output pointer");
+  *out = nullptr;
+  if (batch <= 0 || cache_size < 0 || chunk_len <= 0)
+    return fail(MHSA_EINVAL, "bad stream shape (batch %d, cache %d, chunk %d)", batch, cache_size, chunk_len);
+  mhsa_stream* S = new (std::nothrow) mhsa_stream();
+  if (!S) return fail(MHSA_ENOMEM, "out of host memory");
+  S->layer = L;
+  S->B = batch;
+  S->C = cache_size;
+  S->Tc = chunk_len;
+  S->R = cache_size + chunk_len;
+  S->fill.assign(batch, 0);
+  const int D = L->D;
+  const size_t hb = (size_t)batch * S->R * D * 4, kvb = 2 * hb;
+  hipError_t e = S->ring_h.ensure(hb);
+  if (e == hipSuccess) e = S->ring_kv.ensure(kvb);
+  if (e == hipSuccess) e = hipMemset(S->ring_h.p, 0, hb);
+  if (e == hipSuccess) e = hipMemset(S->ring_kv.p, 0, kvb);
+  if (e != hipSuccess) {
+    delete S;
+    return fail(MHSA_EHIP, "stream allocation: %s", hipGetErrorString(e));
+  }
+  *out = S;
+  return MHSA_OK;
+}
+
+void mhsa_stream_destroy(mhsa_stream* S) { delete S; }
+
+int32_t mhsa_stream_fill(const mhsa_stream* S, int32_t* out) {
+  if (!S || !out) return fail(MHSA_EINVAL, "null argument");
+  std::copy(S->fill.begin(), S->fill.end(), out);
+  return MHSA_OK;
+}
+
+int32_t mhsa_stream_load_cache(mhsa_stream* S, const void* cache, const int32_t* filled, void* hs) {
+  if (!S || !cache) return fail(MHSA_EINVAL, "null argument");
+  mhsa_layer* L = S->layer;
+  if (L->dt != mhsa::kF32) return fail(MHSA_ENOTSUP, "streaming supports fp32 layers only");
+  if (!aligned16(cache)) return fail(MHSA_EINVAL, "cache must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  int32_t rc = prepare(L);
+  if (rc) return rc;
+  const int D = L->D;
+  S->head = 0;
+  for (int b = 0; b < S->B; ++b) S->fill[b] = filled ? std::min(std::max(filled[b], 0), S->C) : 0;
+  if (S->C == 0) return MHSA_OK;
+  HIPCHK(mhsa::ring_write(mhsa::kF32, cache, S->ring_h.p, S->B, S->C, D, S->R, D, 0, s));
+  const int M = S->B * S->C;
+  char* kv = static_cast<char*>(S->ring_kv.p);
+  if (L->qkv_fused)
+    return run_gemm(L, L->dev[1], 2 * D, cache, D, M, kv, 2 * D, nullptr, 0, s, S->C, S->R, 0, S->R);
+  if ((rc = run_gemm(L, L->dev[1], D, cache, D, M, kv, 2 * D, nullptr, 0, s, S->C, S->R, 0, S->R))) return rc;
+  return run_gemm(L, L->dev[2], D, cache, D, M, kv + (size_t)D * 4, 2 * D, nullptr, 0, s, S->C, S->R, 0, S->R);
+}
+
+int32_t mhsa_stream_read_cache(const mhsa_stream* S, void* out, void* hs) {
+  if (!S || !out) return fail(MHSA_EINVAL, "null argument");
+  if (!aligned16(out)) return fail(MHSA_EINVAL, "cache_out must be 16-byte aligned");
+  HIPCHK(mhsa::ring_read(mhsa::kF32, S->ring_h.p, out, S->B, S->C, S->layer->D, S->R, S->layer->D, S->head,
+                         static_cast<hipStream_t>(hs)));
+  return MHSA_OK;
+}
+
+int32_t mhsa_forward_with_cache(mhsa_layer* L, mhsa_stream* S, const void* x, const void* pos_emb, int32_t pos_len,
+                                const mhsa_stream_mask* mask, void* out, void* hs) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (!S || S->layer != L) return fail(MHSA_EINVAL, "stream does not belong to this layer");
+  if (!x || !pos_emb || !out) return fail(MHSA_EINVAL, "null tensor pointer");
+  if (!aligned16(x) || !aligned16(pos_emb) || !aligned16(out))
+    return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  if (L->dt != mhsa::kF32) return fail(MHSA_ENOTSUP, "streaming supports fp32 layers only");
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  int32_t rc = prepare(L);
+  if (rc) return rc;
+  const int D = L->D, B = S->B, C = S->C, T = S->Tc, R = S->R, Lk = C + T;
+  const bool masked = mask && mask->present;
+  const mhsa_context* ctx = masked ? &mask->ctx : nullptr;
+  const DistRange dr = context_distances(ctx, C, T, Lk);
+  int row0, nrows, center;
+  if ((rc = plan_positions(pos_len, Lk, dr, row0, nrows, center))) return rc;
+
+  // memoised position projection, keyed by pos_len (attention.rs:749-761)
+  if (L->pmemo_len != pos_len) {
+    HIPCHK(L->pmemo.ensure(align_up((int64_t)pos_len * D * 4, 256)));
+    ProfScope ps(L, "gemm_pos", s);
+    if ((rc = run_gemm(L, L->dev[4], D, pos_emb, D, pos_len, L->pmemo.p, D, nullptr, 0, s))) return rc;
+    L->pmemo_len = pos_len;
+  }
+  const int64_t M = (int64_t)B * T;
+  const size_t qb = align_up(M * D * 4, 256);
+  HIPCHK(S->ws.ensure(2 * qb));
+  char* q = static_cast<char*>(S->ws.p);
+  char* cx = q + qb;
+  char* kv = static_cast<char*>(S->ring_kv.p);
+  const int slot = (S->head + C) % R;  // ring rows of this chunk
+
+  {
+    ProfScope ps(L, "gemm_q", s);
+    if ((rc = run_gemm(L, L->dev[0], D, x, D, (int)M, q, D, nullptr, 0, s))) return rc;
+  }
+  ProfScope ps_kv(L, "gemm_kv", s);
+  if (L->qkv_fused) {
+    if ((rc = run_gemm(L, L->dev[1], 2 * D, x, D, (int)M, kv, 2 * D, nullptr, 0, s, T, R, slot, R))) return rc;
+  } else {
+    if ((rc = run_gemm(L, L->dev[1], D, x, D, (int)M, kv, 2 * D, nullptr, 0, s, T, R, slot, R))) return rc;
+    if ((rc = run_gemm(L, L->dev[2], D, x, D, (int)M, kv + (size_t)D * 4, 2 * D, nullptr, 0, s, T, R, slot, R)))
+      return rc;
+  }
+  ps_kv.next("ring_write");
+  HIPCHK(mhsa::ring_write(mhsa::kF32, x, S->ring_h.p, B, T, D, R, D, slot, s));
+  ps_kv.next("attention");
+
+  std::vector<int32_t> used(B);
+  for (int b = 0; b < B; ++b)
+    used[b] = std::min(std::max(masked && mask->filled_host ? mask->filled_host[b] : S->fill[b], 0), C);
+  mhsa::AttnParams a;
+  fill_attn_common(L, a);
+  a.q = q;
+  a.q_bs = (int64_t)T * D;
+  a.q_rs = D;
+  a.k = kv;
+  a.v = kv + (size_t)D * 4;
+  a.kv_bs = (int64_t)R * 2 * D;
+  a.kv_rs = 2 * D;
+  a.ring_head = S->head;
+  a.ring_len = R;
+  a.p = static_cast<char*>(L->pmemo.p) + (size_t)row0 * D * 4;
+  a.p_rs = D;
+  a.p_rows = nrows;
+  a.center = center;
+  a.o = cx;
+  a.o_bs = (int64_t)T * D;
+  a.o_rs = D;
+  a.T = T;
+  a.L = Lk;
+  a.qoff = C;
+  set_ctx(a, ctx);
+  rc = run_attention(
+      L, a, B,
+      [&](int b, int& lo, int& hi, int& qv) {
+        lo = masked ? C - used[b] : 0;  // unfilled cache rows (conformer.rs:155-181)
+        hi = Lk;
+        qv = masked && mask->valid_host ? std::min(std::max(mask->valid_host[b], 0), T) : T;
+      },
+      s);
+  if (rc) return rc;
+  ps_kv.next("gemm_out");
+  if ((rc = run_gemm(L, L->dev[3], D, cx, D, (int)M, out, D, nullptr, 0, s))) return rc;
+  const int keep = std::max(T - L->cache_drop, 0);  // attention.rs:665
+  S->head = (S->head + keep) % R;
+  for (int b = 0; b < B; ++b) S->fill[b] = std::min(used[b] + keep, C);  // conformer.rs:1025-1036
+  return MHSA_OK;
+}
+
+int32_t mhsa_pos_encoding(int32_t d_model, int32_t max_len, int32_t seq_len, float* out) {
+  if (!out) return fail(MHSA_EINVAL, "null output pointer");
+  if (seq_len <= 0) return fail(MHSA_EINVAL, "positional encoding requested for an empty sequence");
+  if (d_model <= 0 || d_model % 2 || max_len <= 0) return fail(MHSA_EINVAL, "bad d_model / max_len");
+  // Rows of a table of any max_len >= seq_len agree for the same distance,
+  // so the slice (attention.rs:158-174) and the regenerated table
+  // (attention.rs:137-145) are both the distances seq_len-1 .. -(seq_len-1).
+  const float step = std::log(10000.0f) / (float)d_model;
+  std::vector<float> div(d_model / 2);
+  for (int k = 0; k < d_model / 2; ++k) div[k] = std::exp(-(float)(2 * k) * step);
+  for (int r = 0; r < 2 * seq_len - 1; ++r) {
+    const float pos = (float)(seq_len - 1 - r);
+    for (int k = 0; k < d_model / 2; ++k) {
+      const float ang = pos * div[k];
+      out[(size_t)r * d_model + 2 * k] = (float)std::sin((double)ang);
+      out[(size_t)r * d_model + 2 * k + 1] = (float)std::cos((double)ang);
+    }
+  }
+  return MHSA_OK;
+}
+
+int32_t mhsa_profile_enable(mhsa_layer* L, int32_t enable) {
+  if (int32_t rc = check_layer(L)) return rc;
+  L->prof.flush();
+  L->prof.on = enable != 0;
+  return MHSA_OK;
+}
+
+int32_t mhsa_profile_reset(mhsa_layer* L) {
+  if (int32_t rc = check_layer(L)) return rc;
+  L->prof.flush();
+  L->prof.names.clear();
+  L->prof.ms.clear();
+  L->prof.count.clear();
+  return MHSA_OK;
+}
+
+int32_t mhsa_profile_count(mhsa_layer* L) {
+  if (!L) return -1;
+  L->prof.flush();
+  return (int32_t)L->prof.names.size();
+}
+
+int32_t mhsa_profile_entry(mhsa_layer* L, int32_t idx, const char** name, double* total_ms, int32_t* launches) {
+  if (int32_t rc = check_layer(L)) return rc;
+  L->prof.flush();
+  if (idx < 0 || idx >= (int32_t)L->prof.names.size()) return fail(MHSA_EINVAL, "profile entry %d out of range", idx);
+  if (name) *name = L->prof.names[idx].c_str();
+  if (total_ms) *total_ms = L->prof.ms[idx];
+  if (launches) *launches = L->prof.count[idx];
+  return MHSA_OK;
+}
+
+int32_t mhsa_debug_dequantize(mhsa_layer* L, int32_t which, float* out, void* hs) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (which < 0 || which > 4 || !out) return fail(MHSA_EINVAL, "bad arguments");
+  if (!L->lin[which].quantized) return fail(MHSA_EINVAL, "projection %d is not quantized", which);
+  int32_t rc = prepare(L);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  HIPCHK(mhsa::dequant_export(dtype_of(L), static_cast<const uint32_t*>(L->dev[which].w), L->dev[which].sb, out, L->D,
+                              L->D, s));
+  HIPCHK(hipStreamSynchronize(s));
+  return MHSA_OK;
+}
+
+int32_t mhsa_debug_linear(mhsa_layer* L, int32_t which, const void* x, int32_t rows, void* out, void* hs) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (which < 0 || which > 4 || !x || !out || rows < 0) return fail(MHSA_EINVAL, "bad arguments");
+  if (!aligned16(x) || !aligned16(out)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  int32_t rc = prepare(L);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  if ((rc = run_gemm(L, L->dev[which], L->D, x, L->D, rows, out, L->D, nullptr, 0, s))) return rc;
+  HIPCHK(hipStreamSynchronize(s));
+  return MHSA_OK;
+}
+
+int32_t mhsa_debug_offline_mask(int32_t B, int32_t T, const mhsa_context* ctx, const int32_t* lens, uint8_t* out,
+                                void* hs) {
+  if (B <= 0 || T <= 0 || !out) return fail(MHSA_EINVAL, "bad arguments");
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  mhsa::AttnParams a;
+  a.T = a.L = T;
+  set_ctx(a, ctx);
+  for (int b0 = 0; b0 < B; b0 += mhsa::kMaxBatch) {
+    const int nb = std::min(mhsa::kMaxBatch, B - b0);
+    for (int i = 0; i < nb; ++i) {
+      a.key_lo[i] = 0;
+      a.key_hi[i] = lens ? std::min(std::max(lens[b0 + i], 1), T) : T;
+      a.q_valid[i] = T;
+    }
+    HIPCHK(mhsa::export_mask(a, nb, out + (size_t)b0 * T * T, s));
+  }
+  HIPCHK(hipStreamSynchronize(s));
+  return MHSA_OK;
+}
+
+int32_t mhsa_debug_stream_mask(int32_t B, int32_t C, int32_t T, const mhsa_stream_mask* mask, uint8_t* out,
+                               void* hs) {
+  if (B <= 0 || C < 0 || T <= 0 || !out || !mask) return fail(MHSA_EINVAL, "bad arguments");
+  if (mask->present && !mask->filled_host) return fail(MHSA_EINVAL, "filled_host is required");
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  mhsa::AttnParams a;
+  a.T = T;
+  a.L = C + T;
+  a.qoff = C;
+  set_ctx(a, mask->present ? &mask->ctx : nullptr);
+  for (int b0 = 0; b0 < B; b0 += mhsa::kMaxBatch) {
+    const int nb = std::min(mhsa::kMaxBatch, B - b0);
+    for (int i = 0; i < nb; ++i) {
+      const int f = mask->present ? std::min(std::max(mask->filled_host[b0 + i], 0), C) : C;
+      a.key_lo[i] = mask->present ? C - f : 0;
+      a.key_hi[i] = C + T;
+      a.q_valid[i] = mask->present && mask->valid_host ? std::min(std::max(mask->valid_host[b0 + i], 0), T) : T;
+    }
+    HIPCHK(mhsa::export_mask(a, nb, out + (size_t)b0 * T * (C + T), s));
+  }
+  HIPCHK(hipStreamSynchronize(s));
+  return MHSA_OK;
+}
+
+int32_t mhsa_debug_rel_shift_index(int32_t rows, int32_t total_len, int32_t* out, void* hs) {
+  if (rows <= 0 || total_len < rows || !out) return fail(MHSA_EINVAL, "bad arguments");
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  // bd column = table row: centre total_len - 1, query i at frame total_len - rows + i
+  HIPCHK(mhsa::export_pos_index(rows, total_len, total_len - rows, total_len - 1, out, s));
+  HIPCHK(hipStreamSynchronize(s));
+  return MHSA_OK;
+}
+
+int32_t mhsa_debug_position_scores(mhsa_layer* L, const void* x, int32_t B, int32_t T, const void* pos_emb,
+                                   int32_t pos_len, float* out, void* hs) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (!out) return fail(MHSA_EINVAL, "null output pointer");
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  int32_t rc = forward_impl(L, x, B, T, pos_emb, pos_len, nullptr, nullptr, nullptr, nullptr, out, s);
+  if (rc) return rc;
+  HIPCHK(hipStreamSynchronize(s));
+  return MHSA_OK;
+}
+
+}  // extern "C"

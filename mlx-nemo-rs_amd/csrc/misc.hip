@@ -1,0 +1,141 @@
+// Small kernels around the attention path: the pre-LayerNorm of the MHSA
+// sublayer (conformer.rs:1749), the streaming cache ring copies
+// (attention.rs:650, 670-684; conformer.rs:983-1016) and the dequantised
+// weight export used by the bit-exact checks.
+#include "common.hpp"
+#include "kernels.hpp"
+#include "quant.hpp"
+
+namespace mhsa {
+namespace {
+
+// One wave per row; two-pass statistics in fp32 from registers.
+template <typename T, int VPL>
+__global__ __launch_bounds__(256) void ln_kernel(const T* x, T* y, const float* gamma, const float* beta,
+                                                 float eps, int rows, int D) {
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const T* xr = x + (int64_t)row * D;
+  float v[VPL];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = lane + 64 * i;
+    v[i] = c < D ? (float)xr[c] : 0.f;
+    s += v[i];
+  }
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  const float mean = s / (float)D;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = lane + 64 * i;
+    const float d = c < D ? v[i] - mean : 0.f;
+    q += d * d;
+  }
+  for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+  const float rstd = rsqrtf(q / (float)D + eps);
+  T* yr = y + (int64_t)row * D;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const int c = lane + 64 * i;
+    if (c < D) {
+      float t = (v[i] - mean) * rstd;
+      if (gamma) t *= gamma[c];
+      if (beta) t += beta[c];
+      yr[c] = from_float<T>(t);
+    }
+  }
+}
+
+template <typename T>
+hipError_t ln_launch(const void* x, void* y, const float* g, const float* b, float eps, int rows, int D,
+                     hipStream_t s) {
+  dim3 grid((rows + 3) / 4);
+  if (D <= 512)
+    hipLaunchKernelGGL((ln_kernel<T, 8>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
+  else
+    hipLaunchKernelGGL((ln_kernel<T, 16>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
+  return hipGetLastError();
+}
+
+// 16-byte chunks; `to_ring` selects the copy direction.
+__global__ void ring_copy_kernel(const char* src, char* dst, int B, int n, int row_bytes, int R, int64_t ld_bytes,
+                                 int off, bool to_ring) {
+  const int cpr = row_bytes / 16;
+  const int64_t total = (int64_t)B * n * cpr;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(e % cpr);
+    const int64_t bt = e / cpr;
+    const int t = (int)(bt % n), b = (int)(bt / n);
+    const int64_t lin = ((int64_t)b * n + t) * row_bytes + c * 16;
+    const int64_t ring = ((int64_t)b * R + (off + t) % R) * ld_bytes + c * 16;
+    if (to_ring)
+      *reinterpret_cast<uint4*>(dst + ring) = *reinterpret_cast<const uint4*>(src + lin);
+    else
+      *reinterpret_cast<uint4*>(dst + lin) = *reinterpret_cast<const uint4*>(src + ring);
+  }
+}
+
+template <typename T>
+__global__ void dequant_kernel(const uint32_t* w, const float* sb, float* out, int N, int K) {
+  const int chunks = K / 16;
+  const int64_t total = (int64_t)N * chunks;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+    const int n = (int)(e / chunks), k = (int)(e % chunks) * 16;
+    const uint4 q = *reinterpret_cast<const uint4*>(reinterpret_cast<const unsigned char*>(w) + (int64_t)n * K + k);
+    const float2 s = *reinterpret_cast<const float2*>(sb + 2 * ((int64_t)n * (K / 64) + k / 64));
+    T vals[16];
+    dequant16<T>(q, s.x, s.y, vals);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) out[(int64_t)n * K + k + i] = (float)vals[i];
+  }
+}
+
+unsigned grid_for(int64_t n) { return (unsigned)std::min<int64_t>(std::max<int64_t>((n + 255) / 256, 1), 8192); }
+
+}  // namespace
+
+hipError_t layer_norm(DType dt, const void* x, void* y, const float* gamma, const float* beta, float eps, int rows,
+                      int D, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (!x || !y || D <= 0 || D > 1024) return hipErrorInvalidValue;
+  return dt == kF32 ? ln_launch<float>(x, y, gamma, beta, eps, rows, D, s)
+                    : ln_launch<bf16>(x, y, gamma, beta, eps, rows, D, s);
+}
+
+static hipError_t ring_copy(DType dt, const void* src, void* dst, int B, int n, int D, int R, int64_t ld, int off,
+                            bool to_ring, hipStream_t s) {
+  if (B <= 0 || n <= 0) return hipSuccess;
+  const int es = dtype_size(dt);
+  if (!src || !dst || R <= 0 || off < 0 || (D * es) % 16 || (ld * es) % 16 || ld < D) return hipErrorInvalidValue;
+  if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) return hipErrorInvalidValue;
+  const int64_t total = (int64_t)B * n * (D * es / 16);
+  hipLaunchKernelGGL(ring_copy_kernel, dim3(grid_for(total)), dim3(256), 0, s, (const char*)src, (char*)dst, B, n,
+                     D * es, R, ld * es, off, to_ring);
+  return hipGetLastError();
+}
+
+hipError_t ring_write(DType dt, const void* src, void* ring, int B, int n, int D, int R, int64_t ld, int off,
+                      hipStream_t s) {
+  return ring_copy(dt, src, ring, B, n, D, R, ld, off, true, s);
+}
+
+hipError_t ring_read(DType dt, const void* ring, void* dst, int B, int n, int D, int R, int64_t ld, int off,
+                     hipStream_t s) {
+  return ring_copy(dt, ring, dst, B, n, D, R, ld, off, false, s);
+}
+
+hipError_t dequant_export(DType dt, const uint32_t* w, const float* sb, float* out, int N, int K, hipStream_t s) {
+  if (N <= 0 || K <= 0) return hipSuccess;
+  if (!w || !sb || !out || K % 64) return hipErrorInvalidValue;
+  const int64_t total = (int64_t)N * (K / 16);
+  if (dt == kF32)
+    hipLaunchKernelGGL(dequant_kernel<float>, dim3(grid_for(total)), dim3(256), 0, s, w, sb, out, N, K);
+  else
+    hipLaunchKernelGGL(dequant_kernel<bf16>, dim3(grid_for(total)), dim3(256), 0, s, w, sb, out, N, K);
+  return hipGetLastError();
+}
+
+}  // namespace mhsa

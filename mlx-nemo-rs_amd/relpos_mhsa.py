@@ -1,0 +1,529 @@
+"""Python mirror of the reference's rel-pos MHSA API over the HIP C ABI.
+
+The classes follow animaslabs/mlx-nemo-rs (crate mlx-voice 0.3.0) so tests and
+callers read like the reference:
+
+* `RelPositionMultiHeadAttention`  src/asr/modules/encoders/attention.rs:328-893
+* `RelPositionalEncoding`          attention.rs:19-194
+* `AttentionContext`, `key_padding_mask`  attention.rs:208-294
+* `LinearLayer`, `QuantizationConfig`     src/core/quantization.rs:17-162
+
+Device tensors are torch tensors on the GPU (torch supplies memory and the
+current HIP stream); all arithmetic runs in `libmhsa_hip.so`. There is no CPU
+fallback: constructing a layer without the built library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from typing import Dict, Optional, Sequence, Tuple
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmhsa_hip.so")
+
+MHSA_OK, MHSA_ENOENT, MHSA_ENOMEM, MHSA_EINVAL, MHSA_ENOTSUP, MHSA_EHIP = 0, 2, 12, 22, 95, 1000
+F32, BF16, F16, U32 = 0, 1, 2, 3
+LINEARS = ("linear_q", "linear_k", "linear_v", "linear_out", "linear_pos")
+
+# Every symbol include/relpos_mhsa.h declares.
+EXPORTS = (
+    "mhsa_last_error", "mhsa_version", "mhsa_create", "mhsa_destroy", "mhsa_set_dtype", "mhsa_get_dtype",
+    "mhsa_head_dim", "mhsa_n_heads", "mhsa_d_model", "mhsa_set_cache_drop_size", "mhsa_load_linear_standard",
+    "mhsa_load_linear_quantized", "mhsa_load_pos_bias", "mhsa_load_weights", "mhsa_forward",
+    "mhsa_sublayer_forward", "mhsa_stream_create", "mhsa_stream_destroy", "mhsa_stream_load_cache",
+    "mhsa_stream_read_cache", "mhsa_stream_fill", "mhsa_forward_with_cache", "mhsa_pos_encoding",
+    "mhsa_debug_dequantize", "mhsa_debug_linear", "mhsa_debug_offline_mask", "mhsa_debug_stream_mask", "mhsa_debug_rel_shift_index",
+    "mhsa_debug_position_scores", "mhsa_profile_enable", "mhsa_profile_reset", "mhsa_profile_count",
+    "mhsa_profile_entry",
+)
+
+
+class MhsaError(RuntimeError):
+    """A failing C-ABI call (the reference's `Error`, src/core/error.rs:7-12)."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[{code}] {msg}")
+        self.code = code
+
+
+class Context(ctypes.Structure):
+    _fields_ = [("left", ctypes.c_int32), ("right", ctypes.c_int32), ("chunked", ctypes.c_int32)]
+
+
+class StreamMask(ctypes.Structure):
+    _fields_ = [("present", ctypes.c_int32), ("ctx", Context),
+                ("filled_host", ctypes.POINTER(ctypes.c_int32)),
+                ("valid_host", ctypes.POINTER(ctypes.c_int32))]
+
+
+class Tensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("dtype", ctypes.c_int32), ("ndim", ctypes.c_int32),
+                ("shape", ctypes.c_int64 * 4), ("data", ctypes.c_void_p)]
+
+
+_LIB = None
+
+
+def library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Load the HIP library once; raises if it has not been built."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(path):
+        raise MhsaError(MHSA_ENOENT, f"{path} is missing: build it with mlx-nemo-rs_amd/build.py")
+    lib = ctypes.CDLL(path)
+    P, I, F, VP = ctypes.POINTER, ctypes.c_int32, ctypes.c_float, ctypes.c_void_p
+    PI = P(ctypes.c_int32)
+    sig = {
+        "mhsa_last_error": (ctypes.c_char_p, []),
+        "mhsa_version": (I, []),
+        "mhsa_create": (I, [I, I, I, P(VP)]),
+        "mhsa_destroy": (None, [VP]),
+        "mhsa_set_dtype": (I, [VP, I]),
+        "mhsa_get_dtype": (I, [VP]),
+        "mhsa_head_dim": (I, [VP]),
+        "mhsa_n_heads": (I, [VP]),
+        "mhsa_d_model": (I, [VP]),
+        "mhsa_set_cache_drop_size": (I, [VP, I]),
+        "mhsa_load_linear_standard": (I, [VP, I, I, VP, VP]),
+        "mhsa_load_linear_quantized": (I, [VP, I, VP, VP, VP, VP, I, I]),
+        "mhsa_load_pos_bias": (I, [VP, I, VP, VP]),
+        "mhsa_load_weights": (I, [VP, P(Tensor), I, ctypes.c_char_p, I, I, I]),
+        "mhsa_forward": (I, [VP, VP, I, I, VP, I, P(Context), PI, VP, VP]),
+        "mhsa_sublayer_forward": (I, [VP, VP, I, I, P(ctypes.c_float), P(ctypes.c_float), F, VP, I, P(Context), PI,
+                                      VP]),
+        "mhsa_stream_create": (I, [VP, I, I, I, P(VP)]),
+        "mhsa_stream_destroy": (None, [VP]),
+        "mhsa_stream_load_cache": (I, [VP, VP, PI, VP]),
+        "mhsa_stream_read_cache": (I, [VP, VP, VP]),
+        "mhsa_stream_fill": (I, [VP, PI]),
+        "mhsa_forward_with_cache": (I, [VP, VP, VP, VP, I, P(StreamMask), VP, VP]),
+        "mhsa_pos_encoding": (I, [I, I, I, P(ctypes.c_float)]),
+        "mhsa_debug_dequantize": (I, [VP, I, VP, VP]),
+        "mhsa_debug_linear": (I, [VP, I, VP, I, VP, VP]),
+        "mhsa_debug_offline_mask": (I, [I, I, P(Context), PI, VP, VP]),
+        "mhsa_debug_stream_mask": (I, [I, I, I, P(StreamMask), VP, VP]),
+        "mhsa_debug_rel_shift_index": (I, [I, I, VP, VP]),
+        "mhsa_debug_position_scores": (I, [VP, VP, I, I, VP, I, VP, VP]),
+        "mhsa_profile_enable": (I, [VP, I]),
+        "mhsa_profile_reset": (I, [VP]),
+        "mhsa_profile_count": (I, [VP]),
+        "mhsa_profile_entry": (I, [VP, I, P(ctypes.c_char_p), P(ctypes.c_double), PI]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _LIB = lib
+    return lib
+
+
+def _check(rc: int):
+    if rc != MHSA_OK:
+        raise MhsaError(rc, library().mhsa_last_error().decode())
+
+
+def _stream_ptr():
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _dptr(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _int_array(vals) -> Optional[ctypes.Array]:
+    if vals is None:
+        return None
+    return (ctypes.c_int32 * len(vals))(*[int(v) for v in vals])
+
+
+def _host_f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+def _torch_dtype(dtype):
+    import torch
+    return torch.float32 if dtype == F32 else torch.bfloat16
+
+
+def _dtype_code(dtype) -> int:
+    import torch
+    if dtype in (F32, "float32", "f32", torch.float32):
+        return F32
+    if dtype in (BF16, "bfloat16", "bf16", torch.bfloat16):
+        return BF16
+    raise MhsaError(MHSA_ENOTSUP, f"dtype {dtype!r} not supported (float32, bfloat16)")
+
+
+# ---------------------------------------------------------------------------
+# reference helper types
+# ---------------------------------------------------------------------------
+
+@dataclass(frozen=True)
+class QuantizationConfig:
+    """quantization.rs:17-32."""
+
+    bits: int = 8
+    group_size: int = 64
+
+
+@dataclass
+class LinearLayer:
+    """quantization.rs:36-59: standard (weight [out,in] + bias) or MLX affine
+    quantized (u32 weight, f16 scales/biases, optional f16 bias)."""
+
+    weight: np.ndarray
+    bias: Optional[np.ndarray] = None
+    scales: Optional[np.ndarray] = None
+    biases: Optional[np.ndarray] = None
+    bits: int = 8
+    group_size: int = 64
+
+    @staticmethod
+    def standard(weight, bias=None) -> "LinearLayer":
+        return LinearLayer(np.asarray(weight), None if bias is None else np.asarray(bias))
+
+    @staticmethod
+    def quantized(weight, scales, biases, bias=None, bits=8, group_size=64) -> "LinearLayer":
+        return LinearLayer(np.asarray(weight, dtype=np.uint32), None if bias is None else np.asarray(bias),
+                           np.asarray(scales, dtype=np.float16), np.asarray(biases, dtype=np.float16), bits,
+                           group_size)
+
+    def is_quantized(self) -> bool:
+        return self.scales is not None
+
+
+@dataclass(frozen=True)
+class AttentionContext:
+    """attention.rs:208-227; `new` returns None for full attention."""
+
+    left: int
+    right: int
+    chunked: bool
+
+    @staticmethod
+    def new(size: Tuple[int, int], style: str) -> Optional["AttentionContext"]:
+        left, right = size
+        if left >= 0 or right >= 0:
+            return AttentionContext(int(left), int(right), style == "chunked_limited")
+        return None
+
+    def c(self) -> Context:
+        return Context(self.left, self.right, 1 if self.chunked else 0)
+
+
+def key_padding_mask(lengths: Sequence[int], seq_len: int) -> Optional[Tuple[int, ...]]:
+    """attention.rs:280-294: None when no frame is padding, otherwise the
+    per-item valid lengths (clamped to >= 1) the kernel masks keys with."""
+    if all(int(v) >= seq_len for v in lengths):
+        return None
+    return tuple(max(int(v), 1) for v in lengths)
+
+
+class RelPositionalEncoding:
+    """attention.rs:19-194. `get_encoding` returns a host float32 tensor
+    [1, 2*seq_len-1, d_model]; move it to the device in the layer dtype."""
+
+    def __init__(self, d_model: int, max_len: int, xscaling: bool):
+        self._d_model = d_model
+        self.max_len = max_len
+        self._xscale = float(np.sqrt(np.float32(d_model))) if xscaling else 1.0
+
+    def get_encoding(self, seq_len: int):
+        import torch
+        out = np.empty((2 * seq_len - 1, self._d_model) if seq_len > 0 else (0,), dtype=np.float32)
+        _check(library().mhsa_pos_encoding(self._d_model, self.max_len, seq_len,
+                                           out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))))
+        return torch.from_numpy(out).reshape(1, 2 * seq_len - 1, self._d_model)
+
+    def xscale(self) -> float:
+        return self._xscale
+
+    def d_model(self) -> int:
+        return self._d_model
+
+
+@dataclass
+class StreamingMask:
+    """The parameters `create_attention_mask` takes (conformer.rs:97-221);
+    `filled`/`valid` are per session (the reference uses session 0's)."""
+
+    att_context_size: Optional[Tuple[int, int]]
+    style: str = "chunked_limited"
+    filled: Optional[Sequence[int]] = None
+    valid: Optional[Sequence[int]] = None
+
+    def c(self):
+        keep = []
+        if self.att_context_size is None:
+            return StreamMask(0, Context(-1, -1, 0), None, None), keep
+        left, right = self.att_context_size
+        f = _int_array(self.filled)
+        v = _int_array(self.valid)
+        keep += [f, v]
+        m = StreamMask(1, Context(int(left), int(right), 1 if self.style == "chunked_limited" else 0),
+                       ctypes.cast(f, ctypes.POINTER(ctypes.c_int32)) if f is not None else None,
+                       ctypes.cast(v, ctypes.POINTER(ctypes.c_int32)) if v is not None else None)
+        return m, keep
+
+
+# ---------------------------------------------------------------------------
+# the attention module
+# ---------------------------------------------------------------------------
+
+class RelPositionMultiHeadAttention:
+    """RelPositionMultiHeadAttention (attention.rs:328-893) backed by the HIP library."""
+
+    def __init__(self, d_model: int, n_heads: int, use_bias: bool):
+        lib = library()
+        h = ctypes.c_void_p()
+        _check(lib.mhsa_create(d_model, n_heads, 1 if use_bias else 0, ctypes.byref(h)))
+        self._h = h
+        self._lib = lib
+        self.d_model = d_model
+        self._cache_drop_size = 0
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            self._lib.mhsa_destroy(h)
+            self._h = None
+
+    # attention.rs:409-433
+    def set_dtype(self, dtype) -> None:
+        _check(self._lib.mhsa_set_dtype(self._h, _dtype_code(dtype)))
+
+    @property
+    def dtype(self):
+        return _torch_dtype(self._lib.mhsa_get_dtype(self._h))
+
+    def head_dim(self) -> int:
+        return self._lib.mhsa_head_dim(self._h)
+
+    def n_heads(self) -> int:
+        return self._lib.mhsa_n_heads(self._h)
+
+    @property
+    def cache_drop_size(self) -> int:
+        return self._cache_drop_size
+
+    @cache_drop_size.setter
+    def cache_drop_size(self, n: int) -> None:
+        _check(self._lib.mhsa_set_cache_drop_size(self._h, int(n)))
+        self._cache_drop_size = int(n)
+
+    # weights (attention.rs:863-893, quantization.rs:62-82)
+    def set_linear(self, name: str, layer: LinearLayer) -> None:
+        which = LINEARS.index(name)
+        if layer.is_quantized():
+            w = np.ascontiguousarray(layer.weight, dtype=np.uint32)
+            s = np.ascontiguousarray(layer.scales, dtype=np.float16)
+            b = np.ascontiguousarray(layer.biases, dtype=np.float16)
+            bias = None if layer.bias is None else np.ascontiguousarray(layer.bias, dtype=np.float16)
+            _check(self._lib.mhsa_load_linear_quantized(
+                self._h, which, w.ctypes.data, s.ctypes.data, b.ctypes.data,
+                None if bias is None else bias.ctypes.data, layer.bits, layer.group_size))
+        else:
+            w = _host_f32(layer.weight)
+            bias = None if layer.bias is None else _host_f32(layer.bias)
+            _check(self._lib.mhsa_load_linear_standard(self._h, which, F32, w.ctypes.data,
+                                                       None if bias is None else bias.ctypes.data))
+
+    def set_pos_bias(self, u, v) -> None:
+        u, v = _host_f32(u), _host_f32(v)
+        _check(self._lib.mhsa_load_pos_bias(self._h, F32, u.ctypes.data, v.ctypes.data))
+
+    def load_weights(self, weights: Dict[str, np.ndarray], prefix: str,
+                     quant: Optional[QuantizationConfig] = None, strict: bool = True) -> None:
+        arrays, tensors = [], []
+        for name, arr in weights.items():
+            a = np.ascontiguousarray(arr)
+            code = {np.dtype(np.float32): F32, np.dtype(np.float16): F16, np.dtype(np.uint32): U32}.get(a.dtype)
+            if code is None:
+                a = np.ascontiguousarray(a, dtype=np.float32)
+                code = F32
+            arrays.append(a)
+            shape = (ctypes.c_int64 * 4)(*(list(a.shape) + [0] * (4 - a.ndim)))
+            tensors.append(Tensor(name.encode(), code, a.ndim, shape, a.ctypes.data))
+        arr_t = (Tensor * max(len(tensors), 1))(*tensors)
+        bits, group = (quant.bits, quant.group_size) if quant else (0, 0)
+        _check(self._lib.mhsa_load_weights(self._h, arr_t, len(tensors), prefix.encode(), 1 if strict else 0,
+                                           bits, group))
+
+    # attention.rs:446-573
+    def forward(self, x, pos_emb, context: Optional[AttentionContext] = None,
+                key_mask: Optional[Sequence[int]] = None):
+        import torch
+        b, t, d = x.shape
+        pe = pos_emb.reshape(-1, d)
+        self._check_dev(x, pe)
+        out = torch.empty_like(x)
+        ctx = context.c() if context is not None else None
+        lens = _int_array(key_mask)
+        _check(self._lib.mhsa_forward(self._h, _dptr(x), b, t, _dptr(pe), pe.shape[0],
+                                      ctypes.byref(ctx) if ctx is not None else None, lens, _dptr(out),
+                                      _stream_ptr()))
+        return out
+
+    def sublayer_forward_(self, x, pos_emb, context=None, key_mask=None, gamma=None, beta=None, eps=1e-5):
+        """In place x <- x + forward(LayerNorm(x)) (conformer.rs:1747-1780)."""
+        b, t, d = x.shape
+        pe = pos_emb.reshape(-1, d)
+        self._check_dev(x, pe)
+        ctx = context.c() if context is not None else None
+        g = None if gamma is None else _host_f32(gamma)
+        bb = None if beta is None else _host_f32(beta)
+        fp = ctypes.POINTER(ctypes.c_float)
+        _check(self._lib.mhsa_sublayer_forward(
+            self._h, _dptr(x), b, t, None if g is None else g.ctypes.data_as(fp),
+            None if bb is None else bb.ctypes.data_as(fp), float(eps), _dptr(pe), pe.shape[0],
+            ctypes.byref(ctx) if ctx is not None else None, _int_array(key_mask), _stream_ptr()))
+        return x
+
+    # attention.rs:606-816, functional form: cache in, cache out
+    def forward_with_cache(self, x, pos_emb, cache, cache_filled_len=0, att_mask: Optional[StreamingMask] = None):
+        """Returns (output, new_cache) like the reference; the cache is [B, C, D].
+        `att_mask` describes the mask (None = no mask); its `filled` defaults
+        to `cache_filled_len` for every session."""
+        import torch
+        b, t, d = x.shape
+        c = cache.shape[1]
+        st = self.stream(b, c, t)
+        if att_mask is not None and att_mask.att_context_size is not None and att_mask.filled is None:
+            att_mask = StreamingMask(att_mask.att_context_size, att_mask.style, [cache_filled_len] * b,
+                                     att_mask.valid)
+        st.load_cache(cache, [cache_filled_len] * b)
+        out = st.step(x, pos_emb, att_mask)
+        return out, st.read_cache()
+
+    def stream(self, batch: int, cache_size: int, chunk_len: int) -> "StreamState":
+        return StreamState(self, batch, cache_size, chunk_len)
+
+    def debug_dequantize(self, name: str):
+        import torch
+        out = torch.empty((self.d_model, self.d_model), dtype=torch.float32, device="cuda")
+        _check(self._lib.mhsa_debug_dequantize(self._h, LINEARS.index(name), _dptr(out), _stream_ptr()))
+        return out
+
+    # per-kernel HIP-event timing (no counterpart in the reference)
+    def profile(self, enable: bool = True) -> None:
+        _check(self._lib.mhsa_profile_enable(self._h, 1 if enable else 0))
+
+    def profile_reset(self) -> None:
+        _check(self._lib.mhsa_profile_reset(self._h))
+
+    def profile_read(self) -> Dict[str, Tuple[float, int]]:
+        """{kernel tag: (total ms, launches)} accumulated since the last reset."""
+        out = {}
+        for i in range(self._lib.mhsa_profile_count(self._h)):
+            name, ms, n = ctypes.c_char_p(), ctypes.c_double(), ctypes.c_int32()
+            _check(self._lib.mhsa_profile_entry(self._h, i, ctypes.byref(name), ctypes.byref(ms), ctypes.byref(n)))
+            out[name.value.decode()] = (ms.value, n.value)
+        return out
+
+    def debug_linear(self, name: str, x):
+        """One projection alone through the forward pass's GEMM kernels."""
+        import torch
+        rows = x.numel() // self.d_model
+        self._check_dev(x)
+        out = torch.empty_like(x)
+        _check(self._lib.mhsa_debug_linear(self._h, LINEARS.index(name), _dptr(x), rows, _dptr(out),
+                                           _stream_ptr()))
+        return out
+
+    def debug_position_scores(self, x, pos_emb):
+        import torch
+        b, t, d = x.shape
+        pe = pos_emb.reshape(-1, d)
+        self._check_dev(x, pe)
+        out = torch.empty((b, self.n_heads(), t, t), dtype=torch.float32, device=x.device)
+        _check(self._lib.mhsa_debug_position_scores(self._h, _dptr(x), b, t, _dptr(pe), pe.shape[0], _dptr(out),
+                                                    _stream_ptr()))
+        return out
+
+    def _check_dev(self, *ts):
+        want = self.dtype
+        for t in ts:
+            if not t.is_cuda or t.dtype != want or not t.is_contiguous():
+                raise MhsaError(MHSA_EINVAL, f"expected a contiguous {want} GPU tensor, got {t.dtype} "
+                                             f"on {t.device}")
+
+
+class StreamState:
+    """Per-layer streaming state: the attention cache as an HBM ring
+    (EncoderCache::last_channel slice, streaming/core.rs:117-166)."""
+
+    def __init__(self, layer: RelPositionMultiHeadAttention, batch: int, cache_size: int, chunk_len: int):
+        self.layer = layer
+        self.batch, self.cache_size, self.chunk_len = batch, cache_size, chunk_len
+        h = ctypes.c_void_p()
+        _check(layer._lib.mhsa_stream_create(layer._h, batch, cache_size, chunk_len, ctypes.byref(h)))
+        self._h = h
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            self.layer._lib.mhsa_stream_destroy(h)
+            self._h = None
+
+    def load_cache(self, cache, filled: Optional[Sequence[int]] = None) -> None:
+        self.layer._check_dev(cache)
+        _check(self.layer._lib.mhsa_stream_load_cache(self._h, _dptr(cache), _int_array(filled), _stream_ptr()))
+
+    def read_cache(self):
+        import torch
+        out = torch.empty((self.batch, self.cache_size, self.layer.d_model), dtype=torch.float32, device="cuda")
+        _check(self.layer._lib.mhsa_stream_read_cache(self._h, _dptr(out), _stream_ptr()))
+        return out
+
+    def fill(self):
+        arr = (ctypes.c_int32 * self.batch)()
+        _check(self.layer._lib.mhsa_stream_fill(self._h, arr))
+        return list(arr)
+
+    def step(self, x, pos_emb, mask: Optional[StreamingMask] = None, out=None):
+        import torch
+        b, t, d = x.shape
+        pe = pos_emb.reshape(-1, d)
+        self.layer._check_dev(x, pe)
+        if out is None:
+            out = torch.empty_like(x)
+        m, keep = (mask.c() if mask is not None else (None, []))
+        _check(self.layer._lib.mhsa_forward_with_cache(self.layer._h, self._h, _dptr(x), _dptr(pe), pe.shape[0],
+                                                       ctypes.byref(m) if m is not None else None, _dptr(out),
+                                                       _stream_ptr()))
+        return out
+
+
+# ---------------------------------------------------------------------------
+# debug exports
+# ---------------------------------------------------------------------------
+
+def debug_offline_mask(batch: int, seq_len: int, context: Optional[AttentionContext],
+                       key_lengths: Optional[Sequence[int]]):
+    import torch
+    out = torch.empty((batch, seq_len, seq_len), dtype=torch.uint8, device="cuda")
+    ctx = context.c() if context is not None else None
+    _check(library().mhsa_debug_offline_mask(batch, seq_len, ctypes.byref(ctx) if ctx is not None else None,
+                                             _int_array(key_lengths), _dptr(out), _stream_ptr()))
+    return out
+
+
+def debug_stream_mask(batch: int, cache_size: int, chunk_len: int, mask: StreamingMask):
+    import torch
+    out = torch.empty((batch, chunk_len, cache_size + chunk_len), dtype=torch.uint8, device="cuda")
+    m, keep = mask.c()
+    _check(library().mhsa_debug_stream_mask(batch, cache_size, chunk_len, ctypes.byref(m), _dptr(out),
+                                            _stream_ptr()))
+    return out
+
+
+def debug_rel_shift_index(rows: int, total_len: int):
+    import torch
+    out = torch.empty((rows, total_len), dtype=torch.int32, device="cuda")
+    _check(library().mhsa_debug_rel_shift_index(rows, total_len, _dptr(out), _stream_ptr()))
+    return out

@@ -1,0 +1,164 @@
+"""Synthetic workloads for the rel-pos MHSA path (host-side numpy generators).
+
+Five configurations of the FastConformer attention sublayer:
+
+* ``large_f32``       D=512, H=8, B=1, T=125, fp32, no padding, full context
+                      (FastConformer-large, 10 s of audio), seed 0
+* ``xl_offline_bf16`` D=1024, H=8, B=8, T=375, bf16, key padding with valid
+                      lengths U{188..375}, seed 1
+* ``xl_stream_f32``   D=1024, H=8, 16 sessions, 14-frame chunks against a
+                      70-frame cache, [70, 13] chunked_limited context, fills
+                      U{0..70}, 50 steps, fp32, seed 2
+* ``xl_local_bf16``   D=1024, H=8, B=2, T=7500, bf16, regular (128, 128)
+                      window with a 257-row banded position table, seed 3
+* ``xl_stack_u8``     24 sublayers x <- x + MHSA(LN(x)) with affine u8
+                      projections (group 64, f16 scales U(0.002, 0.02), f16
+                      biases N(0, 0.01), codes U{0..255}), B=4, T=1500, bf16,
+                      valid lengths U{1000..1500}, seed 4
+
+Weights are Xavier-uniform U(+-sqrt(6 / 2D)), pos_bias_u/v ~ N(0, 0.02^2),
+inputs x ~ N(0, 1); every array comes from numpy's PCG64 with the stated
+seed, so the same bytes reach the GPU and the oracle.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Tuple
+
+import numpy as np
+
+
+@dataclass
+class Workload:
+    name: str
+    d_model: int
+    n_heads: int
+    batch: int
+    seq_len: int
+    dtype: str  # "float32" | "bfloat16"
+    seed: int
+    use_bias: bool = False
+    lengths: Optional[List[int]] = None
+    context: Optional[Tuple[int, int, str]] = None  # (left, right, style)
+    pos_band: Optional[int] = None  # rows of a centred banded table (2W+1)
+    quantized: bool = False
+    layers: int = 1
+    # streaming
+    cache_size: int = 0
+    steps: int = 0
+    fills: Optional[List[int]] = None
+
+    @property
+    def head_dim(self) -> int:
+        return self.d_model // self.n_heads
+
+
+def xavier(rng, d_out, d_in):
+    bound = np.sqrt(6.0 / (d_in + d_out))
+    return rng.uniform(-bound, bound, size=(d_out, d_in)).astype(np.float32)
+
+
+def pack_u8(codes: np.ndarray) -> np.ndarray:
+    """MLX 8-bit packing: four codes per u32 along the input dim, lowest byte first."""
+    c = codes.astype(np.uint32)
+    return (c[:, 0::4] | (c[:, 1::4] << 8) | (c[:, 2::4] << 16) | (c[:, 3::4] << 24)).astype(np.uint32)
+
+
+def make_layer_weights(rng, d_model: int, n_heads: int, use_bias: bool, quantized: bool,
+                       centred: bool = False) -> Dict[str, np.ndarray]:
+    """Weights of one layer keyed like a checkpoint (`{name}.weight`, ...)."""
+    d = d_model
+    w: Dict[str, np.ndarray] = {}
+    for name in ("linear_q", "linear_k", "linear_v", "linear_out", "linear_pos"):
+        if quantized:
+            codes = rng.integers(0, 256, size=(d, d))
+            scales = rng.uniform(0.002, 0.02, size=(d, d // 64)).astype(np.float16)
+            qb = rng.normal(0.0, 0.01, size=(d, d // 64))
+            if centred:
+                qb = qb - 128.0 * scales.astype(np.float64)
+            w[f"{name}.weight"] = pack_u8(codes)
+            w[f"{name}.scales"] = scales
+            w[f"{name}.biases"] = qb.astype(np.float16)
+        else:
+            w[f"{name}.weight"] = xavier(rng, d, d)
+        if use_bias and name != "linear_pos":
+            w[f"{name}.bias"] = np.zeros(d, dtype=np.float16 if quantized else np.float32)
+    dk = d // n_heads
+    w["pos_bias_u"] = rng.normal(0.0, 0.02, size=(n_heads, dk)).astype(np.float32)
+    w["pos_bias_v"] = rng.normal(0.0, 0.02, size=(n_heads, dk)).astype(np.float32)
+    return w
+
+
+def prefixed(weights: Dict[str, np.ndarray], prefix: str) -> Dict[str, np.ndarray]:
+    return {f"{prefix}.{k}": v for k, v in weights.items()}
+
+
+CONFIGS: Dict[str, Workload] = {
+    "large_f32": Workload("large_f32", 512, 8, 1, 125, "float32", seed=0, use_bias=True),
+    "xl_offline_bf16": Workload("xl_offline_bf16", 1024, 8, 8, 375, "bfloat16", seed=1),
+    "xl_stream_f32": Workload("xl_stream_f32", 1024, 8, 16, 14, "float32", seed=2,
+                              context=(70, 13, "chunked_limited"), cache_size=70, steps=50),
+    "xl_local_bf16": Workload("xl_local_bf16", 1024, 8, 2, 7500, "bfloat16", seed=3,
+                              context=(128, 128, "regular"), pos_band=257),
+    "xl_stack_u8": Workload("xl_stack_u8", 1024, 8, 4, 1500, "bfloat16", seed=4, quantized=True, layers=24),
+}
+
+
+def instantiate(cfg: Workload, centred: bool = False):
+    """Draw the workload's weights and inputs. Returns (layers, x, extras):
+    layers: list of per-layer weight dicts; x: float32 [B, T, D] (or the first
+    chunk for streaming); extras: lengths / fills / per-step chunks."""
+    rng = np.random.default_rng(cfg.seed)
+    layers = [make_layer_weights(rng, cfg.d_model, cfg.n_heads, cfg.use_bias, cfg.quantized, centred)
+              for _ in range(cfg.layers)]
+    extras = {}
+    if cfg.cache_size:
+        extras["fills"] = [int(v) for v in rng.integers(0, cfg.cache_size + 1, size=cfg.batch)]
+        cache = rng.standard_normal((cfg.batch, cfg.cache_size, cfg.d_model)).astype(np.float32)
+        for b, f in enumerate(extras["fills"]):
+            cache[b, : cfg.cache_size - f] = 0.0  # unfilled rows are zeros, as EncoderCache::new
+        extras["cache"] = cache
+        extras["chunks"] = rng.standard_normal((cfg.steps, cfg.batch, cfg.seq_len, cfg.d_model)).astype(np.float32)
+        return layers, extras["chunks"][0], extras
+    if cfg.name == "xl_offline_bf16":
+        extras["lengths"] = [int(v) for v in rng.integers(188, 376, size=cfg.batch)]
+    elif cfg.name == "xl_stack_u8":
+        extras["lengths"] = [int(v) for v in rng.integers(1000, 1501, size=cfg.batch)]
+    x = rng.standard_normal((cfg.batch, cfg.seq_len, cfg.d_model)).astype(np.float32)
+    return layers, x, extras
+
+
+def algorithmic_flops(cfg: Workload, lengths=None, fills=None) -> float:
+    """Useful MFMA work of one pass: the projections plus 2*D FLOPs per
+    (query, visible key) pair for each of QK^T, the surviving part of QP^T
+    and PV. Padded queries count, padded keys and masked pairs do not."""
+    D, T, B = cfg.d_model, cfg.seq_len, cfg.batch
+    if cfg.cache_size:  # one streaming step with projected K/V cached
+        pairs = sum(T * (T + f) for f in (fills or [cfg.cache_size] * B))
+        return 2.0 * D * D * (3 * B * T) + 6.0 * D * pairs
+    lens = lengths or [T] * B
+    if cfg.context is not None and cfg.context[2] == "regular":
+        left, right = cfg.context[0], cfg.context[1]
+        pairs = 0
+        for ln in lens:
+            i = np.arange(T)
+            lo = np.maximum(i - left, 0)
+            hi = np.minimum(i + right, ln - 1)
+            pairs += int(np.maximum(hi - lo + 1, 0).sum())
+        pos_rows = cfg.pos_band or (2 * T - 1)
+    else:
+        pairs = sum(T * ln for ln in lens)
+        pos_rows = 2 * T - 1
+    return cfg.layers * (2.0 * D * D * (4 * B * T + pos_rows) + 6.0 * D * pairs)
+
+
+def algorithmic_bytes(cfg: Workload) -> float:
+    """One compulsory read of every input and weight and one write of every output."""
+    D, T, B = cfg.d_model, cfg.seq_len, cfg.batch
+    es = 2 if cfg.dtype == "bfloat16" else 4
+    if cfg.quantized:
+        w = 5 * (D * D + 2 * 2 * D * (D // 64))
+    else:
+        w = 5 * D * D * es
+    pos_rows = cfg.pos_band or (2 * T - 1)
+    return cfg.layers * (w + 2 * B * T * D * es + pos_rows * D * es)

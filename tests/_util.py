@@ -1,0 +1,55 @@
+"""Helpers shared by the test modules (not a test module itself)."""
+from __future__ import annotations
+
+import numpy as np
+
+import relpos_oracle as O
+
+LINEARS = ("linear_q", "linear_k", "linear_v", "linear_out", "linear_pos")
+
+
+def oracle_params(weights, d_model, n_heads, cache_drop_size=0) -> O.MhsaParams:
+    """Oracle view of a workload weight dict (keys `linear_q.weight`, ...)."""
+    lin = {}
+    for name in LINEARS:
+        if f"{name}.scales" in weights:
+            lin[name] = O.LinearLayer(weights[f"{name}.weight"], weights.get(f"{name}.bias"),
+                                      weights[f"{name}.scales"], weights[f"{name}.biases"])
+        else:
+            lin[name] = O.LinearLayer(np.asarray(weights[f"{name}.weight"], dtype=np.float64),
+                                      weights.get(f"{name}.bias"))
+    return O.MhsaParams(d_model, n_heads, lin["linear_q"], lin["linear_k"], lin["linear_v"], lin["linear_out"],
+                        lin["linear_pos"], np.asarray(weights["pos_bias_u"], dtype=np.float64),
+                        np.asarray(weights["pos_bias_v"], dtype=np.float64), cache_drop_size)
+
+
+def rel_err(got, ref, mask=None) -> float:
+    """max |got - ref| / max |ref| over the selected rows."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if mask is not None:
+        got, ref = got[mask], ref[mask]
+    return float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30))
+
+
+def abs_err(got, ref, mask=None) -> float:
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if mask is not None:
+        got, ref = got[mask], ref[mask]
+    return float(np.max(np.abs(got - ref)))
+
+
+def random_weights(rng, d_model, n_heads, use_bias=True, scale=None, quantized=False):
+    """Random layer weights (Xavier-like unless `scale`), keyed like a checkpoint."""
+    import workloads as W
+    w = W.make_layer_weights(rng, d_model, n_heads, use_bias, quantized)
+    if use_bias and not quantized:
+        for name in LINEARS[:4]:
+            w[f"{name}.bias"] = (rng.standard_normal(d_model) * 0.1).astype(np.float32)
+    if scale is not None and not quantized:
+        for name in LINEARS:
+            w[f"{name}.weight"] = (rng.standard_normal((d_model, d_model)) * scale).astype(np.float32)
+    w["pos_bias_u"] = (rng.standard_normal(w["pos_bias_u"].shape) * 0.3).astype(np.float32)
+    w["pos_bias_v"] = (rng.standard_normal(w["pos_bias_v"].shape) * 0.3).astype(np.float32)
+    return w

@@ -1,0 +1,489 @@
+"""Pins for the CPU oracle (`oracle/relpos_oracle.py`), run without a GPU.
+
+Every oracle function is checked against something that does not restate
+its own formula:
+
+* the reference's known-answer and invariant tests (`attention.rs:896-1358`,
+  `quantization.rs:413-430`), re-expressed on numpy inputs;
+* the mathematical definition of Transformer-XL relative attention, evaluated
+  with an explicit relative-position index per (query, key) pair instead of
+  the oracle's pad + reshape `rel_shift` and query blocking;
+* exact arithmetic (dequantisation in float64, bf16 rounding against torch's
+  own float32 -> bfloat16 conversion, LayerNorm against torch);
+* hand-derived known answers for the streaming mask and the cache slide.
+
+The reference has no numeric golden tensors for this path (its randomized
+tests draw from `mlx::random`, which is unavailable here), so only their
+invariants carry over.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import relpos_oracle as O
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+
+def random_params(d_model, n_heads, seed, use_bias=True, scale=0.3):
+    """Random weights in the style of `random_attention` (attention.rs:1000-1016)."""
+    rng = np.random.default_rng(seed)
+    d = d_model
+    w = lambda: rng.standard_normal((d, d)) * scale
+    b = lambda: rng.standard_normal(d) * scale
+    dk = d // n_heads
+    return O.MhsaParams(
+        d_model, n_heads,
+        O.LinearLayer(w(), b() if use_bias else None),
+        O.LinearLayer(w(), b() if use_bias else None),
+        O.LinearLayer(w(), b() if use_bias else None),
+        O.LinearLayer(w(), None),
+        O.LinearLayer(w(), None),
+        rng.standard_normal((n_heads, dk)) * scale,
+        rng.standard_normal((n_heads, dk)) * scale,
+    )
+
+
+def direct_attention(p, x_q, kv_in, pos_emb, cache_len, visible, scale=None, scale_bd=None):
+    """Rel-pos attention from its definition, one (query, key) pair at a time.
+
+    Query row i sits at absolute frame cache_len + i; key j at frame j. The
+    table row for relative distance r = (cache_len + i) - j is (L - 1) - r,
+    since the table lists distances L-1 down to -(L-1). `visible` is a bool
+    array [B, T, L]; a row with no visible key yields 0 (attention.rs:788).
+    """
+    h, dk = p.n_heads, p.head_dim
+    L = kv_in.shape[1]
+    q = p.linear_q.forward(x_q)
+    k = p.linear_k.forward(kv_in)
+    v = p.linear_v.forward(kv_in)
+    P = p.linear_pos.forward(pos_emb[0])
+    s = O.f32_scale(dk) if scale is None else scale
+    sb = s if scale_bd is None else scale_bd
+    B, T, _ = x_q.shape
+    ctx = np.zeros((B, T, h * dk))
+    for b in range(B):
+        for hh in range(h):
+            sl = slice(hh * dk, (hh + 1) * dk)
+            for i in range(T):
+                qu = q[b, i, sl] + p.pos_bias_u[hh]
+                qv = q[b, i, sl] + p.pos_bias_v[hh]
+                scores = np.full(L, -np.inf)
+                for j in range(L):
+                    if not visible[b, i, j]:
+                        continue
+                    row = (L - 1) - ((cache_len + i) - j)
+                    scores[j] = s * (qu @ k[b, j, sl]) + sb * (qv @ P[row, sl])
+                if np.isfinite(scores).any():
+                    e = np.exp(scores - scores.max())
+                    ctx[b, i, sl] = (e / e.sum()) @ v[b, :, sl]
+    return p.linear_out.forward(ctx)
+
+
+def nemo_visible(size, style, i, j):
+    """Brute-force port of NeMo `_create_masks` (attention.rs:1108-1119)."""
+    left, right = size
+    if style == "chunked_limited" and right >= 0:
+        chunk = right + 1
+        lc = left // chunk if left >= 0 else 10000
+        diff = i // chunk - j // chunk
+        return 0 <= diff <= lc
+    right_ok = style == "chunked_limited" or right < 0 or j - i <= right
+    return (left < 0 or j - i >= -left) and right_ok
+
+
+# ---------------------------------------------------------------------------
+# a1: positional encoding (attention.rs:902-915, 1150-1246, 1337-1357)
+# ---------------------------------------------------------------------------
+
+def test_rel_positional_encoding_creation():
+    pe = O.RelPositionalEncoding(512, 100, True)
+    assert abs(pe.xscale - math.sqrt(512.0)) < 1e-5
+
+
+def test_rel_positional_encoding_shape():
+    pe = O.RelPositionalEncoding(512, 100, False)
+    assert pe.get_encoding(50).shape == (1, 99, 512)
+
+
+def test_rel_positional_encoding_empty_is_error():
+    with pytest.raises(ValueError):
+        O.RelPositionalEncoding(16, 10, False).get_encoding(0)
+
+
+def test_rel_positional_encoding_values():
+    enc = O.RelPositionalEncoding(4, 3, False).get_encoding(3)
+    assert enc.shape == (1, 5, 4)
+    data = enc.reshape(-1)
+    d1 = math.exp(-2.0 * math.log(10000.0) / 4.0)
+    exp_row0 = [math.sin(2.0), math.cos(2.0), math.sin(2.0 * d1), math.cos(2.0 * d1)]
+    for c in range(4):
+        assert abs(data[c] - exp_row0[c]) < 1e-5
+    assert abs(data[8] - 0.0) < 1e-5 and abs(data[9] - 1.0) < 1e-5
+    # the last row is distance -2: sin is odd, cos even
+    assert abs(data[16] + math.sin(2.0)) < 1e-5 and abs(data[17] - math.cos(2.0)) < 1e-5
+
+
+def test_rel_positional_encoding_extends_past_max_len():
+    a = O.RelPositionalEncoding(16, 10, False).get_encoding(25)
+    b = O.RelPositionalEncoding(16, 40, False).get_encoding(25)
+    assert a.shape == (1, 49, 16)
+    assert np.max(np.abs(a - b)) < 1e-6
+
+
+def test_rel_positional_encoding_streaming_dimensions():
+    pe = O.RelPositionalEncoding(512, 5000, False)
+    assert pe.get_encoding(84).shape == (1, 167, 512)
+
+
+def test_positional_table_against_float64_sinusoid():
+    # every entry is sin/cos of distance * 10000^(-2k/d), to f32 accuracy
+    d, L = 64, 50
+    enc = O.RelPositionalEncoding(d, 60, False).get_encoding(L)[0].astype(np.float64)
+    dist = np.arange(L - 1, -L, -1, dtype=np.float64).reshape(-1, 1)
+    freq = 10000.0 ** (-np.arange(0, d, 2, dtype=np.float64) / d)
+    ang = dist * freq
+    assert np.max(np.abs(enc[:, 0::2] - np.sin(ang))) < 5e-5
+    assert np.max(np.abs(enc[:, 1::2] - np.cos(ang))) < 5e-5
+
+
+# ---------------------------------------------------------------------------
+# a7: rel_shift (attention.rs:917-998, 1248-1335)
+# ---------------------------------------------------------------------------
+
+def test_rel_shift_shape():
+    assert O.rel_shift(np.ones((1, 1, 4, 7))).shape == (1, 1, 4, 7)
+
+
+def test_rel_shift_correctness():
+    x = np.arange(15, dtype=np.float64).reshape(1, 1, 3, 5)
+    s = O.rel_shift(x).reshape(-1)
+    assert list(s[0:3]) == [2.0, 3.0, 4.0]
+    assert list(s[5:8]) == [6.0, 7.0, 8.0]
+    assert list(s[10:13]) == [10.0, 11.0, 12.0]
+
+
+def _verify_rel_shift(seq_len, pos_len, num_keys):
+    x = np.arange(seq_len * pos_len, dtype=np.float64).reshape(1, 1, seq_len, pos_len)
+    s = O.rel_shift(x).reshape(seq_len, pos_len)
+    for i in range(seq_len):
+        for j in range(num_keys):
+            assert s[i, j] == i * pos_len + (seq_len - 1 - i + j)
+
+
+def test_rel_shift_property_standard():
+    for seq_len in range(1, 9):
+        _verify_rel_shift(seq_len, 2 * seq_len - 1, seq_len)
+
+
+def test_rel_shift_property_streaming():
+    for seq_len in range(1, 7):
+        for cache_len in range(1, 7):
+            total = seq_len + cache_len
+            _verify_rel_shift(seq_len, 2 * total - 1, total)
+
+
+def test_rel_shift_no_padding_zeros_in_output():
+    seq_len, total = 4, 7
+    pos_len = 2 * total - 1
+    x = 100.0 + np.arange(seq_len * pos_len, dtype=np.float64).reshape(1, 1, seq_len, pos_len)
+    s = O.rel_shift(x).reshape(seq_len, pos_len)
+    assert (s[:, :total] >= 100.0).all()
+
+
+def test_rel_shift_index_map_closed_form():
+    for rows, total in [(1, 1), (5, 5), (14, 84), (13, 13), (7, 30)]:
+        pos_len = 2 * total - 1
+        idx = O.rel_shift_index(rows, total, pos_len)
+        i = np.arange(rows).reshape(-1, 1)
+        j = np.arange(total).reshape(1, -1)
+        assert (idx == i * pos_len + (rows - 1 - i + j)).all()
+
+
+# ---------------------------------------------------------------------------
+# a8, a9: masks and blocking (attention.rs:1106-1148, 196-206)
+# ---------------------------------------------------------------------------
+
+def test_attention_context_mask_matches_nemo():
+    seq_len = 23
+    cases = [((56, 3), "chunked_limited"), ((5, 1), "chunked_limited"),
+             ((-1, 2), "chunked_limited"), ((4, -1), "chunked_limited"),
+             ((3, 2), "regular"), ((-1, 0), "regular")]
+    for size, style in cases:
+        ctx = O.AttentionContext.new(size, style)
+        m = ctx.block_mask(7, 19, seq_len)
+        assert m.shape == (12, seq_len)
+        for i in range(7, 19):
+            for j in range(seq_len):
+                assert (m[i - 7, j] == 0.0) == nemo_visible(size, style, i, j), (size, style, i, j)
+    assert O.AttentionContext.new((-1, -1), "chunked_limited") is None
+
+
+def test_key_padding_mask():
+    assert O.key_padding_mask([13, 13], 13) is None
+    m = O.key_padding_mask([13, 9, 0], 13)
+    assert m.shape == (3, 1, 1, 13)
+    assert (m[0] == 0).all()
+    assert (m[1, 0, 0, :9] == 0).all() and np.isneginf(m[1, 0, 0, 9:]).all()
+    # length clamped to at least one key (attention.rs:285)
+    assert m[2, 0, 0, 0] == 0 and np.isneginf(m[2, 0, 0, 1:]).all()
+
+
+def test_query_block_size():
+    assert O.query_block_size(4, 13, 2 * 2 * 2 * 13 * 5) == 5
+    assert O.query_block_size(4, 13, 1 << 62) == 13
+    assert O.query_block_size(4, 13, 1) == 1
+    # configuration shapes quoted in the survey of the reference path
+    assert O.query_block_size(2 * 8, 7500, O.MAX_SCORE_ELEMENTS) == 279
+    assert O.query_block_size(4 * 8, 1500, O.MAX_SCORE_ELEMENTS) == 699
+
+
+# ---------------------------------------------------------------------------
+# a2, a3: linear layers and dequantisation
+# ---------------------------------------------------------------------------
+
+def test_standard_linear_forward():
+    # quantization.rs:413-430
+    layer = O.LinearLayer(np.array([[1.0, 2, 3], [4, 5, 6]]), np.array([0.1, 0.2]))
+    y = layer.forward(np.ones((1, 3)))
+    assert abs(y[0, 0] - 6.1) < 1e-5 and abs(y[0, 1] - 15.2) < 1e-5
+
+
+def test_unpack_codes_known_word():
+    w = np.array([[0x04030201, 0xFFEE0080]], dtype=np.uint32)
+    assert list(O.unpack_codes(w, 8)[0]) == [1, 2, 3, 4, 0x80, 0x00, 0xEE, 0xFF]
+
+
+def test_dequantize_known_values():
+    # one row, one group of 64: s = 0.5, b = 0.25 (both exact in f16 and bf16)
+    codes = np.arange(64, dtype=np.uint32)
+    w = (codes[0::4] | (codes[1::4] << 8) | (codes[2::4] << 16) | (codes[3::4] << 24)).reshape(1, 16)
+    s = np.array([[0.5]], dtype=np.float16)
+    b = np.array([[0.25]], dtype=np.float16)
+    for dt in (O.F32, O.BF16):
+        deq = O.dequantize(w, s, b, 8, 64, dt)
+        assert (deq[0] == 0.5 * np.arange(64) + 0.25).all()
+
+
+def test_dequantize_exact_in_float64():
+    # f32(s) * q is exact, so the f32 result equals float64 s*q + b rounded once
+    rng = np.random.default_rng(5)
+    n, k = 32, 256
+    w = rng.integers(0, 2 ** 32, size=(n, k // 4), dtype=np.uint64).astype(np.uint32)
+    s = rng.uniform(0.002, 0.02, size=(n, k // 64)).astype(np.float16)
+    b = (rng.standard_normal((n, k // 64)) * 0.01).astype(np.float16)
+    codes = np.stack([(w.astype(np.uint64) >> (8 * p)) & 255 for p in range(4)], -1).reshape(n, k)
+    exact = np.repeat(s.astype(np.float64), 64, 1) * codes + np.repeat(b.astype(np.float64), 64, 1)
+    got = O.dequantize(w, s, b, 8, 64, O.F32)
+    assert (got == exact.astype(np.float32).astype(np.float64)).all()
+    # bf16 mode: scales and biases cast to bf16 first, weight stored as bf16
+    sb = torch.from_numpy(s.astype(np.float32)).to(torch.bfloat16).double().numpy()
+    bb = torch.from_numpy(b.astype(np.float32)).to(torch.bfloat16).double().numpy()
+    exact_b = np.repeat(sb, 64, 1) * codes + np.repeat(bb, 64, 1)
+    ref_b = torch.from_numpy(exact_b.astype(np.float32)).to(torch.bfloat16).double().numpy()
+    assert (O.dequantize(w, s, b, 8, 64, O.BF16) == ref_b).all()
+
+
+def test_bf16_round_matches_torch():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(10000) * 10.0 ** rng.integers(-8, 8, 10000),
+                        [1 + 2 ** -8, 1 + 3 * 2 ** -8, -1 - 2 ** -8, 0.0, 65504.0]])
+    ref = torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16).double().numpy()
+    assert (O.bf16_round(x) == ref).all()
+    bits = torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert (O.bf16_bits(x) == bits).all()
+
+
+def test_layer_norm_matches_torch():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((3, 7, 64)) * 3 + 1
+    g, b = rng.standard_normal(64), rng.standard_normal(64)
+    ref = torch.nn.functional.layer_norm(torch.from_numpy(x), (64,), torch.from_numpy(g),
+                                         torch.from_numpy(b), 1e-5).numpy()
+    assert np.max(np.abs(O.layer_norm(x, g, b, 1e-5) - ref)) < 1e-12
+
+
+# ---------------------------------------------------------------------------
+# a10/a15 offline attention against the definition (attention.rs:446-573)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("ctx", [None, ((4, 1), "chunked_limited"), ((3, 2), "regular"),
+                                 ((-1, 2), "chunked_limited"), ((2, -1), "regular")])
+def test_offline_forward_matches_definition(ctx):
+    d, h, T = 16, 2, 13
+    p = random_params(d, h, seed=1)
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((2, T, d))
+    lengths = [T, 9]
+    pos = O.RelPositionalEncoding(d, 64, False).get_encoding(T)
+    context = O.AttentionContext.new(*ctx) if ctx else None
+    out = O.mhsa_forward(p, x, pos, context, O.key_padding_mask(lengths, T))
+    vis = np.ones((2, T, T), dtype=bool)
+    for b in range(2):
+        for i in range(T):
+            for j in range(T):
+                ok = j < lengths[b]
+                if context is not None:
+                    ok = ok and nemo_visible(ctx[0], ctx[1], i, j)
+                vis[b, i, j] = ok
+    ref = direct_attention(p, x, x, pos, 0, vis)
+    # compare rows that see at least one key (others are unspecified in the reference)
+    rows = vis.any(axis=2)
+    assert np.max(np.abs(out - ref)[rows]) < 1e-10
+
+
+def test_blocked_attention_matches_full():
+    d, h, T = 16, 2, 13
+    p = random_params(d, h, seed=2)
+    x = np.random.default_rng(11).standard_normal((2, T, d))
+    pos = O.RelPositionalEncoding(d, 64, False).get_encoding(T)
+    for ctx in [None, O.AttentionContext.new((4, 1), "chunked_limited"),
+                O.AttentionContext.new((3, 2), "regular")]:
+        full = O.mhsa_forward(p, x, pos, ctx, None, max_score_elements=1 << 62)
+        blocked = O.mhsa_forward(p, x, pos, ctx, None, max_score_elements=2 * 2 * 2 * 13 * 5)
+        assert np.max(np.abs(full - blocked)) < 1e-12
+        for dt in (O.BF16,):
+            fb = O.mhsa_forward(p, O.bf16_round(x), O.bf16_round(pos), ctx, None, dt, 1 << 62)
+            bb = O.mhsa_forward(p, O.bf16_round(x), O.bf16_round(pos), ctx, None, dt, 2 * 2 * 2 * 13 * 5)
+            assert np.max(np.abs(fb - bb)) == 0.0
+
+
+def test_padded_keys_are_ignored():
+    d, h, T, valid = 16, 2, 13, 9
+    p = random_params(d, h, seed=3)
+    x = np.random.default_rng(12).standard_normal((2, T, d))
+    x[1, valid:, :] = 50.0
+    pe = O.RelPositionalEncoding(d, 64, False)
+    km = O.key_padding_mask([T, valid], T)
+    assert km is not None and O.key_padding_mask([T, T], T) is None
+    for ctx in [None, O.AttentionContext.new((3, 2), "regular")]:
+        masked = O.mhsa_forward(p, x, pe.get_encoding(T), ctx, km)
+        full_row = O.mhsa_forward(p, x[:1], pe.get_encoding(T), ctx, None)
+        short_row = O.mhsa_forward(p, x[1:2, :valid], pe.get_encoding(valid), ctx, None)
+        assert np.max(np.abs(masked[:1] - full_row)) < 1e-10
+        assert np.max(np.abs(masked[1:2, :valid] - short_row)) < 1e-10
+
+
+def test_bf16_mode_rounds_only_at_op_boundaries():
+    # with bf16-exact inputs the bf16 oracle stays within bf16 noise of float64
+    d, h, T = 32, 2, 11
+    p = random_params(d, h, seed=4, scale=0.15)
+    x = O.bf16_round(np.random.default_rng(1).standard_normal((1, T, d)))
+    pos = O.bf16_round(O.RelPositionalEncoding(d, 64, False).get_encoding(T))
+    for lin in (p.linear_q, p.linear_k, p.linear_v, p.linear_out, p.linear_pos):
+        lin.weight = O.bf16_round(lin.weight)
+        if lin.bias is not None:
+            lin.bias = O.bf16_round(lin.bias)
+    p.pos_bias_u, p.pos_bias_v = O.bf16_round(p.pos_bias_u), O.bf16_round(p.pos_bias_v)
+    f = O.mhsa_forward(p, x, pos)
+    b = O.mhsa_forward(p, x, pos, dtype=O.BF16)
+    assert (O.bf16_round(b) == b).all()
+    assert 0 < np.max(np.abs(f - b)) < 0.05 * np.max(np.abs(f))
+
+
+# ---------------------------------------------------------------------------
+# a11-a14: streaming (attention.rs:606-816, conformer.rs:97-323, 883-1036)
+# ---------------------------------------------------------------------------
+
+def test_streaming_mask_c3_shape_only_offset():
+    # [70,13] chunked_limited, 14-frame chunks: query chunk (70+i)//14 = 5 and
+    # key chunks 0..5, 70/14 = 5 left chunks -> only the unfilled-cache offset hides keys
+    for f in (0, 1, 13, 56, 69, 70):
+        m = O.create_attention_mask((70, 13), "chunked_limited", 84, 70, f, 14, 14)
+        assert m.shape == (1, 14, 84)
+        expect = np.broadcast_to(np.arange(84) >= 70 - f, (14, 84))
+        assert (m[0] == expect).all()
+
+
+def test_streaming_mask_regular_known_answer():
+    # regular (2, 1), cache 3 (filled 2), chunk 3: query i at frame 3+i sees
+    # frames 3+i-2 .. 3+i+1, and frame 0 is unfilled
+    m = O.create_attention_mask((2, 1), "regular", 6, 3, 2, 3, 3)[0].astype(int)
+    expect = np.array([[0, 1, 1, 1, 1, 0],
+                       [0, 0, 1, 1, 1, 1],
+                       [0, 0, 0, 1, 1, 1]])
+    assert (m == expect).all()
+    # valid length 2: the last query row sees nothing
+    m2 = O.create_attention_mask((2, 1), "regular", 6, 3, 2, 3, 2)[0].astype(int)
+    assert (m2[:2] == expect[:2]).all() and (m2[2] == 0).all()
+
+
+def test_streaming_mask_chunked_known_answer():
+    # chunked_limited (2, 1): chunk 2, 1 left chunk; cache 4 (full), 2 queries at frames 4, 5
+    m = O.create_attention_mask((2, 1), "chunked_limited", 6, 4, 4, 2, 2)[0].astype(int)
+    expect = np.array([[0, 0, 1, 1, 1, 1],
+                       [0, 0, 1, 1, 1, 1]])
+    assert (m == expect).all()
+    # unlimited right context: only triu(-left) (conformer.rs:126-130)
+    m = O.create_attention_mask((1, -1), "chunked_limited", 5, 3, 3, 2, 2)[0].astype(int)
+    assert (m == np.array([[0, 0, 1, 1, 1], [0, 0, 0, 1, 1]])).all()
+
+
+def test_streaming_mask_kinds():
+    assert O.streaming_mask(None, "regular", 4, 0, 2, 2) is None
+    assert O.streaming_mask((70, 13), "chunked_limited", 70, 70, 14, 14) is None
+    add = O.streaming_mask((70, 13), "chunked_limited", 70, 10, 14, 14)
+    assert add.dtype == np.float64 and np.isneginf(add).any()
+    bm = O.streaming_mask((70, 13), "chunked_limited", 70, 10, 14, 12)
+    assert bm.dtype == np.bool_ and not bm[0, 13].any()
+
+
+def test_cache_update_known_answer():
+    cache = np.arange(1, 6, dtype=np.float64).reshape(1, 5, 1)  # rows 1..5
+    x = np.arange(10, 13, dtype=np.float64).reshape(1, 3, 1)  # rows 10..12
+    assert list(O.cache_update(cache, x, 0)[0, :, 0]) == [4, 5, 10, 11, 12]
+    assert list(O.cache_update(cache, x, 1)[0, :, 0]) == [3, 4, 5, 10, 11]
+    assert list(O.cache_update(cache, x, 3)[0, :, 0]) == [1, 2, 3, 4, 5]
+    small = np.arange(1, 3, dtype=np.float64).reshape(1, 2, 1)
+    # more kept frames than the cache holds: newest rows win (conformer.rs:994-997)
+    assert list(O.cache_update(small, x, 0)[0, :, 0]) == [11, 12]
+    assert O.next_fill(60, 14, 0, 70) == 70 and O.next_fill(0, 14, 0, 70) == 14
+    assert O.next_fill(5, 14, 20, 70) == 5
+
+
+@pytest.mark.parametrize("kind", ["none", "additive", "bool"])
+def test_streaming_forward_matches_definition(kind):
+    d, h, C, T = 16, 2, 6, 3
+    p = random_params(d, h, seed=7)
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((2, T, d))
+    filled, valid = (6, T) if kind == "none" else ((4, T) if kind == "additive" else (4, 2))
+    cache = rng.standard_normal((2, C, d))
+    cache[:, : C - filled, :] = 0.0
+    pos = O.RelPositionalEncoding(d, 64, False).get_encoding(C + T)
+    mask = O.streaming_mask((4, 1), "regular", C, filled, T, valid)
+    if kind == "none":
+        mask = O.streaming_mask(None, "regular", C, filled, T, valid)
+        assert mask is None
+    else:
+        assert (mask.dtype == np.bool_) == (kind == "bool")
+    out, nc = O.mhsa_forward_with_cache(p, x, pos, cache, mask)
+    vis = np.ones((2, T, C + T), dtype=bool)
+    if kind != "none":
+        for i in range(T):
+            for j in range(C + T):
+                fi = C + i
+                vis[:, i, j] = (j - fi >= -4) and (j - fi <= 1) and j >= C - filled and i < valid
+    # the unfused bool path divides by the f32 sqrt(d_k) (attention.rs:784)
+    scale = 1.0 / float(np.sqrt(np.float32(p.head_dim))) if kind == "bool" else None
+    ref = direct_attention(p, x, np.concatenate([cache, x], 1), pos, C, vis, scale=scale)
+    assert np.max(np.abs(out - ref)) < 1e-10
+    assert (nc == np.concatenate([cache[:, T:], x], 1)).all()
+
+
+def test_streaming_chunk_equals_offline_rows():
+    # A full cache holding the previous frames and no mask: the chunk's outputs
+    # equal the last T rows of offline attention over cache + chunk.
+    d, h, C, T = 16, 2, 5, 4
+    p = random_params(d, h, seed=9)
+    rng = np.random.default_rng(10)
+    seq = rng.standard_normal((1, C + T, d))
+    pos = O.RelPositionalEncoding(d, 64, False).get_encoding(C + T)
+    out, _ = O.mhsa_forward_with_cache(p, seq[:, C:], pos, seq[:, :C], None)
+    # offline over all C+T frames, keeping only the last T query rows
+    full = O.mhsa_forward(p, seq, pos)
+    assert np.max(np.abs(out - full[:, C:])) < 1e-10
