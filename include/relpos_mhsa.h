@@ -252,9 +252,13 @@ int32_t mhsa_debug_stream_mask(int32_t batch, int32_t cache_size, int32_t chunk_
 int32_t mhsa_debug_rel_shift_index(int32_t rows, int32_t total_len, int32_t* out_dev, void* hip_stream);
 /* Scaled position scores cast(s) * rel_shift(q_v P^T)[..., :seq_len]
  * [batch, n_heads, seq_len, seq_len] fp32 (device), computed by the fused
- * kernel's MFMA + LDS remap path, for a full-attention offline call. */
+ * kernel's MFMA + LDS remap path, for a full-attention offline call.
+ * q_out_dev [batch, seq_len, d_model] and p_out_dev [pos_len, d_model]
+ * (layer dtype, device, each may be NULL) receive the projected queries and
+ * position rows the kernel consumed. */
 int32_t mhsa_debug_position_scores(mhsa_layer* layer, const void* x, int32_t batch, int32_t seq_len,
-                                   const void* pos_emb, int32_t pos_len, float* out_dev, void* hip_stream);
+                                   const void* pos_emb, int32_t pos_len, float* out_dev, void* q_out_dev,
+                                   void* p_out_dev, void* hip_stream);
 
 #ifdef __cplusplus
 }

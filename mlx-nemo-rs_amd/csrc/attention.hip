@@ -28,21 +28,35 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-__device__ __forceinline__ bool ctx_visible(const AttnParams& p, int ia, int j) {
-  if (!p.has_ctx) return true;
-  if (p.chunked && p.right >= 0) {
-    const int chunk = p.right + 1;
-    const int lc = p.left >= 0 ? p.left / chunk : 10000;
-    const int d = ia / chunk - j / chunk;
-    return d >= 0 && d <= lc;
+// Every mask of the path hides keys outside one interval per query (i at
+// absolute frame ia = qoff + i): the padding / unfilled-cache range
+// [key_lo, key_hi) (attention.rs:280-294, conformer.rs:155-181); the regular
+// context j - ia in [-left, right] (attention.rs:256-269); the chunked_limited
+// context 0 <= ia/chunk - j/chunk <= left/chunk, i.e. whole chunks
+// [(ia/chunk - left/chunk) * chunk, (ia/chunk + 1) * chunk)
+// (attention.rs:241-255, conformer.rs:293-323). They intersect to [lo, hi),
+// empty for rows past q_valid (conformer.rs:197-215).
+__device__ __forceinline__ int2 query_interval(const AttnParams& p, int bl, int i) {
+  int lo = max(p.key_lo[bl], 0), hi = min(p.key_hi[bl], p.L);
+  if (i >= p.q_valid[bl] || i >= p.T) hi = lo;
+  if (p.has_ctx) {
+    const int ia = p.qoff + i;
+    if (p.chunked && p.right >= 0) {
+      const int chunk = p.right + 1;
+      const int lc = p.left >= 0 ? p.left / chunk : 10000;
+      const int qc = ia / chunk;
+      lo = max(lo, (qc - lc) * chunk);
+      hi = min(hi, (qc + 1) * chunk);
+    } else {
+      if (p.left >= 0) lo = max(lo, ia - p.left);
+      if (!p.chunked && p.right >= 0) hi = min(hi, ia + p.right + 1);
+    }
   }
-  bool vis = p.left < 0 || j - ia >= -p.left;
-  if (!p.chunked && p.right >= 0) vis = vis && j - ia <= p.right;
-  return vis;
+  return make_int2(lo, max(hi, lo));
 }
 
-__device__ __forceinline__ bool pair_visible(const AttnParams& p, int bl, int i, int j) {
-  return i < p.q_valid[bl] && j >= p.key_lo[bl] && j < p.key_hi[bl] && ctx_visible(p, p.qoff + i, j);
+__device__ __forceinline__ bool in_interval(int j, int2 iv) {
+  return (unsigned)(j - iv.x) < (unsigned)(iv.y - iv.x);
 }
 
 __device__ __forceinline__ int key_row(const AttnParams& p, int j) {
@@ -136,6 +150,7 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
 
   int jbeg, jend;
   key_range(p, bl, i0, min(i0 + QB, p.T), jbeg, jend);
+  const int2 iv = query_interval(p, bl, qi);
   const float sc_qk = p.scale * kLog2e, sc_bd = p.scale_bd * kLog2e;
   const char* kbase = reinterpret_cast<const char*>(p.k) + ((int64_t)b * p.kv_bs + h * DK) * sizeof(T);
   const char* vbase = reinterpret_cast<const char*>(p.v) + ((int64_t)b * p.kv_bs + h * DK) * sizeof(T);
@@ -150,7 +165,7 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
       const int j = j0 + row;
       const bool ok = j < p.L;
       const int64_t off = (int64_t)(ok ? key_row(p, j) : 0) * p.kv_rs * sizeof(T) + cb;
-      *reinterpret_cast<uint4*>(Ks + row * C::KP + cb) = load16<uint4>(kbase + off, ok);
+      *reinterpret_cast<u32x4*>(Ks + row * C::KP + cb) = load16<u32x4>(kbase + off, ok);
       const frag_t vv = load16<frag_t>(vbase + off, ok);
       const int d0 = cb / (int)sizeof(T);
 #pragma unroll
@@ -163,8 +178,8 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
       const int row = c / CPR, cb = (c % CPR) * 16;
       const int tp = pmin + row;
       const bool ok = tp >= 0 && tp < p.p_rows;
-      *reinterpret_cast<uint4*>(Ps + row * C::KP + cb) =
-          load16<uint4>(pbase + (int64_t)(ok ? tp : 0) * p.p_rs * sizeof(T) + cb, ok);
+      *reinterpret_cast<u32x4*>(Ps + row * C::KP + cb) =
+          load16<u32x4>(pbase + (int64_t)(ok ? tp : 0) * p.p_rs * sizeof(T) + cb, ok);
     }
     __syncthreads();
 
@@ -199,6 +214,7 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
 
     float sc[C::NU][4];
     float tmax = -INFINITY;
+    const bool full = __all(iv.x <= j0 && iv.y >= j0 + NK);  // no key of the tile hidden
 #pragma unroll
     for (int u = 0; u < C::NU; ++u) {
 #pragma unroll
@@ -209,29 +225,34 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
         if (DEBUG && qi < p.T && j < p.L)
           p.dbg_bd[(((int64_t)b * p.H + h) * p.T + qi) * p.L + j] = p.scale_bd * bdv;
         const float v = s[u][r] * sc_qk + bdv * sc_bd;
-        sc[u][r] = pair_visible(p, bl, qi, j) ? v : -INFINITY;
+        sc[u][r] = full || in_interval(j, iv) ? v : -INFINITY;
         tmax = fmaxf(tmax, sc[u][r]);
       }
     }
     __builtin_amdgcn_wave_barrier();
     tmax = col_max(tmax);
-    // Branch-free (the MFMAs below run wave-wide): a column with nothing
-    // visible yet keeps alpha = 0 and all-zero probabilities.
-    const float m_new = fmaxf(m_run, tmax);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    m_run = m_new;
+    // Lazy rescale (wave-uniform branch; the MFMAs are outside it): O and l
+    // move to a new maximum only when some column's maximum grew by more than
+    // 8 in log2 units, so probabilities stay <= 2^8 and O / l is unchanged.
+    // A column with nothing visible yet keeps zero O, l and probabilities.
+    if (__any(tmax > m_run + 8.f)) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < DK / 16; ++d) o[d] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
     float psum = 0.f;
 #pragma unroll
     for (int u = 0; u < C::NU; ++u)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        sc[u][r] = exp2f(sc[u][r] - m_use);
+        sc[u][r] = __builtin_amdgcn_exp2f(sc[u][r] - m_use);  // v_exp_f32; exp2(-inf) = 0
         psum += sc[u][r];
       }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int d = 0; d < DK / 16; ++d) o[d] *= alpha;
+    l_run += psum;
 
     // O^T += V^T Pr^T. The contraction slots of a fragment map to the keys
     // this lane already holds in S^T layout: keys 16u + 4g + r.
@@ -277,12 +298,299 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) vals[r] = from_float<T>(o[d][r] * inv);
       if constexpr (sizeof(T) == 2) {
-        *reinterpret_cast<uint2*>(orow + 16 * d + 4 * g) = *reinterpret_cast<const uint2*>(vals);
+        *reinterpret_cast<u32x2*>(orow + 16 * d + 4 * g) = *reinterpret_cast<const u32x2*>(vals);
       } else {
-        *reinterpret_cast<uint4*>(orow + 16 * d + 4 * g) = *reinterpret_cast<const uint4*>(vals);
+        *reinterpret_cast<u32x4*>(orow + 16 * d + 4 * g) = *reinterpret_cast<const u32x4*>(vals);
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// bf16 path with 32x32x16 MFMAs: 32 queries per wave, NW waves per
+// workgroup, 64-key tiles. K rows and a V^T tile (written transposed by the
+// projection GEMM) are staged in LDS and shared by the waves; the next tile
+// is fetched into registers while the current one is consumed. Each wave
+// reads its own position band straight from L2 into MFMA operands: 96 rows
+// (three 32-row band tiles) cover the pairs of its 32 queries and 64 keys,
+// and the last band tile of one key tile is the first of the next, so only
+// two are computed per step. bd is rounded to bf16 in the remap strip, as the
+// reference stores matrix_bd in bf16 (attention.rs:530).
+// ---------------------------------------------------------------------------
+template <int DK, int NW>
+struct Cfg2 {
+  static constexpr int NT = 64 * NW;
+  static constexpr int QB = 32 * NW;
+  static constexpr int NK = 64;
+  static constexpr int KP = DK * 2 + 16;      // K row pitch (bytes)
+  static constexpr int VP = NK * 2 + 16;      // V^T row pitch (bytes)
+  static constexpr int RMP = 96 + 8;          // remap row pitch (bf16 elements)
+  static constexpr int K_OFF = 0;
+  static constexpr int V_OFF = K_OFF + NK * KP;
+  static constexpr int R_OFF = V_OFF + DK * VP;
+  static constexpr int LDS = R_OFF + NW * 32 * RMP * 2;
+  static constexpr int NS = DK / 16;          // 16-wide d_k steps
+  static constexpr int KCH = NK * (DK * 2 / 16) / NT;  // K chunks per thread
+  static constexpr int VCH = DK * (NK * 2 / 16) / NT;  // V^T chunks per thread
+  // Hold the next tile in registers only when that costs <= 32 VGPRs.
+  static constexpr bool PREFETCH = KCH + VCH <= 8;
+};
+
+template <int DK, int NW, bool DEBUG>
+__global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p) {
+  using C = Cfg2<DK, NW>;
+  constexpr int NT = C::NT, QB = C::QB, NK = C::NK;
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS];
+  char* Ks = smem + C::K_OFF;
+  char* Vt = smem + C::V_OFF;
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5, c = lane & 31;
+  const int bl = blockIdx.z, b = p.b0 + bl, h = blockIdx.y;
+  const int i0 = blockIdx.x * QB;
+  const int iw = i0 + 32 * w;  // first query of this wave
+  const int qi = iw + c;       // this lane's query column
+  bf16* Rm = reinterpret_cast<bf16*>(smem + C::R_OFF) + (w * 32 + c) * C::RMP;
+
+  bf16x8 qu[C::NS], qv[C::NS];
+  {
+    const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + (int64_t)b * p.q_bs + (int64_t)qi * p.q_rs + h * DK;
+    const bool ok = qi < p.T;
+#pragma unroll
+    for (int s = 0; s < C::NS; ++s) {
+      const int d0 = 16 * s + 8 * hh;
+      const bf16x8 raw = load16<bf16x8>(qrow + d0, ok);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = (float)raw[e];
+        qu[s][e] = (bf16)(ok ? x + p.bias_u[h * DK + d0 + e] : 0.f);
+        qv[s][e] = (bf16)(ok ? x + p.bias_v[h * DK + d0 + e] : 0.f);
+      }
+    }
+  }
+
+  floatx16 o[DK / 32];
+#pragma unroll
+  for (int d = 0; d < DK / 32; ++d) o[d] = floatx16{};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  int jbeg, jend;
+  key_range(p, bl, i0, min(i0 + QB, p.T), jbeg, jend);
+  const int2 iv = query_interval(p, bl, qi);
+  const float sc_qk = p.scale * kLog2e, sc_bd = p.scale_bd * kLog2e;
+  const char* kbase = reinterpret_cast<const char*>(p.k) + ((int64_t)b * p.kv_bs + h * DK) * 2;
+  const char* vtbase = reinterpret_cast<const char*>(p.vt) + ((int64_t)h * DK * p.vt_ld + (int64_t)b * p.vt_bs) * 2;
+  const bf16* pbase = reinterpret_cast<const bf16*>(p.p) + h * DK;
+
+  constexpr int KR = C::PREFETCH ? C::KCH : 1, VR = C::PREFETCH ? C::VCH : 1;
+  u32x4 kr[KR], vr[VR];
+  // Without the register prefetch: copy one chunk at a time into LDS.
+  auto copy_direct = [&](int j0) {
+    for (int ch = tid; ch < NK * (DK * 2 / 16); ch += NT) {
+      const int row = ch / (DK * 2 / 16), cb = (ch % (DK * 2 / 16)) * 16;
+      const int j = j0 + row;
+      // rows past the last key are clamped (their scores are masked)
+      *reinterpret_cast<u32x4*>(Ks + row * C::KP + cb) =
+          *reinterpret_cast<const u32x4*>(kbase + (int64_t)min(j, p.L - 1) * p.kv_rs * 2 + cb);
+    }
+    for (int ch = tid; ch < DK * (NK * 2 / 16); ch += NT) {
+      const int d = ch / (NK * 2 / 16), cb = (ch % (NK * 2 / 16)) * 16;
+      *reinterpret_cast<u32x4*>(Vt + d * C::VP + cb) =
+          *reinterpret_cast<const u32x4*>(vtbase + (int64_t)d * p.vt_ld * 2 + (int64_t)j0 * 2 + cb);
+    }
+  };
+  auto fetch = [&](int j0) {
+#pragma unroll
+    for (int i = 0; i < C::KCH; ++i) {
+      const int ch = tid + NT * i;
+      const int row = ch / (DK * 2 / 16), cb = (ch % (DK * 2 / 16)) * 16;
+      const int j = j0 + row;
+      kr[i] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)min(j, p.L - 1) * p.kv_rs * 2 + cb);
+    }
+#pragma unroll
+    for (int i = 0; i < C::VCH; ++i) {
+      const int ch = tid + NT * i;
+      const int d = ch / (NK * 2 / 16), cb = (ch % (NK * 2 / 16)) * 16;
+      vr[i] = *reinterpret_cast<const u32x4*>(vtbase + (int64_t)d * p.vt_ld * 2 + (int64_t)j0 * 2 + cb);
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int i = 0; i < C::KCH; ++i) {
+      const int ch = tid + NT * i;
+      const int row = ch / (DK * 2 / 16), cb = (ch % (DK * 2 / 16)) * 16;
+      *reinterpret_cast<u32x4*>(Ks + row * C::KP + cb) = kr[i];
+    }
+#pragma unroll
+    for (int i = 0; i < C::VCH; ++i) {
+      const int ch = tid + NT * i;
+      const int d = ch / (NK * 2 / 16), cb = (ch % (NK * 2 / 16)) * 16;
+      *reinterpret_cast<u32x4*>(Vt + d * C::VP + cb) = vr[i];
+    }
+  };
+
+  const int jfirst = (jbeg / NK) * NK;
+  if (jfirst < jend) {
+    if constexpr (C::PREFETCH) {
+      fetch(jfirst);
+      stage();
+    } else {
+      copy_direct(jfirst);
+    }
+  }
+  __syncthreads();
+
+  floatx16 carry = floatx16{};
+  for (int j0 = jfirst; j0 < jend; j0 += NK) {
+    const bool more = j0 + NK < jend;
+    if (C::PREFETCH && more) fetch(j0 + NK);
+
+    // Position band of this wave: rows pb + n, n in [0, 96).
+    const int pb = p.center - p.qoff - (iw + 31) + j0;
+    floatx16 bd[3];
+    bd[0] = carry;
+    bd[1] = floatx16{};
+    bd[2] = floatx16{};
+    const bool first = j0 == jfirst;
+    if (first) bd[0] = floatx16{};
+    // Band rows outside the table are clamped into it: every pair reading
+    // such a row lies outside its query's interval (past the last key or
+    // query, or beyond a window the table was checked to cover), so it is
+    // masked, and the finite values it reads cannot reach the output.
+    const bf16* prow[3];
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+      prow[t] = pbase + (int64_t)min(max(pb + 32 * t + c, 0), p.p_rows - 1) * p.p_rs + 8 * hh;
+    floatx16 s[2] = {floatx16{}, floatx16{}};
+#pragma unroll
+    for (int st = 0; st < C::NS; ++st) {
+      const int cb = 32 * st + 16 * hh;  // byte offset of this lane's 8 d_k values
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(Ks + (32 * u + c) * C::KP + cb);
+        s[u] = mma32(a, qu[st], s[u]);
+      }
+#pragma unroll
+      for (int t = 0; t < 3; ++t) {
+        if (t == 0 && !first) continue;
+        const bf16x8 a = *reinterpret_cast<const bf16x8*>(prow[t] + 16 * st);
+        bd[t] = mma32(a, qv[st], bd[t]);
+      }
+    }
+    carry = bd[2];
+
+    // rel_shift: band row n of query column c holds key j0 + n - 31 + c.
+#pragma unroll
+    for (int t = 0; t < 3; ++t)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        bf16x4 v4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v4[e] = (bf16)bd[t][4 * m + e];
+        *reinterpret_cast<bf16x4*>(Rm + 32 * t + 8 * m + 4 * hh) = v4;
+      }
+    __builtin_amdgcn_wave_barrier();
+
+    float sc[2][16];
+    float tmax = -INFINITY;
+    const bool full = __all(iv.x <= j0 && iv.y >= j0 + NK);  // no key of the tile hidden
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int jl = 32 * u + 8 * (r >> 2) + 4 * hh + (r & 3);
+        const int j = j0 + jl;
+        const float bdv = (float)Rm[jl + 31 - c];
+        if (DEBUG && qi < p.T && j < p.L)
+          p.dbg_bd[(((int64_t)b * p.H + h) * p.T + qi) * p.L + j] = p.scale_bd * bdv;
+        const float v = s[u][r] * sc_qk + bdv * sc_bd;
+        sc[u][r] = full || in_interval(j, iv) ? v : -INFINITY;
+        tmax = fmaxf(tmax, sc[u][r]);
+      }
+    __builtin_amdgcn_wave_barrier();
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    // Lazy rescale, as in the 16x16 kernel.
+    if (__any(tmax > m_run + 8.f)) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int d = 0; d < DK / 32; ++d) o[d] *= alpha;
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    float psum = 0.f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sc[u][r] = __builtin_amdgcn_exp2f(sc[u][r] - m_use);  // v_exp_f32; exp2(-inf) = 0
+        psum += sc[u][r];
+      }
+    l_run += psum;
+
+    // O^T += V^T Pr^T; k-slot e of step jj maps to key
+    // 32u + 16jj + (e < 4 ? 4hh + e : 8 + 4hh + e - 4), i.e. registers 8jj..8jj+7.
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        bf16x8 pb8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pb8[e] = (bf16)sc[u][8 * jj + e];
+        const int kb = (32 * u + 16 * jj + 4 * hh) * 2;
+#pragma unroll
+        for (int d = 0; d < DK / 32; ++d) {
+          const char* vrow = Vt + (32 * d + c) * C::VP;
+          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow + kb);
+          const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + kb + 16);
+          const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          o[d] = mma32(a, pb8, o[d]);
+        }
+      }
+
+    __syncthreads();  // every wave is done with this tile's K / V^T
+    if (more) {
+      if constexpr (C::PREFETCH)
+        stage();
+      else
+        copy_direct(j0 + NK);
+    }
+    __syncthreads();
+  }
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (qi < p.T) {
+    bf16* orow = reinterpret_cast<bf16*>(p.o) + (int64_t)b * p.o_bs + (int64_t)qi * p.o_rs + h * DK;
+#pragma unroll
+    for (int d = 0; d < DK / 32; ++d)
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        bf16x4 v4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v4[e] = (bf16)(o[d][4 * m + e] * inv);
+        *reinterpret_cast<bf16x4*>(orow + 32 * d + 8 * m + 4 * hh) = v4;
+      }
+  }
+}
+
+template <int DK, int NW, bool DEBUG>
+hipError_t launch2(const AttnParams& p, int nb, hipStream_t s) {
+  using C = Cfg2<DK, NW>;
+  dim3 grid((p.T + C::QB - 1) / C::QB, p.H, nb);
+  hipLaunchKernelGGL((attn_bf16_kernel<DK, NW, DEBUG>), grid, dim3(C::NT), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int DK>
+hipError_t dispatch_bf16(const AttnParams& p, int nb, hipStream_t s) {
+  const bool dbg = p.dbg_bd != nullptr;
+  const int64_t bh = (int64_t)p.H * nb;
+  if ((p.T + 127) / 128 * bh >= 320)
+    return dbg ? launch2<DK, 4, true>(p, nb, s) : launch2<DK, 4, false>(p, nb, s);
+  if ((p.T + 63) / 64 * bh >= 128)
+    return dbg ? launch2<DK, 2, true>(p, nb, s) : launch2<DK, 2, false>(p, nb, s);
+  return dbg ? launch2<DK, 1, true>(p, nb, s) : launch2<DK, 1, false>(p, nb, s);
 }
 
 template <typename T, int DK, int NW, bool DEBUG>
@@ -307,7 +615,7 @@ __global__ void mask_kernel(const AttnParams p, uint8_t* out) {
   const int64_t n = (int64_t)p.T * p.L;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.x * blockDim.x) {
     const int i = (int)(e / p.L), j = (int)(e % p.L);
-    out[bl * n + e] = pair_visible(p, bl, i, j) ? 1 : 0;
+    out[bl * n + e] = in_interval(j, query_interval(p, bl, i)) ? 1 : 0;
   }
 }
 
@@ -334,6 +642,15 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
       p.o_bs % epv)
     return hipErrorInvalidValue;
   if (p.ring_len < 0 || (p.ring_len && p.ring_head < 0)) return hipErrorInvalidValue;
+  if (p.vt) {
+    // V^T columns of each batch are read in whole 64-key tiles
+    if (dt != kBF16 || p.ring_len || !aligned16(p.vt) || p.vt_ld % 8 || p.vt_bs % 64 || p.vt_bs < p.T ||
+        p.vt_ld < (int64_t)(p.b0 + nb) * p.vt_bs || p.L != p.T)
+      return hipErrorInvalidValue;
+    if (head_dim == 64) return dispatch_bf16<64>(p, nb, s);
+    if (head_dim == 128) return dispatch_bf16<128>(p, nb, s);
+    return hipErrorInvalidValue;
+  }
   if (dt == kF32) {
     if (head_dim == 64) return dispatch_nw<float, 64>(p, nb, s);
     if (head_dim == 128) return dispatch_nw<float, 128>(p, nb, s);

@@ -21,6 +21,10 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx2 __attribute__((ext_vector_type(2)));
+// 16- and 8-byte chunks as native vectors (HIP's uint4/uint2 are wrapper
+// structs that keep staging arrays from being promoted to registers).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 namespace mhsa {
 
@@ -47,6 +51,13 @@ __device__ __forceinline__ floatx4 mma16(const floatx4 a, const floatx4 b, float
 }
 __device__ __forceinline__ floatx4 mma16(const bf16x8 a, const bf16x8 b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// 32x32 output tile, K = 16: lane l holds A[l%32][8*(l/32) + e],
+// B[8*(l/32) + e][l%32] and C rows 8*(r/4) + 4*(l/32) + r%4 of column l%32.
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ floatx16 mma32(const bf16x8 a, const bf16x8 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 // Round an fp32 value to the storage type and back (identity for fp32).

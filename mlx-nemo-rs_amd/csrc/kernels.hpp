@@ -30,7 +30,23 @@ struct GemmParams {
   int64_t ldc = 0;
   int M = 0, N = 0, K = 0;
   int seg_rows = 0, seg_stride = 0, ring_off = 0, ring_len = 0;
+  // fp32 scratch for K-split partial sums (small problems); null = no split
+  float* partial = nullptr;
+  int64_t partial_elems = 0;
+  // Optional transposed copy of output columns [vt_col0, N) (the V
+  // projection): VT[col - vt_col0][(row / seg_T) * vt_Tpad + row % seg_T],
+  // row stride vt_ld; those columns are then not written to C. Columns past
+  // each utterance's seg_T tokens receive finite filler.
+  void* vt = nullptr;
+  int64_t vt_ld = 0;
+  int vt_col0 = 0, vt_Tpad = 0;
+  // > 0: M tiles per utterance of seg_T rows (M a multiple of seg_T);
+  // required with vt, where utterance b's tokens start at column b * vt_Tpad
+  int seg_T = 0;
 };
+// Scratch the K-split path can use: 64x64 tiles x splits stays <= ~512
+// workgroups, so M*N*splits <= kGemmPartialElems.
+constexpr int64_t kGemmPartialElems = (int64_t)1 << 22;
 hipError_t gemm(DType dt, bool quantized, const GemmParams& p, hipStream_t s);
 
 constexpr int kMaxBatch = 64;
@@ -56,6 +72,10 @@ struct AttnParams {
   void* o = nullptr;
   int64_t o_bs = 0, o_rs = 0;
   float* dbg_bd = nullptr;  // debug: scaled position scores [B, H, T, L]
+  // bf16 path: V^T [H*dk][B*Tpad] (key j of batch b at column b*vt_bs + j,
+  // zeros or finite values past T); null selects the row-major V path.
+  const void* vt = nullptr;
+  int64_t vt_ld = 0, vt_bs = 0;
   int T = 0, L = 0, qoff = 0, H = 0;
   float scale = 0.f, scale_bd = 0.f;
   int has_ctx = 0, left = -1, right = -1, chunked = 0;

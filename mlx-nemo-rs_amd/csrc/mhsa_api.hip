@@ -194,6 +194,8 @@ struct mhsa_layer {
   const float* d_pbv = nullptr;
   // scratch
   DevBuf ws;
+  DevBuf gemm_partial;         // K-split partial sums of small GEMMs
+  DevBuf vtbuf;                // bf16: transposed V [D][B * Tpad]
   DevBuf hbuf;                 // sublayer: LayerNorm output
   DevBuf ln_dev;               // sublayer: LayerNorm gamma, beta
   std::vector<float> ln_host;  // values currently in ln_dev
@@ -311,9 +313,17 @@ int32_t prepare(mhsa_layer* L) {
   return MHSA_OK;
 }
 
+// Transposed output of the V projection for the bf16 attention kernel.
+struct VtOut {
+  void* p = nullptr;
+  int64_t ld = 0;  // row stride (elements) = B * Tpad
+  int col0 = 0;    // first GEMM output column that belongs to V
+  int T = 0, Tpad = 0;
+};
+
 int32_t run_gemm(mhsa_layer* L, const DevLinear& lin, int n_rows_w, const void* A, int64_t lda, int M, void* C,
                  int64_t ldc, const void* R, int64_t ldr, hipStream_t s, int seg_rows = 0, int seg_stride = 0,
-                 int ring_off = 0, int ring_len = 0) {
+                 int ring_off = 0, int ring_len = 0, const VtOut* vt = nullptr) {
   mhsa::GemmParams p;
   p.A = A;
   p.lda = lda;
@@ -331,17 +341,41 @@ int32_t run_gemm(mhsa_layer* L, const DevLinear& lin, int n_rows_w, const void* 
   p.seg_stride = seg_rows > 0 ? seg_stride : 0;
   p.ring_off = ring_off;
   p.ring_len = ring_len > 0 ? ring_len : std::max(M, 1);
+  HIPCHK(L->gemm_partial.ensure((size_t)mhsa::kGemmPartialElems * sizeof(float)));
+  p.partial = static_cast<float*>(L->gemm_partial.p);
+  p.partial_elems = mhsa::kGemmPartialElems;
+  if (vt) {
+    p.vt = vt->p;
+    p.vt_ld = vt->ld;
+    p.vt_col0 = vt->col0;
+    p.vt_Tpad = vt->Tpad;
+    p.seg_T = vt->T;  // per-utterance M tiles
+  }
   HIPCHK(mhsa::gemm(dtype_of(L), lin.quantized, p, s));
   return MHSA_OK;
 }
 
 // q, k, v (and optionally only k, v) projections of `A` [M, D].
-int32_t project_qkv(mhsa_layer* L, const void* A, int M, void* out, int64_t ldo, hipStream_t s) {
+// With `vt`, V goes to the transposed buffer instead of columns [2D, 3D).
+int32_t project_qkv(mhsa_layer* L, const void* A, int M, void* out, int64_t ldo, hipStream_t s,
+                    const VtOut* vt = nullptr) {
   const size_t es = esz(L);
-  if (L->qkv_fused) return run_gemm(L, L->dev[0], 3 * L->D, A, L->D, M, out, ldo, nullptr, 0, s);
+  if (L->qkv_fused) {
+    VtOut v;
+    if (vt) {
+      v = *vt;
+      v.col0 = 2 * L->D;
+    }
+    return run_gemm(L, L->dev[0], 3 * L->D, A, L->D, M, out, ldo, nullptr, 0, s, 0, 0, 0, 0, vt ? &v : nullptr);
+  }
   for (int i = 0; i < 3; ++i) {
+    VtOut v;
+    if (vt && i == 2) {
+      v = *vt;
+      v.col0 = 0;
+    }
     int32_t rc = run_gemm(L, L->dev[i], L->D, A, L->D, M, static_cast<char*>(out) + (size_t)i * L->D * es, ldo,
-                          nullptr, 0, s);
+                          nullptr, 0, s, 0, 0, 0, 0, (vt && i == 2) ? &v : nullptr);
     if (rc) return rc;
   }
   return MHSA_OK;
@@ -453,10 +487,24 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   char* qkv = static_cast<char*>(L->ws.p);
   char* P = qkv + qkv_b;
   char* cx = P + p_b;
+  // bf16: V also transposed per batch, [D][B * Tpad], for the MFMA PV operand;
+  // zero-filled on allocation so padding columns are finite
+  VtOut vt;
+  const bool use_vt = L->dt == mhsa::kBF16;
+  if (use_vt) {
+    vt.T = T;
+    vt.Tpad = (int)align_up(T, 256);  // whole GEMM tiles of tokens per utterance
+    vt.ld = (int64_t)B * vt.Tpad;
+    const size_t bytes = (size_t)D * vt.ld * 2;
+    const size_t before = L->vtbuf.n;
+    HIPCHK(L->vtbuf.ensure(bytes));
+    if (L->vtbuf.n != before) HIPCHK(hipMemsetAsync(L->vtbuf.p, 0, L->vtbuf.n, s));
+    vt.p = L->vtbuf.p;
+  }
 
   {
     ProfScope ps(L, "gemm_qkv", s);
-    if ((rc = project_qkv(L, x, (int)M, qkv, 3 * D, s))) return rc;
+    if ((rc = project_qkv(L, x, (int)M, qkv, 3 * D, s, use_vt ? &vt : nullptr))) return rc;
   }
   {
     ProfScope ps(L, "gemm_pos", s);
@@ -480,6 +528,11 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   a.o_bs = (int64_t)T * D;
   a.o_rs = D;
   a.dbg_bd = dbg_bd;
+  if (use_vt) {
+    a.vt = vt.p;
+    a.vt_ld = vt.ld;
+    a.vt_bs = vt.Tpad;
+  }
   a.T = T;
   a.L = T;
   a.qoff = 0;
@@ -1018,12 +1071,23 @@ int32_t mhsa_debug_rel_shift_index(int32_t rows, int32_t total_len, int32_t* out
 }
 
 int32_t mhsa_debug_position_scores(mhsa_layer* L, const void* x, int32_t B, int32_t T, const void* pos_emb,
-                                   int32_t pos_len, float* out, void* hs) {
+                                   int32_t pos_len, float* out, void* q_out, void* p_out, void* hs) {
   if (int32_t rc = check_layer(L)) return rc;
   if (!out) return fail(MHSA_EINVAL, "null output pointer");
   hipStream_t s = static_cast<hipStream_t>(hs);
   int32_t rc = forward_impl(L, x, B, T, pos_emb, pos_len, nullptr, nullptr, nullptr, nullptr, out, s);
   if (rc) return rc;
+  // the workspace still holds [q | k | v] rows and, after them, the projected
+  // position table (all pos_len rows: full attention projects every row)
+  const size_t es = esz(L);
+  const int64_t M = (int64_t)B * T;
+  const char* qkv = static_cast<const char*>(L->ws.p);
+  if (q_out)
+    HIPCHK(hipMemcpy2DAsync(q_out, (size_t)L->D * es, qkv, (size_t)3 * L->D * es, (size_t)L->D * es, (size_t)M,
+                            hipMemcpyDeviceToDevice, s));
+  if (p_out)
+    HIPCHK(hipMemcpyAsync(p_out, qkv + align_up(M * 3 * L->D * es, 256), (size_t)pos_len * L->D * es,
+                          hipMemcpyDeviceToDevice, s));
   HIPCHK(hipStreamSynchronize(s));
   return MHSA_OK;
 }

@@ -72,9 +72,9 @@ __global__ void ring_copy_kernel(const char* src, char* dst, int B, int n, int r
     const int64_t lin = ((int64_t)b * n + t) * row_bytes + c * 16;
     const int64_t ring = ((int64_t)b * R + (off + t) % R) * ld_bytes + c * 16;
     if (to_ring)
-      *reinterpret_cast<uint4*>(dst + ring) = *reinterpret_cast<const uint4*>(src + lin);
+      *reinterpret_cast<u32x4*>(dst + ring) = *reinterpret_cast<const u32x4*>(src + lin);
     else
-      *reinterpret_cast<uint4*>(dst + lin) = *reinterpret_cast<const uint4*>(src + ring);
+      *reinterpret_cast<u32x4*>(dst + lin) = *reinterpret_cast<const u32x4*>(src + ring);
   }
 }
 
@@ -84,8 +84,8 @@ __global__ void dequant_kernel(const uint32_t* w, const float* sb, float* out, i
   const int64_t total = (int64_t)N * chunks;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
     const int n = (int)(e / chunks), k = (int)(e % chunks) * 16;
-    const uint4 q = *reinterpret_cast<const uint4*>(reinterpret_cast<const unsigned char*>(w) + (int64_t)n * K + k);
-    const float2 s = *reinterpret_cast<const float2*>(sb + 2 * ((int64_t)n * (K / 64) + k / 64));
+    const u32x4 q = *reinterpret_cast<const u32x4*>(reinterpret_cast<const unsigned char*>(w) + (int64_t)n * K + k);
+    const floatx2 s = *reinterpret_cast<const floatx2*>(sb + 2 * ((int64_t)n * (K / 64) + k / 64));
     T vals[16];
     dequant16<T>(q, s.x, s.y, vals);
 #pragma unroll

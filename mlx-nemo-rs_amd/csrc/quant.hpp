@@ -14,7 +14,7 @@
 namespace mhsa {
 
 template <typename T>
-__device__ __forceinline__ void dequant16(const uint4 w, const float s, const float b, T* out) {
+__device__ __forceinline__ void dequant16(const u32x4 w, const float s, const float b, T* out) {
   const uint32_t words[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
   for (int i = 0; i < 4; ++i) {

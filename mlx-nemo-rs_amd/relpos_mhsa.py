@@ -107,7 +107,7 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_debug_offline_mask": (I, [I, I, P(Context), PI, VP, VP]),
         "mhsa_debug_stream_mask": (I, [I, I, I, P(StreamMask), VP, VP]),
         "mhsa_debug_rel_shift_index": (I, [I, I, VP, VP]),
-        "mhsa_debug_position_scores": (I, [VP, VP, I, I, VP, I, VP, VP]),
+        "mhsa_debug_position_scores": (I, [VP, VP, I, I, VP, I, VP, VP, VP, VP]),
         "mhsa_profile_enable": (I, [VP, I]),
         "mhsa_profile_reset": (I, [VP]),
         "mhsa_profile_count": (I, [VP]),
@@ -435,15 +435,21 @@ class RelPositionMultiHeadAttention:
                                            _stream_ptr()))
         return out
 
-    def debug_position_scores(self, x, pos_emb):
+    def debug_position_scores(self, x, pos_emb, with_inputs: bool = False):
+        """Scaled rel-shifted position scores [B, H, T, T] (fp32); with
+        `with_inputs`, also the projected q [B, T, D] and position rows the
+        kernel consumed."""
         import torch
         b, t, d = x.shape
         pe = pos_emb.reshape(-1, d)
         self._check_dev(x, pe)
         out = torch.empty((b, self.n_heads(), t, t), dtype=torch.float32, device=x.device)
+        q = torch.empty_like(x) if with_inputs else None
+        p = torch.empty_like(pe) if with_inputs else None
         _check(self._lib.mhsa_debug_position_scores(self._h, _dptr(x), b, t, _dptr(pe), pe.shape[0], _dptr(out),
-                                                    _stream_ptr()))
-        return out
+                                                    _dptr(q) if q is not None else None,
+                                                    _dptr(p) if p is not None else None, _stream_ptr()))
+        return (out, q, p) if with_inputs else out
 
     def _check_dev(self, *ts):
         want = self.dtype
