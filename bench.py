@@ -41,7 +41,21 @@ def parse():
     ap.add_argument("--config", default="xl_offline_bf16")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device copy of BYTES (calibrates rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
+
+
+def copy_probe(nbytes: int):
+    """A plain copy kernel of known size: FETCH_SIZE / WRITE_SIZE for it should
+    read nbytes / 1024 KiB per dispatch; the ratio scales the path's counters."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": nbytes, "dispatches": 5}))
 
 
 def kernel_work(cfg, tag, lengths, fills):
@@ -73,6 +87,23 @@ def kernel_work(cfg, tag, lengths, fills):
     if tag == "layer_norm":
         es = 2 if cfg.dtype == "bfloat16" else 4
         return (2.0 * B * T * D * es, "GB/s", "hbm")
+    return None
+
+
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel`, from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    summary committed for this workload (each counter scaled by what it reads for a
+    plain copy of known size). None when no summary covers the kernel."""
+    path = os.path.join(ROOT, "profiles", f"hbm_traffic_{workload}.txt")
+    if not os.path.exists(path):
+        return None
+    ff = wf = None
+    for line in open(path):
+        kv = dict(t.split("=", 1) for t in line.split()[1:] if "=" in t)
+        if line.startswith("calibration"):
+            ff, wf = float(kv["fetch_factor"]), float(kv["write_factor"])
+        elif line.startswith("traffic") and kv.get("kernel") == kernel and ff is not None:
+            return round((float(kv["fetch_kib"]) * ff + float(kv["write_kib"]) * wf) * 1024.0)
     return None
 
 
@@ -125,6 +156,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X GPU", file=sys.stderr)
         sys.exit(1)
+    if args.copy_probe:
+        copy_probe(args.copy_probe)
+        return
     M.library()  # fails loudly if the HIP library is missing
     cfg = W.CONFIGS[args.config]
     layers_w, x, ex = W.instantiate(cfg)
@@ -221,7 +255,7 @@ def main():
         else:
             ach, peak = amount / (avg_ms * 1e-3) / 1e9, HBM_PEAK
         roof = {"bound": bound, "kernel": dom, "achieved": round(ach, 2), "peak": peak, "unit": unit,
-                "frac": round(ach / peak, 4), "traffic": None, "avg_launch_us": round(avg_ms * 1e3, 2),
+                "frac": round(ach / peak, 4), "traffic": measured_traffic(cfg.name, dom), "avg_launch_us": round(avg_ms * 1e3, 2),
                 "algorithmic_per_launch": amount}
 
     total_flops = W.algorithmic_flops(cfg, lengths, fills)
