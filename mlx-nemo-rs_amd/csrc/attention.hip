@@ -308,41 +308,59 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
 
 // ---------------------------------------------------------------------------
 // bf16 path with 32x32x16 MFMAs: 32 queries per wave, NW waves per
-// workgroup, 64-key tiles. K rows and a V^T tile (written transposed by the
-// projection GEMM) are staged in LDS and shared by the waves; the next tile
-// is fetched into registers while the current one is consumed. Each wave
-// reads its own position band straight from L2 into MFMA operands: 96 rows
-// (three 32-row band tiles) cover the pairs of its 32 queries and 64 keys,
-// and the last band tile of one key tile is the first of the next, so only
-// two are computed per step. bd is rounded to bf16 in the remap strip, as the
-// reference stores matrix_bd in bf16 (attention.rs:530).
+// workgroup, 64-key tiles.
+//  * K rows and a V^T tile (written transposed by the projection GEMM) are
+//    double-buffered in LDS and shared by the waves: the next tile is fetched
+//    into registers while the current one is consumed, one barrier per tile.
+//    K rows are staged in the order key(m) = m with bits 2 and 3 swapped, so
+//    the score MFMA's output registers hold, per lane, 8 consecutive keys of
+//    each 16-key step: exactly the B operand layout of the PV MFMA, whose V^T
+//    operand is then one 16-byte LDS read.
+//  * Each wave reads its own position band straight from L2 into MFMA
+//    operands, issued ahead of the score MFMAs: 96 rows (three 32-row band tiles)
+//    cover the pairs of its 32 queries and 64 keys, and the last band tile of
+//    one key tile is the first of the next, so two are computed per step.
+//  * Only q_u = q + pos_bias_u is held in registers. The position term uses
+//    q_v P^T = q_u P^T - (u - v) . P[n]; the per-row constant comes from
+//    pos_bias_diff and is the band MFMA's initial accumulator.
+//  * bd is rounded to bf16 in the remap strip, as the reference stores
+//    matrix_bd in bf16 (attention.rs:530). The logits are
+//    s * (q_u k + bd): the reference scales bd by cast(s) (attention.rs:
+//    308-311), which differs from s by 1.1e-4 relative at d_k = 128, far
+//    below the bf16 resolution of bd itself.
 // ---------------------------------------------------------------------------
 template <int DK, int NW>
 struct Cfg2 {
   static constexpr int NT = 64 * NW;
   static constexpr int QB = 32 * NW;
   static constexpr int NK = 64;
-  static constexpr int KP = DK * 2 + 16;      // K row pitch (bytes)
-  static constexpr int VP = NK * 2 + 16;      // V^T row pitch (bytes)
-  static constexpr int RMP = 96 + 8;          // remap row pitch (bf16 elements)
-  static constexpr int K_OFF = 0;
-  static constexpr int V_OFF = K_OFF + NK * KP;
-  static constexpr int R_OFF = V_OFF + DK * VP;
+  static constexpr int KP = DK * 2 + 16;   // K row pitch (bytes)
+  static constexpr int VP = NK * 2 + 16;   // V^T row pitch (bytes)
+  static constexpr int RMP = 96 + 8;       // remap row pitch (bf16 elements)
+  static constexpr int KBUF = NK * KP;
+  static constexpr int VBUF = DK * VP;
+  static constexpr int K_OFF = 0;          // two K tiles
+  static constexpr int V_OFF = 2 * KBUF;   // two V^T tiles
+  static constexpr int R_OFF = V_OFF + 2 * VBUF;
   static constexpr int LDS = R_OFF + NW * 32 * RMP * 2;
-  static constexpr int NS = DK / 16;          // 16-wide d_k steps
-  static constexpr int KCH = NK * (DK * 2 / 16) / NT;  // K chunks per thread
-  static constexpr int VCH = DK * (NK * 2 / 16) / NT;  // V^T chunks per thread
-  // Hold the next tile in registers only when that costs <= 32 VGPRs.
-  static constexpr bool PREFETCH = KCH + VCH <= 8;
+  static constexpr int NS = DK / 16;                    // 16-wide d_k steps
+  static constexpr int KCH = NK * (DK * 2 / 16) / NT;   // 16-byte K chunks per thread
+  static constexpr int VCH = DK * (NK * 2 / 16) / NT;   // 16-byte V^T chunks per thread
+  static_assert(KCH * NT == NK * (DK * 2 / 16) && VCH * NT == DK * (NK * 2 / 16), "tile split");
+  static_assert(LDS <= 160 * 1024, "LDS");
 };
+
+// Tile-local key held by LDS K row m (an involution on [0, 64)).
+__device__ __forceinline__ constexpr int swap23(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
+
+// 4 floats from a dword-aligned address.
+typedef float floatx4_u __attribute__((ext_vector_type(4), aligned(4)));
 
 template <int DK, int NW, bool DEBUG>
 __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p) {
   using C = Cfg2<DK, NW>;
-  constexpr int NT = C::NT, QB = C::QB, NK = C::NK;
+  constexpr int NT = C::NT, QB = C::QB, NK = C::NK, NS = C::NS;
   __shared__ __attribute__((aligned(16))) char smem[C::LDS];
-  char* Ks = smem + C::K_OFF;
-  char* Vt = smem + C::V_OFF;
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5, c = lane & 31;
   const int bl = blockIdx.z, b = p.b0 + bl, h = blockIdx.y;
@@ -351,19 +369,23 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p) 
   const int qi = iw + c;       // this lane's query column
   bf16* Rm = reinterpret_cast<bf16*>(smem + C::R_OFF) + (w * 32 + c) * C::RMP;
 
-  bf16x8 qu[C::NS], qv[C::NS];
+  // q_u fragments (B operand): lane holds d_k values 16s + 8hh + [0, 8).
+  // Rows past T read the last row (finite; their keys are all masked).
+  bf16x8 qu[NS];
   {
-    const bf16* qrow = reinterpret_cast<const bf16*>(p.q) + (int64_t)b * p.q_bs + (int64_t)qi * p.q_rs + h * DK;
-    const bool ok = qi < p.T;
+    const bf16* qrow =
+        reinterpret_cast<const bf16*>(p.q) + (int64_t)b * p.q_bs + (int64_t)min(qi, p.T - 1) * p.q_rs + h * DK;
+    const float* bu = p.bias_u + h * DK;
 #pragma unroll
-    for (int s = 0; s < C::NS; ++s) {
+    for (int s = 0; s < NS; ++s) {
       const int d0 = 16 * s + 8 * hh;
-      const bf16x8 raw = load16<bf16x8>(qrow + d0, ok);
+      const bf16x8 raw = *reinterpret_cast<const bf16x8*>(qrow + d0);
+      const floatx4 b0 = *reinterpret_cast<const floatx4*>(bu + d0);
+      const floatx4 b1 = *reinterpret_cast<const floatx4*>(bu + d0 + 4);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = (float)raw[e];
-        qu[s][e] = (bf16)(ok ? x + p.bias_u[h * DK + d0 + e] : 0.f);
-        qv[s][e] = (bf16)(ok ? x + p.bias_v[h * DK + d0 + e] : 0.f);
+      for (int e = 0; e < 4; ++e) {
+        qu[s][e] = (bf16)((float)raw[e] + b0[e]);
+        qu[s][e + 4] = (bf16)((float)raw[e + 4] + b1[e]);
       }
     }
   }
@@ -376,35 +398,21 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p) 
   int jbeg, jend;
   key_range(p, bl, i0, min(i0 + QB, p.T), jbeg, jend);
   const int2 iv = query_interval(p, bl, qi);
-  const float sc_qk = p.scale * kLog2e, sc_bd = p.scale_bd * kLog2e;
+  const float sc = p.scale * kLog2e;
+  const float thr = 8.f / sc;  // lazy rescale threshold (2^8 in probability)
   const char* kbase = reinterpret_cast<const char*>(p.k) + ((int64_t)b * p.kv_bs + h * DK) * 2;
   const char* vtbase = reinterpret_cast<const char*>(p.vt) + ((int64_t)h * DK * p.vt_ld + (int64_t)b * p.vt_bs) * 2;
-  const bf16* pbase = reinterpret_cast<const bf16*>(p.p) + h * DK;
+  const bf16* pbase = reinterpret_cast<const bf16*>(p.p) + h * DK + 8 * hh;
+  const float* pdh = p.pdiff + (int64_t)h * p.pdiff_ld + 4;  // row n at pdh[n], n in [-4, p_rows + 4)
 
-  constexpr int KR = C::PREFETCH ? C::KCH : 1, VR = C::PREFETCH ? C::VCH : 1;
-  u32x4 kr[KR], vr[VR];
-  // Without the register prefetch: copy one chunk at a time into LDS.
-  auto copy_direct = [&](int j0) {
-    for (int ch = tid; ch < NK * (DK * 2 / 16); ch += NT) {
-      const int row = ch / (DK * 2 / 16), cb = (ch % (DK * 2 / 16)) * 16;
-      const int j = j0 + row;
-      // rows past the last key are clamped (their scores are masked)
-      *reinterpret_cast<u32x4*>(Ks + row * C::KP + cb) =
-          *reinterpret_cast<const u32x4*>(kbase + (int64_t)min(j, p.L - 1) * p.kv_rs * 2 + cb);
-    }
-    for (int ch = tid; ch < DK * (NK * 2 / 16); ch += NT) {
-      const int d = ch / (NK * 2 / 16), cb = (ch % (NK * 2 / 16)) * 16;
-      *reinterpret_cast<u32x4*>(Vt + d * C::VP + cb) =
-          *reinterpret_cast<const u32x4*>(vtbase + (int64_t)d * p.vt_ld * 2 + (int64_t)j0 * 2 + cb);
-    }
-  };
+  u32x4 kr[C::KCH], vr[C::VCH];
   auto fetch = [&](int j0) {
 #pragma unroll
     for (int i = 0; i < C::KCH; ++i) {
       const int ch = tid + NT * i;
       const int row = ch / (DK * 2 / 16), cb = (ch % (DK * 2 / 16)) * 16;
-      const int j = j0 + row;
-      kr[i] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)min(j, p.L - 1) * p.kv_rs * 2 + cb);
+      // rows past the last key are clamped (their scores are masked)
+      kr[i] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)min(j0 + row, p.L - 1) * p.kv_rs * 2 + cb);
     }
 #pragma unroll
     for (int i = 0; i < C::VCH; ++i) {
@@ -413,12 +421,14 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p) 
       vr[i] = *reinterpret_cast<const u32x4*>(vtbase + (int64_t)d * p.vt_ld * 2 + (int64_t)j0 * 2 + cb);
     }
   };
-  auto stage = [&]() {
+  auto stage = [&](int buf) {
+    char* Ks = smem + C::K_OFF + buf * C::KBUF;
+    char* Vt = smem + C::V_OFF + buf * C::VBUF;
 #pragma unroll
     for (int i = 0; i < C::KCH; ++i) {
       const int ch = tid + NT * i;
       const int row = ch / (DK * 2 / 16), cb = (ch % (DK * 2 / 16)) * 16;
-      *reinterpret_cast<u32x4*>(Ks + row * C::KP + cb) = kr[i];
+      *reinterpret_cast<u32x4*>(Ks + swap23(row) * C::KP + cb) = kr[i];
     }
 #pragma unroll
     for (int i = 0; i < C::VCH; ++i) {
@@ -427,134 +437,160 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p) 
       *reinterpret_cast<u32x4*>(Vt + d * C::VP + cb) = vr[i];
     }
   };
+  // Band tile rows n0 + [0, 32): A operand row c, d_k values 16st + 8hh + [0, 8).
+  // Rows outside the table are clamped into it: every pair reading such a row
+  // lies outside its query's interval (past the last key or query, or beyond
+  // a window the table was checked to cover), so it is masked, and the finite
+  // values it reads cannot reach the output.
+  auto band_ptr = [&](int n0) { return pbase + (int64_t)min(max(n0 + c, 0), p.p_rows - 1) * p.p_rs; };
+  // Initial accumulator of band tile n0: row n0 + 8a + 4hh + e in register
+  // 4a + e. Groups of 4 rows wholly outside the table read the zero pad rows.
+  auto band_init = [&](int n0) {
+    floatx16 acc;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const int na = min(max(n0 + 8 * a + 4 * hh, -4), p.p_rows);
+      const floatx4_u v = *reinterpret_cast<const floatx4_u*>(pdh + na);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[4 * a + e] = v[e];
+    }
+    return acc;
+  };
 
   const int jfirst = (jbeg / NK) * NK;
+  // band rows of this wave for key tile j0: pb + [0, 96)
+  int pb = p.center - p.qoff - (iw + 31) + jfirst;
+  floatx16 carry = floatx16{};
   if (jfirst < jend) {
-    if constexpr (C::PREFETCH) {
-      fetch(jfirst);
-      stage();
-    } else {
-      copy_direct(jfirst);
-    }
+    fetch(jfirst);
+    stage(0);
+    carry = band_init(pb);
+    const bf16* r0 = band_ptr(pb);
+#pragma unroll
+    for (int st = 0; st < NS; ++st) carry = mma32(*reinterpret_cast<const bf16x8*>(r0 + 16 * st), qu[st], carry);
   }
   __syncthreads();
 
-  floatx16 carry = floatx16{};
-  for (int j0 = jfirst; j0 < jend; j0 += NK) {
+  int buf = 0;
+  for (int j0 = jfirst; j0 < jend; j0 += NK, buf ^= 1) {
     const bool more = j0 + NK < jend;
-    if (C::PREFETCH && more) fetch(j0 + NK);
-
-    // Position band of this wave: rows pb + n, n in [0, 96).
-    const int pb = p.center - p.qoff - (iw + 31) + j0;
-    floatx16 bd[3];
-    bd[0] = carry;
-    bd[1] = floatx16{};
-    bd[2] = floatx16{};
-    const bool first = j0 == jfirst;
-    if (first) bd[0] = floatx16{};
-    // Band rows outside the table are clamped into it: every pair reading
-    // such a row lies outside its query's interval (past the last key or
-    // query, or beyond a window the table was checked to cover), so it is
-    // masked, and the finite values it reads cannot reach the output.
-    const bf16* prow[3];
+    // band tiles 1 and 2 (rows pb + [32, 96)): initial accumulators and
+    // operands, issued before the K/V prefetch (loads complete in order), so
+    // the score MFMAs below cover their latency
+    floatx16 bd1 = band_init(pb + 32), bd2 = band_init(pb + 64);
+    bf16x8 pf[2][NS];
+    {
+      const bf16* r1 = band_ptr(pb + 32);
+      const bf16* r2 = band_ptr(pb + 64);
 #pragma unroll
-    for (int t = 0; t < 3; ++t)
-      prow[t] = pbase + (int64_t)min(max(pb + 32 * t + c, 0), p.p_rows - 1) * p.p_rs + 8 * hh;
-    floatx16 s[2] = {floatx16{}, floatx16{}};
-#pragma unroll
-    for (int st = 0; st < C::NS; ++st) {
-      const int cb = 32 * st + 16 * hh;  // byte offset of this lane's 8 d_k values
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(Ks + (32 * u + c) * C::KP + cb);
-        s[u] = mma32(a, qu[st], s[u]);
-      }
-#pragma unroll
-      for (int t = 0; t < 3; ++t) {
-        if (t == 0 && !first) continue;
-        const bf16x8 a = *reinterpret_cast<const bf16x8*>(prow[t] + 16 * st);
-        bd[t] = mma32(a, qv[st], bd[t]);
+      for (int st = 0; st < NS; ++st) {
+        pf[0][st] = *reinterpret_cast<const bf16x8*>(r1 + 16 * st);
+        pf[1][st] = *reinterpret_cast<const bf16x8*>(r2 + 16 * st);
       }
     }
-    carry = bd[2];
+    if (more) fetch(j0 + NK);
 
-    // rel_shift: band row n of query column c holds key j0 + n - 31 + c.
+    // S = K . q_u: output row m of block u is key 32u + swap23(m)
+    const char* Ks = smem + C::K_OFF + buf * C::KBUF;
+    floatx16 s[2] = {floatx16{}, floatx16{}};
 #pragma unroll
-    for (int t = 0; t < 3; ++t)
+    for (int st = 0; st < NS; ++st) {
+      const int cb = 32 * st + 16 * hh;  // byte offset of this lane's 8 d_k values
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
-        bf16x4 v4;
+      for (int u = 0; u < 2; ++u)
+        s[u] = mma32(*reinterpret_cast<const bf16x8*>(Ks + (32 * u + c) * C::KP + cb), qu[st], s[u]);
+    }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v4[e] = (bf16)bd[t][4 * m + e];
-        *reinterpret_cast<bf16x4*>(Rm + 32 * t + 8 * m + 4 * hh) = v4;
-      }
+    for (int st = 0; st < NS; ++st) {
+      bd1 = mma32(pf[0][st], qu[st], bd1);
+      bd2 = mma32(pf[1][st], qu[st], bd2);
+    }
+
+    // rel_shift: band row n of query column c pairs with key j0 + n - 31 + c.
+    {
+      const floatx16 bt[3] = {carry, bd1, bd2};
+#pragma unroll
+      for (int t = 0; t < 3; ++t)
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          bf16x4 v4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v4[e] = (bf16)bt[t][4 * a + e];
+          *reinterpret_cast<bf16x4*>(Rm + 32 * t + 8 * a + 4 * hh) = v4;
+        }
+    }
+    carry = bd2;
+    pb += NK;
     __builtin_amdgcn_wave_barrier();
 
-    float sc[2][16];
+    // x = q_u k + bd for this lane's keys jl(u, r) = 32u + 16(r / 8) + 8hh + r % 8
+    const bf16* rq = Rm + 31 - c + 8 * hh;
     float tmax = -INFINITY;
-    const bool full = __all(iv.x <= j0 && iv.y >= j0 + NK);  // no key of the tile hidden
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int jl = 32 * u + 8 * (r >> 2) + 4 * hh + (r & 3);
-        const int j = j0 + jl;
-        const float bdv = (float)Rm[jl + 31 - c];
-        if (DEBUG && qi < p.T && j < p.L)
-          p.dbg_bd[(((int64_t)b * p.H + h) * p.T + qi) * p.L + j] = p.scale_bd * bdv;
-        const float v = s[u][r] * sc_qk + bdv * sc_bd;
-        sc[u][r] = full || in_interval(j, iv) ? v : -INFINITY;
-        tmax = fmaxf(tmax, sc[u][r]);
+        const float bdv = (float)rq[32 * u + 16 * (r >> 3) + (r & 7)];
+        if (DEBUG) {
+          const int j = j0 + 32 * u + 16 * (r >> 3) + 8 * hh + (r & 7);
+          if (qi < p.T && j < p.L) p.dbg_bd[(((int64_t)b * p.H + h) * p.T + qi) * p.L + j] = p.scale_bd * bdv;
+        }
+        s[u][r] += bdv;
       }
     __builtin_amdgcn_wave_barrier();
+    if (!__all(iv.x <= j0 && iv.y >= j0 + NK)) {  // some key of the tile is hidden from some query
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int j = j0 + 32 * u + 16 * (r >> 3) + 8 * hh + (r & 7);
+          if (!in_interval(j, iv)) s[u][r] = -INFINITY;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[u][r]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    // Lazy rescale, as in the 16x16 kernel.
-    if (__any(tmax > m_run + 8.f)) {
+    // Lazy rescale: the running max moves only when a score exceeds it by
+    // more than thr, so probabilities stay below 2^8 and fp32 sums stay exact
+    // enough; the final normalisation divides by the same sum.
+    if (__any(tmax > m_run + thr)) {
       const float m_new = fmaxf(m_run, tmax);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+      const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m_run - m_new) * sc);
       m_run = m_new;
       l_run *= alpha;
 #pragma unroll
       for (int d = 0; d < DK / 32; ++d) o[d] *= alpha;
     }
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;
+    const float msc = m_run == -INFINITY ? 0.f : m_run * sc;
     float psum = 0.f;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        sc[u][r] = __builtin_amdgcn_exp2f(sc[u][r] - m_use);  // v_exp_f32; exp2(-inf) = 0
-        psum += sc[u][r];
+        s[u][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][r], sc, -msc));  // exp2(-inf) = 0
+        psum += s[u][r];
       }
     l_run += psum;
 
-    // O^T += V^T Pr^T; k-slot e of step jj maps to key
-    // 32u + 16jj + (e < 4 ? 4hh + e : 8 + 4hh + e - 4), i.e. registers 8jj..8jj+7.
+    // O^T += V^T P^T over 16-key steps (u, jj): k-slot e of lane (c, hh) is
+    // key 32u + 16jj + 8hh + e, register 8jj + e of block u.
+    const char* Vt = smem + C::V_OFF + buf * C::VBUF;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int jj = 0; jj < 2; ++jj) {
         bf16x8 pb8;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pb8[e] = (bf16)sc[u][8 * jj + e];
-        const int kb = (32 * u + 16 * jj + 4 * hh) * 2;
+        for (int e = 0; e < 8; ++e) pb8[e] = (bf16)s[u][8 * jj + e];
+        const int kb = (32 * u + 16 * jj + 8 * hh) * 2;
 #pragma unroll
-        for (int d = 0; d < DK / 32; ++d) {
-          const char* vrow = Vt + (32 * d + c) * C::VP;
-          const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow + kb);
-          const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + kb + 16);
-          const bf16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          o[d] = mma32(a, pb8, o[d]);
-        }
+        for (int d = 0; d < DK / 32; ++d)
+          o[d] = mma32(*reinterpret_cast<const bf16x8*>(Vt + (32 * d + c) * C::VP + kb), pb8, o[d]);
       }
 
-    __syncthreads();  // every wave is done with this tile's K / V^T
-    if (more) {
-      if constexpr (C::PREFETCH)
-        stage();
-      else
-        copy_direct(j0 + NK);
-    }
+    if (more) stage(buf ^ 1);  // that buffer was last read before the previous barrier
     __syncthreads();
   }
 
@@ -565,32 +601,46 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p) 
 #pragma unroll
     for (int d = 0; d < DK / 32; ++d)
 #pragma unroll
-      for (int m = 0; m < 4; ++m) {
+      for (int a = 0; a < 4; ++a) {
         bf16x4 v4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v4[e] = (bf16)(o[d][4 * m + e] * inv);
-        *reinterpret_cast<bf16x4*>(orow + 32 * d + 8 * m + 4 * hh) = v4;
+        for (int e = 0; e < 4; ++e) v4[e] = (bf16)(o[d][4 * a + e] * inv);
+        *reinterpret_cast<bf16x4*>(orow + 32 * d + 8 * a + 4 * hh) = v4;
       }
   }
 }
 
-template <int DK, int NW, bool DEBUG>
+template <int DK, bool DEBUG>
 hipError_t launch2(const AttnParams& p, int nb, hipStream_t s) {
-  using C = Cfg2<DK, NW>;
+  using C = Cfg2<DK, 4>;
   dim3 grid((p.T + C::QB - 1) / C::QB, p.H, nb);
-  hipLaunchKernelGGL((attn_bf16_kernel<DK, NW, DEBUG>), grid, dim3(C::NT), 0, s, p);
+  hipLaunchKernelGGL((attn_bf16_kernel<DK, 4, DEBUG>), grid, dim3(C::NT), 0, s, p);
   return hipGetLastError();
 }
 
 template <int DK>
 hipError_t dispatch_bf16(const AttnParams& p, int nb, hipStream_t s) {
-  const bool dbg = p.dbg_bd != nullptr;
-  const int64_t bh = (int64_t)p.H * nb;
-  if ((p.T + 127) / 128 * bh >= 320)
-    return dbg ? launch2<DK, 4, true>(p, nb, s) : launch2<DK, 4, false>(p, nb, s);
-  if ((p.T + 63) / 64 * bh >= 128)
-    return dbg ? launch2<DK, 2, true>(p, nb, s) : launch2<DK, 2, false>(p, nb, s);
-  return dbg ? launch2<DK, 1, true>(p, nb, s) : launch2<DK, 1, false>(p, nb, s);
+  return p.dbg_bd ? launch2<DK, true>(p, nb, s) : launch2<DK, false>(p, nb, s);
+}
+
+template <int DK>
+__global__ void pos_bias_diff_kernel(const AttnParams p, float* out, int64_t ld) {
+  const int h = blockIdx.y;
+  const int n = (int)(blockIdx.x * blockDim.x + threadIdx.x) - 4;
+  if (n >= p.p_rows + 4) return;
+  float acc = 0.f;
+  if (n >= 0 && n < p.p_rows) {
+    const bf16* row = reinterpret_cast<const bf16*>(p.p) + (int64_t)n * p.p_rs + h * DK;
+    const float* bu = p.bias_u + h * DK;
+    const float* bv = p.bias_v + h * DK;
+#pragma unroll 4
+    for (int k = 0; k < DK; k += 8) {
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(row + k);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf((float)v[e], bu[k + e] - bv[k + e], acc);
+    }
+  }
+  out[(int64_t)h * ld + n + 4] = -acc;
 }
 
 template <typename T, int DK, int NW, bool DEBUG>
@@ -645,7 +695,7 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
   if (p.vt) {
     // V^T columns of each batch are read in whole 64-key tiles
     if (dt != kBF16 || p.ring_len || !aligned16(p.vt) || p.vt_ld % 8 || p.vt_bs % 64 || p.vt_bs < p.T ||
-        p.vt_ld < (int64_t)(p.b0 + nb) * p.vt_bs || p.L != p.T)
+        p.vt_ld < (int64_t)(p.b0 + nb) * p.vt_bs || p.L != p.T || !p.pdiff || p.pdiff_ld < p.p_rows + 8)
       return hipErrorInvalidValue;
     if (head_dim == 64) return dispatch_bf16<64>(p, nb, s);
     if (head_dim == 128) return dispatch_bf16<128>(p, nb, s);
@@ -659,6 +709,21 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
     if (head_dim == 128) return dispatch_nw<bf16, 128>(p, nb, s);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t pos_bias_diff(int head_dim, const AttnParams& p, float* out, int64_t ld, hipStream_t s) {
+  if (p.p_rows <= 0 || p.H <= 0) return hipSuccess;
+  if (!p.p || !p.bias_u || !p.bias_v || !out || ld < p.p_rows + 8 || !aligned16(p.p) || p.p_rs % 8 ||
+      p.p_rs < (int64_t)p.H * head_dim)
+    return hipErrorInvalidValue;
+  const dim3 grid((p.p_rows + 8 + 255) / 256, p.H);
+  if (head_dim == 64)
+    hipLaunchKernelGGL(pos_bias_diff_kernel<64>, grid, dim3(256), 0, s, p, out, ld);
+  else if (head_dim == 128)
+    hipLaunchKernelGGL(pos_bias_diff_kernel<128>, grid, dim3(256), 0, s, p, out, ld);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
 }
 
 hipError_t export_mask(const AttnParams& p, int nb, uint8_t* out, hipStream_t s) {

@@ -76,6 +76,10 @@ struct AttnParams {
   // zeros or finite values past T); null selects the row-major V path.
   const void* vt = nullptr;
   int64_t vt_ld = 0, vt_bs = 0;
+  // bf16 path: -(bias_u - bias_v) . P[n] per head ([H][pdiff_ld] fp32, row n
+  // at column n + 4, four zero rows on each side), from pos_bias_diff
+  const float* pdiff = nullptr;
+  int64_t pdiff_ld = 0;
   int T = 0, L = 0, qoff = 0, H = 0;
   float scale = 0.f, scale_bd = 0.f;
   int has_ctx = 0, left = -1, right = -1, chunked = 0;
@@ -85,6 +89,9 @@ struct AttnParams {
   int q_valid[kMaxBatch];
 };
 hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nbatch, hipStream_t s);
+// The bf16 kernel's position-term offset: out[h][n + 4] = -(bias_u[h] - bias_v[h]) . P[n, h]
+// for n in [0, p_rows), zero for the four pad rows on each side (ld >= p_rows + 8).
+hipError_t pos_bias_diff(int head_dim, const AttnParams& p, float* out, int64_t ld, hipStream_t s);
 
 // Visibility map [nbatch, T, L] (1 = visible) from the same predicate the
 // attention kernel applies.

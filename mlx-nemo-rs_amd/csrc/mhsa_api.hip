@@ -481,16 +481,18 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   if ((rc = plan_positions(pos_len, T, dr, row0, nrows, center))) return rc;
 
   const int64_t M = (int64_t)B * T;
+  const bool use_vt = L->dt == mhsa::kBF16;
+  const int64_t pd_ld = nrows + 8;  // bf16 kernel's position-term offsets, 4 pad rows each side
   const size_t qkv_b = align_up(M * 3 * D * es, 256), p_b = align_up((int64_t)nrows * D * es, 256),
-               ctx_b = align_up(M * D * es, 256);
-  HIPCHK(L->ws.ensure(qkv_b + p_b + ctx_b));
+               ctx_b = align_up(M * D * es, 256), pd_b = use_vt ? align_up(L->H * pd_ld * 4, 256) : 0;
+  HIPCHK(L->ws.ensure(qkv_b + p_b + ctx_b + pd_b));
   char* qkv = static_cast<char*>(L->ws.p);
   char* P = qkv + qkv_b;
   char* cx = P + p_b;
+  float* pdiff = use_vt ? reinterpret_cast<float*>(cx + ctx_b) : nullptr;
   // bf16: V also transposed per batch, [D][B * Tpad], for the MFMA PV operand;
   // zero-filled on allocation so padding columns are finite
   VtOut vt;
-  const bool use_vt = L->dt == mhsa::kBF16;
   if (use_vt) {
     vt.T = T;
     vt.Tpad = (int)align_up(T, 256);  // whole GEMM tiles of tokens per utterance
@@ -532,6 +534,10 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
     a.vt = vt.p;
     a.vt_ld = vt.ld;
     a.vt_bs = vt.Tpad;
+    a.pdiff = pdiff;
+    a.pdiff_ld = pd_ld;
+    ProfScope ps(L, "pos_bias_diff", s);
+    HIPCHK(mhsa::pos_bias_diff(L->dk, a, pdiff, pd_ld, s));
   }
   a.T = T;
   a.L = T;
