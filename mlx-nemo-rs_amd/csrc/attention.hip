@@ -308,18 +308,28 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
 
 // ---------------------------------------------------------------------------
 // bf16 path with 32x32x16 MFMAs: 32 queries per wave, NW waves per
-// workgroup, 64-key tiles.
+// workgroup, 64-key tiles. Every operand a tile needs is in LDS before the
+// tile starts; the next tile's operands stream in meanwhile with
+// direct-to-LDS loads (global_load_lds, 64 lanes per load, lane l at LDS
+// base + l * size), so the loop waits on global memory only at its single
+// barrier per tile.
 //  * K rows and a V^T tile (written transposed by the projection GEMM) are
-//    double-buffered in LDS and shared by the waves: the next tile is fetched
-//    into registers while the current one is consumed, one barrier per tile.
-//    K rows are staged in the order key(m) = m with bits 2 and 3 swapped, so
-//    the score MFMA's output registers hold, per lane, 8 consecutive keys of
-//    each 16-key step: exactly the B operand layout of the PV MFMA, whose V^T
-//    operand is then one 16-byte LDS read.
-//  * Each wave reads its own position band straight from L2 into MFMA
-//    operands, issued ahead of the score MFMAs: 96 rows (three 32-row band tiles)
-//    cover the pairs of its 32 queries and 64 keys, and the last band tile of
-//    one key tile is the first of the next, so two are computed per step.
+//    double-buffered and shared by the waves. K rows are staged in the order
+//    key(m) = m with bits 2 and 3 swapped, so the score MFMA's output
+//    registers hold, per lane, 8 consecutive keys of each 16-key step:
+//    exactly the B operand layout of the PV MFMA, whose V^T operand is then
+//    one 16-byte LDS read.
+//  * Position rows live in a 256-row ring. Wave w needs, for key tile k,
+//    96 rows starting at pb_w = center - qoff - (i_w + 31) + j0 (three 32-row
+//    band tiles covering the pairs of its 32 queries and 64 keys); the last
+//    band tile of one key tile is the first of the next, so two are computed
+//    per step. Ring row rr holds position row R0 + rr with R0 the first row
+//    any wave needs: tile k uses rr in [64k + 32, 64k + 192) and loads
+//    [64k + 192, 64k + 256) for tile k + 1, 224 live rows. The per-row
+//    position-term offsets (below) ride along in a 256-entry float ring.
+//  * LDS rows are unpadded; 16-byte chunk j of a K, V^T or ring row r sits
+//    at chunk j ^ (r % chunks-per-row), so the 8 lanes an LDS read serves
+//    together hit 8 distinct bank groups.
 //  * Only q_u = q + pos_bias_u is held in registers. The position term uses
 //    q_v P^T = q_u P^T - (u - v) . P[n]; the per-row constant comes from
 //    pos_bias_diff and is the band MFMA's initial accumulator.
@@ -334,37 +344,49 @@ struct Cfg2 {
   static constexpr int NT = 64 * NW;
   static constexpr int QB = 32 * NW;
   static constexpr int NK = 64;
-  static constexpr int KP = DK * 2 + 16;   // K row pitch (bytes)
-  static constexpr int VP = NK * 2 + 16;   // V^T row pitch (bytes)
-  static constexpr int RMP = 96 + 8;       // remap row pitch (bf16 elements)
-  static constexpr int KBUF = NK * KP;
-  static constexpr int VBUF = DK * VP;
-  static constexpr int K_OFF = 0;          // two K tiles
-  static constexpr int V_OFF = 2 * KBUF;   // two V^T tiles
-  static constexpr int R_OFF = V_OFF + 2 * VBUF;
+  static constexpr int RB = DK * 2;        // bytes per K / position row
+  static constexpr int KCN = RB / 16;      // 16-byte chunks per K / position row
+  static constexpr int VCN = NK * 2 / 16;  // 16-byte chunks per V^T row (8)
+  static constexpr int RING = 256;         // position ring rows
+  static constexpr int RMP = 100;          // remap row pitch (bf16 elements)
+  static constexpr int KBUF = NK * RB;
+  static constexpr int VBUF = DK * NK * 2;
+  static constexpr int K_OFF = 0;                    // two K tiles
+  static constexpr int V_OFF = 2 * KBUF;             // two V^T tiles
+  static constexpr int P_OFF = V_OFF + 2 * VBUF;     // position ring
+  static constexpr int D_OFF = P_OFF + RING * RB;    // offset ring (floats)
+  static constexpr int R_OFF = D_OFF + RING * 4;     // remap strips
   static constexpr int LDS = R_OFF + NW * 32 * RMP * 2;
-  static constexpr int NS = DK / 16;                    // 16-wide d_k steps
-  static constexpr int KCH = NK * (DK * 2 / 16) / NT;   // 16-byte K chunks per thread
-  static constexpr int VCH = DK * (NK * 2 / 16) / NT;   // 16-byte V^T chunks per thread
-  static_assert(KCH * NT == NK * (DK * 2 / 16) && VCH * NT == DK * (NK * 2 / 16), "tile split");
+  static constexpr int NS = DK / 16;                 // 16-wide d_k steps
+  static constexpr int KDMA = KBUF / 1024 / NW;      // 1 KB direct-to-LDS loads per wave and tile
+  static constexpr int VDMA = VBUF / 1024 / NW;
+  static constexpr int RPL = 1024 / RB;              // position rows per 1 KB load
+  static constexpr int PDMA = 64 / RPL / NW;         // position loads per wave for 64 rows
+  static_assert(KDMA * NW * 1024 == KBUF && VDMA * NW * 1024 == VBUF && PDMA * NW * RPL == 64, "tile split");
   static_assert(LDS <= 160 * 1024, "LDS");
 };
 
 // Tile-local key held by LDS K row m (an involution on [0, 64)).
 __device__ __forceinline__ constexpr int swap23(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
 
-// 4 floats from a dword-aligned address.
-typedef float floatx4_u __attribute__((ext_vector_type(4), aligned(4)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 template <int DK, int NW, bool DEBUG>
-__global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p) {
+__global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, int nb) {
   using C = Cfg2<DK, NW>;
-  constexpr int NT = C::NT, QB = C::QB, NK = C::NK, NS = C::NS;
+  constexpr int QB = C::QB, NK = C::NK, NS = C::NS, RB = C::RB;
   __shared__ __attribute__((aligned(16))) char smem[C::LDS];
 
+  // Work order for 8 XCDs: workgroup L runs on XCD L % 8, so each XCD gets a
+  // contiguous range of (head, item, query block) work items and keeps those
+  // heads' position rows and K/V in its own L2. The grid is a multiple of 8.
+  const int nqb = (p.T + QB - 1) / QB;
+  const int per = (int)gridDim.x / 8;
+  const int W = ((int)blockIdx.x % 8) * per + (int)blockIdx.x / 8;
+  if (W >= nqb * nb * p.H) return;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5, c = lane & 31;
-  const int bl = blockIdx.z, b = p.b0 + bl, h = blockIdx.y;
-  const int i0 = blockIdx.x * QB;
+  const int bl = (W / nqb) % nb, b = p.b0 + bl, h = W / (nqb * nb);
+  const int i0 = (W % nqb) * QB;
   const int iw = i0 + 32 * w;  // first query of this wave
   const int qi = iw + c;       // this lane's query column
   bf16* Rm = reinterpret_cast<bf16*>(smem + C::R_OFF) + (w * 32 + c) * C::RMP;
@@ -400,111 +422,109 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p) 
   const int2 iv = query_interval(p, bl, qi);
   const float sc = p.scale * kLog2e;
   const float thr = 8.f / sc;  // lazy rescale threshold (2^8 in probability)
+  const int jfirst = (jbeg / NK) * NK;
+  // ring row rr holds position row R0 + rr
+  const int R0 = p.center - p.qoff - (i0 + 31) + jfirst - 96;
+
   const char* kbase = reinterpret_cast<const char*>(p.k) + ((int64_t)b * p.kv_bs + h * DK) * 2;
   const char* vtbase = reinterpret_cast<const char*>(p.vt) + ((int64_t)h * DK * p.vt_ld + (int64_t)b * p.vt_bs) * 2;
-  const bf16* pbase = reinterpret_cast<const bf16*>(p.p) + h * DK + 8 * hh;
+  const char* pbase = reinterpret_cast<const char*>(p.p) + h * DK * 2;
   const float* pdh = p.pdiff + (int64_t)h * p.pdiff_ld + 4;  // row n at pdh[n], n in [-4, p_rows + 4)
 
-  u32x4 kr[C::KCH], vr[C::VCH];
-  auto fetch = [&](int j0) {
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int ch = tid + NT * i;
-      const int row = ch / (DK * 2 / 16), cb = (ch % (DK * 2 / 16)) * 16;
-      // rows past the last key are clamped (their scores are masked)
-      kr[i] = *reinterpret_cast<const u32x4*>(kbase + (int64_t)min(j0 + row, p.L - 1) * p.kv_rs * 2 + cb);
-    }
-#pragma unroll
-    for (int i = 0; i < C::VCH; ++i) {
-      const int ch = tid + NT * i;
-      const int d = ch / (NK * 2 / 16), cb = (ch % (NK * 2 / 16)) * 16;
-      vr[i] = *reinterpret_cast<const u32x4*>(vtbase + (int64_t)d * p.vt_ld * 2 + (int64_t)j0 * 2 + cb);
-    }
-  };
-  auto stage = [&](int buf) {
+  // Direct-to-LDS loads of key tile j0 into buffer buf: this wave's share of
+  // the K and V^T chunks. Keys past the last one read the last row (masked).
+  auto load_tile = [&](int j0, int buf) {
     char* Ks = smem + C::K_OFF + buf * C::KBUF;
     char* Vt = smem + C::V_OFF + buf * C::VBUF;
 #pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int ch = tid + NT * i;
-      const int row = ch / (DK * 2 / 16), cb = (ch % (DK * 2 / 16)) * 16;
-      *reinterpret_cast<u32x4*>(Ks + swap23(row) * C::KP + cb) = kr[i];
+    for (int g = 0; g < C::KDMA; ++g) {
+      const int pos = (w * C::KDMA + g) * 64 + lane;
+      const int m = pos / C::KCN, q = pos % C::KCN;
+      const char* src = kbase + (int64_t)min(j0 + swap23(m), p.L - 1) * p.kv_rs * 2 + 16 * (q ^ (m % C::KCN));
+      __builtin_amdgcn_global_load_lds(src, (lds_void*)(Ks + (w * C::KDMA + g) * 1024), 16, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < C::VCH; ++i) {
-      const int ch = tid + NT * i;
-      const int d = ch / (NK * 2 / 16), cb = (ch % (NK * 2 / 16)) * 16;
-      *reinterpret_cast<u32x4*>(Vt + d * C::VP + cb) = vr[i];
+    for (int g = 0; g < C::VDMA; ++g) {
+      const int pos = (w * C::VDMA + g) * 64 + lane;
+      const int d = pos / C::VCN, q = pos % C::VCN;
+      const char* src = vtbase + (int64_t)d * p.vt_ld * 2 + (int64_t)j0 * 2 + 16 * (q ^ (d % C::VCN));
+      __builtin_amdgcn_global_load_lds(src, (lds_void*)(Vt + (w * C::VDMA + g) * 1024), 16, 0, 0);
     }
   };
-  // Band tile rows n0 + [0, 32): A operand row c, d_k values 16st + 8hh + [0, 8).
-  // Rows outside the table are clamped into it: every pair reading such a row
-  // lies outside its query's interval (past the last key or query, or beyond
-  // a window the table was checked to cover), so it is masked, and the finite
-  // values it reads cannot reach the output.
-  auto band_ptr = [&](int n0) { return pbase + (int64_t)min(max(n0 + c, 0), p.p_rows - 1) * p.p_rs; };
-  // Initial accumulator of band tile n0: row n0 + 8a + 4hh + e in register
-  // 4a + e. Groups of 4 rows wholly outside the table read the zero pad rows.
-  auto band_init = [&](int n0) {
+  // Ring rows [rr0, rr0 + 64) (rr0 a multiple of 64): this wave's share of
+  // the position rows, and (wave 0) their offsets. Rows outside the table are
+  // clamped into it (offsets: into the zero pad rows). Every pair reading such
+  // a row lies outside its query's interval (past the last key or query, or
+  // beyond a window the table was checked to cover), so it is masked, and the
+  // finite values it reads cannot reach the output.
+  auto load_ring = [&](int rr0) {
+    char* ring = smem + C::P_OFF;
+#pragma unroll
+    for (int g = 0; g < C::PDMA; ++g) {
+      const int rr = rr0 + (w * C::PDMA + g) * C::RPL + lane / C::KCN, q = lane % C::KCN;
+      const int n = min(max(R0 + rr, 0), p.p_rows - 1);
+      const char* src = pbase + (int64_t)n * p.p_rs * 2 + 16 * (q ^ (rr % C::KCN));
+      __builtin_amdgcn_global_load_lds(src, (lds_void*)(ring + ((rr0 + (w * C::PDMA + g) * C::RPL) % C::RING) * RB),
+                                       16, 0, 0);
+    }
+    if (w == 0) {
+      const int n = min(max(R0 + rr0 + lane, -4), p.p_rows + 3);
+      __builtin_amdgcn_global_load_lds(pdh + n, (lds_void*)(smem + C::D_OFF + (rr0 % C::RING) * 4), 4, 0, 0);
+    }
+  };
+
+  // This lane's byte offset of the 16-byte chunk 2st + hh of row c in a
+  // K tile or ring block of 32 rows starting at a multiple of 32.
+  int lo[NS];
+#pragma unroll
+  for (int st = 0; st < NS; ++st) lo[st] = c * RB + 16 * ((2 * st + hh) ^ (c % C::KCN));
+  // Band tile of 32 ring rows from rr (a multiple of 32): initial accumulator
+  // (row rr + 8a + 4hh + e in register 4a + e) and MFMAs.
+  auto band_tile = [&](int rr) {
+    const float* dr = reinterpret_cast<const float*>(smem + C::D_OFF) + (rr % C::RING) + 4 * hh;
     floatx16 acc;
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
-      const int na = min(max(n0 + 8 * a + 4 * hh, -4), p.p_rows);
-      const floatx4_u v = *reinterpret_cast<const floatx4_u*>(pdh + na);
+      const floatx4 v = *reinterpret_cast<const floatx4*>(dr + 8 * a);
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[4 * a + e] = v[e];
     }
+    const char* rb = smem + C::P_OFF + (rr % C::RING) * RB;
+#pragma unroll
+    for (int st = 0; st < NS; ++st) acc = mma32(*reinterpret_cast<const bf16x8*>(rb + lo[st]), qu[st], acc);
     return acc;
   };
 
-  const int jfirst = (jbeg / NK) * NK;
-  // band rows of this wave for key tile j0: pb + [0, 96)
-  int pb = p.center - p.qoff - (iw + 31) + jfirst;
+  // ring row of band tile 0 of this wave for key tile k: 64k + 96 - 32w
+  int rrw = 96 - 32 * w;
   floatx16 carry = floatx16{};
   if (jfirst < jend) {
-    fetch(jfirst);
-    stage(0);
-    carry = band_init(pb);
-    const bf16* r0 = band_ptr(pb);
-#pragma unroll
-    for (int st = 0; st < NS; ++st) carry = mma32(*reinterpret_cast<const bf16x8*>(r0 + 16 * st), qu[st], carry);
+    load_tile(jfirst, 0);
+    load_ring(0);
+    load_ring(64);
+    load_ring(128);
   }
   __syncthreads();
+  if (jfirst < jend) carry = band_tile(rrw);
 
   int buf = 0;
   for (int j0 = jfirst; j0 < jend; j0 += NK, buf ^= 1) {
     const bool more = j0 + NK < jend;
-    // band tiles 1 and 2 (rows pb + [32, 96)): initial accumulators and
-    // operands, issued before the K/V prefetch (loads complete in order), so
-    // the score MFMAs below cover their latency
-    floatx16 bd1 = band_init(pb + 32), bd2 = band_init(pb + 64);
-    bf16x8 pf[2][NS];
-    {
-      const bf16* r1 = band_ptr(pb + 32);
-      const bf16* r2 = band_ptr(pb + 64);
-#pragma unroll
-      for (int st = 0; st < NS; ++st) {
-        pf[0][st] = *reinterpret_cast<const bf16x8*>(r1 + 16 * st);
-        pf[1][st] = *reinterpret_cast<const bf16x8*>(r2 + 16 * st);
-      }
-    }
-    if (more) fetch(j0 + NK);
+    // the next key tile and its 64 new ring rows (last read before the
+    // previous barrier; awaited at the next one). The last tile reloads
+    // itself, unused, so that every iteration issues the same loads.
+    load_tile(more ? j0 + NK : j0, buf ^ 1);
+    load_ring(rrw + 32 * w + 96);
 
     // S = K . q_u: output row m of block u is key 32u + swap23(m)
     const char* Ks = smem + C::K_OFF + buf * C::KBUF;
     floatx16 s[2] = {floatx16{}, floatx16{}};
 #pragma unroll
-    for (int st = 0; st < NS; ++st) {
-      const int cb = 32 * st + 16 * hh;  // byte offset of this lane's 8 d_k values
+    for (int st = 0; st < NS; ++st)
 #pragma unroll
       for (int u = 0; u < 2; ++u)
-        s[u] = mma32(*reinterpret_cast<const bf16x8*>(Ks + (32 * u + c) * C::KP + cb), qu[st], s[u]);
-    }
-#pragma unroll
-    for (int st = 0; st < NS; ++st) {
-      bd1 = mma32(pf[0][st], qu[st], bd1);
-      bd2 = mma32(pf[1][st], qu[st], bd2);
-    }
+        s[u] = mma32(*reinterpret_cast<const bf16x8*>(Ks + 32 * u * RB + lo[st]), qu[st], s[u]);
+    const floatx16 bd1 = band_tile(rrw + 32), bd2 = band_tile(rrw + 64);
 
     // rel_shift: band row n of query column c pairs with key j0 + n - 31 + c.
     {
@@ -520,7 +540,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p) 
         }
     }
     carry = bd2;
-    pb += NK;
+    rrw += NK;
     __builtin_amdgcn_wave_barrier();
 
     // x = q_u k + bd for this lane's keys jl(u, r) = 32u + 16(r / 8) + 8hh + r % 8
@@ -576,7 +596,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p) 
 
     // O^T += V^T P^T over 16-key steps (u, jj): k-slot e of lane (c, hh) is
     // key 32u + 16jj + 8hh + e, register 8jj + e of block u.
-    const char* Vt = smem + C::V_OFF + buf * C::VBUF;
+    const char* Vrow = smem + C::V_OFF + buf * C::VBUF + c * (NK * 2);
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
@@ -584,14 +604,13 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p) 
         bf16x8 pb8;
 #pragma unroll
         for (int e = 0; e < 8; ++e) pb8[e] = (bf16)s[u][8 * jj + e];
-        const int kb = (32 * u + 16 * jj + 8 * hh) * 2;
+        const char* va = Vrow + 16 * ((4 * u + 2 * jj + hh) ^ (c % C::VCN));
 #pragma unroll
         for (int d = 0; d < DK / 32; ++d)
-          o[d] = mma32(*reinterpret_cast<const bf16x8*>(Vt + (32 * d + c) * C::VP + kb), pb8, o[d]);
+          o[d] = mma32(*reinterpret_cast<const bf16x8*>(va + 32 * d * (NK * 2)), pb8, o[d]);
       }
 
-    if (more) stage(buf ^ 1);  // that buffer was last read before the previous barrier
-    __syncthreads();
+    __syncthreads();  // waits for this wave's loads of the next tile first
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
@@ -613,8 +632,10 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p) 
 template <int DK, bool DEBUG>
 hipError_t launch2(const AttnParams& p, int nb, hipStream_t s) {
   using C = Cfg2<DK, 4>;
-  dim3 grid((p.T + C::QB - 1) / C::QB, p.H, nb);
-  hipLaunchKernelGGL((attn_bf16_kernel<DK, 4, DEBUG>), grid, dim3(C::NT), 0, s, p);
+  const int64_t work = (int64_t)(p.T + C::QB - 1) / C::QB * p.H * nb;
+  if (work > (1 << 30)) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((work + 7) / 8 * 8));
+  hipLaunchKernelGGL((attn_bf16_kernel<DK, 4, DEBUG>), grid, dim3(C::NT), 0, s, p, nb);
   return hipGetLastError();
 }
 
@@ -623,24 +644,25 @@ hipError_t dispatch_bf16(const AttnParams& p, int nb, hipStream_t s) {
   return p.dbg_bd ? launch2<DK, true>(p, nb, s) : launch2<DK, false>(p, nb, s);
 }
 
+// One row per DK/8 lanes: each lane takes 8 d_k values, then a lane-group sum.
 template <int DK>
-__global__ void pos_bias_diff_kernel(const AttnParams p, float* out, int64_t ld) {
+__global__ __launch_bounds__(256) void pos_bias_diff_kernel(const AttnParams p, float* out, int64_t ld) {
+  constexpr int LPR = DK / 8, RPB = 256 / LPR;  // lanes per row, rows per block
   const int h = blockIdx.y;
-  const int n = (int)(blockIdx.x * blockDim.x + threadIdx.x) - 4;
-  if (n >= p.p_rows + 4) return;
+  const int sub = threadIdx.x % LPR;
+  const int n = (int)blockIdx.x * RPB + (int)threadIdx.x / LPR - 4;
   float acc = 0.f;
   if (n >= 0 && n < p.p_rows) {
-    const bf16* row = reinterpret_cast<const bf16*>(p.p) + (int64_t)n * p.p_rs + h * DK;
-    const float* bu = p.bias_u + h * DK;
-    const float* bv = p.bias_v + h * DK;
-#pragma unroll 4
-    for (int k = 0; k < DK; k += 8) {
-      const bf16x8 v = *reinterpret_cast<const bf16x8*>(row + k);
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.p) + (int64_t)n * p.p_rs +
+                                                       h * DK + 8 * sub);
+    const float* bu = p.bias_u + h * DK + 8 * sub;
+    const float* bv = p.bias_v + h * DK + 8 * sub;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf((float)v[e], bu[k + e] - bv[k + e], acc);
-    }
+    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf((float)v[e], bu[e] - bv[e], acc);
   }
-  out[(int64_t)h * ld + n + 4] = -acc;
+#pragma unroll
+  for (int m = LPR / 2; m > 0; m >>= 1) acc += __shfl_xor(acc, m, LPR);
+  if (sub == 0 && n < p.p_rows + 4) out[(int64_t)h * ld + n + 4] = -acc;
 }
 
 template <typename T, int DK, int NW, bool DEBUG>
@@ -716,7 +738,8 @@ hipError_t pos_bias_diff(int head_dim, const AttnParams& p, float* out, int64_t 
   if (!p.p || !p.bias_u || !p.bias_v || !out || ld < p.p_rows + 8 || !aligned16(p.p) || p.p_rs % 8 ||
       p.p_rs < (int64_t)p.H * head_dim)
     return hipErrorInvalidValue;
-  const dim3 grid((p.p_rows + 8 + 255) / 256, p.H);
+  const int rpb = 256 / (head_dim / 8);
+  const dim3 grid((p.p_rows + 8 + rpb - 1) / rpb, p.H);
   if (head_dim == 64)
     hipLaunchKernelGGL(pos_bias_diff_kernel<64>, grid, dim3(256), 0, s, p, out, ld);
   else if (head_dim == 128)
