@@ -34,10 +34,16 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-ta
          "-packed-fp32-ops", "-Wall", "-Wno-unused-result"]
 
 
+# The attention kernels feed every MFMA result to vector ALU work (softmax,
+# rel_shift remap), so their accumulators are kept in VGPRs: with the AGPR
+# form the compiler copies them through v_accvgpr_read/write on every tile.
+FILE_FLAGS = {"attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src):
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc()] + FLAGS + ["-I", os.path.join(os.path.dirname(HERE), "include"), "-c",
-                               os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc()] + FLAGS + FILE_FLAGS.get(src, []) + ["-I", os.path.join(os.path.dirname(HERE), "include"), "-c",
+                                                         os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if noise not in l and "(ignoring feature)" not in l)

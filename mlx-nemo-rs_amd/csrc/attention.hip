@@ -384,7 +384,8 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   const int per = (int)gridDim.x / 8;
   const int W = ((int)blockIdx.x % 8) * per + (int)blockIdx.x / 8;
   if (W >= nqb * nb * p.H) return;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hh = lane >> 5, c = lane & 31;
+  const int tid = threadIdx.x, lane = tid & 63, hh = lane >> 5, c = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index (uniform)
   const int bl = (W / nqb) % nb, b = p.b0 + bl, h = W / (nqb * nb);
   const int i0 = (W % nqb) * QB;
   const int iw = i0 + 32 * w;  // first query of this wave
@@ -431,25 +432,50 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   const char* pbase = reinterpret_cast<const char*>(p.p) + h * DK * 2;
   const float* pdh = p.pdiff + (int64_t)h * p.pdiff_ld + 4;  // row n at pdh[n], n in [-4, p_rows + 4)
 
-  // Direct-to-LDS loads of key tile j0 into buffer buf: this wave's share of
-  // the K and V^T chunks. Keys past the last one read the last row (masked).
+  // Direct-to-LDS loads. Each lane's byte offsets from a per-tile base are
+  // loop-invariant; the bases are uniform, so the loads take a scalar base and
+  // a 32-bit lane offset. Load g of this wave fills LDS chunks 64g' + [0, 64)
+  // of its buffer, g' = w * (loads per wave) + g.
+  uint32_t koff[C::KDMA], voff[C::VDMA], roff[C::PDMA];
+#pragma unroll
+  for (int g = 0; g < C::KDMA; ++g) {
+    const int pos = (w * C::KDMA + g) * 64 + lane, m = pos / C::KCN;
+    koff[g] = (uint32_t)(swap23(m) * p.kv_rs * 2 + 16 * ((pos % C::KCN) ^ (m % C::KCN)));
+  }
+#pragma unroll
+  for (int g = 0; g < C::VDMA; ++g) {
+    const int pos = (w * C::VDMA + g) * 64 + lane, d = pos / C::VCN;
+    voff[g] = (uint32_t)(d * p.vt_ld * 2 + 16 * ((pos % C::VCN) ^ (d % C::VCN)));
+  }
+#pragma unroll
+  for (int g = 0; g < C::PDMA; ++g) {
+    const int lr = (w * C::PDMA + g) * C::RPL + lane / C::KCN;  // ring row - rr0
+    roff[g] = (uint32_t)(lr * p.p_rs * 2 + 16 * ((lane % C::KCN) ^ (lr % C::KCN)));
+  }
+
+  // Key tile j0 into buffer buf. Keys past the last one read the last row
+  // (their scores are masked).
   auto load_tile = [&](int j0, int buf) {
     char* Ks = smem + C::K_OFF + buf * C::KBUF;
     char* Vt = smem + C::V_OFF + buf * C::VBUF;
+    if (j0 + NK <= p.L) {
+      const char* kt = kbase + (int64_t)j0 * p.kv_rs * 2;
 #pragma unroll
-    for (int g = 0; g < C::KDMA; ++g) {
-      const int pos = (w * C::KDMA + g) * 64 + lane;
-      const int m = pos / C::KCN, q = pos % C::KCN;
-      const char* src = kbase + (int64_t)min(j0 + swap23(m), p.L - 1) * p.kv_rs * 2 + 16 * (q ^ (m % C::KCN));
-      __builtin_amdgcn_global_load_lds(src, (lds_void*)(Ks + (w * C::KDMA + g) * 1024), 16, 0, 0);
-    }
+      for (int g = 0; g < C::KDMA; ++g)
+        __builtin_amdgcn_global_load_lds(kt + (int64_t)koff[g], (lds_void*)(Ks + (w * C::KDMA + g) * 1024), 16, 0, 0);
+    } else {
 #pragma unroll
-    for (int g = 0; g < C::VDMA; ++g) {
-      const int pos = (w * C::VDMA + g) * 64 + lane;
-      const int d = pos / C::VCN, q = pos % C::VCN;
-      const char* src = vtbase + (int64_t)d * p.vt_ld * 2 + (int64_t)j0 * 2 + 16 * (q ^ (d % C::VCN));
-      __builtin_amdgcn_global_load_lds(src, (lds_void*)(Vt + (w * C::VDMA + g) * 1024), 16, 0, 0);
+      for (int g = 0; g < C::KDMA; ++g) {
+        const int pos = (w * C::KDMA + g) * 64 + lane, m = pos / C::KCN;
+        const char* src = kbase + (int64_t)min(j0 + swap23(m), p.L - 1) * p.kv_rs * 2 +
+                          16 * ((pos % C::KCN) ^ (m % C::KCN));
+        __builtin_amdgcn_global_load_lds(src, (lds_void*)(Ks + (w * C::KDMA + g) * 1024), 16, 0, 0);
+      }
     }
+    const char* vt = vtbase + (int64_t)j0 * 2;
+#pragma unroll
+    for (int g = 0; g < C::VDMA; ++g)
+      __builtin_amdgcn_global_load_lds(vt + (int64_t)voff[g], (lds_void*)(Vt + (w * C::VDMA + g) * 1024), 16, 0, 0);
   };
   // Ring rows [rr0, rr0 + 64) (rr0 a multiple of 64): this wave's share of
   // the position rows, and (wave 0) their offsets. Rows outside the table are
@@ -459,16 +485,27 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   // finite values it reads cannot reach the output.
   auto load_ring = [&](int rr0) {
     char* ring = smem + C::P_OFF;
+    const int n0 = R0 + rr0;
+    if (n0 >= 0 && n0 + 64 <= p.p_rows) {
+      const char* pt = pbase + (int64_t)n0 * p.p_rs * 2;
 #pragma unroll
-    for (int g = 0; g < C::PDMA; ++g) {
-      const int rr = rr0 + (w * C::PDMA + g) * C::RPL + lane / C::KCN, q = lane % C::KCN;
-      const int n = min(max(R0 + rr, 0), p.p_rows - 1);
-      const char* src = pbase + (int64_t)n * p.p_rs * 2 + 16 * (q ^ (rr % C::KCN));
-      __builtin_amdgcn_global_load_lds(src, (lds_void*)(ring + ((rr0 + (w * C::PDMA + g) * C::RPL) % C::RING) * RB),
-                                       16, 0, 0);
+      for (int g = 0; g < C::PDMA; ++g)
+        __builtin_amdgcn_global_load_lds(pt + (int64_t)roff[g],
+                                         (lds_void*)(ring + ((rr0 + (w * C::PDMA + g) * C::RPL) % C::RING) * RB),
+                                         16, 0, 0);
+    } else {
+#pragma unroll
+      for (int g = 0; g < C::PDMA; ++g) {
+        const int lr = (w * C::PDMA + g) * C::RPL + lane / C::KCN;
+        const int n = min(max(n0 + lr, 0), p.p_rows - 1);
+        const char* src = pbase + (int64_t)n * p.p_rs * 2 + 16 * ((lane % C::KCN) ^ (lr % C::KCN));
+        __builtin_amdgcn_global_load_lds(src,
+                                         (lds_void*)(ring + ((rr0 + (w * C::PDMA + g) * C::RPL) % C::RING) * RB),
+                                         16, 0, 0);
+      }
     }
     if (w == 0) {
-      const int n = min(max(R0 + rr0 + lane, -4), p.p_rows + 3);
+      const int n = min(max(n0 + lane, -4), p.p_rows + 3);
       __builtin_amdgcn_global_load_lds(pdh + n, (lds_void*)(smem + C::D_OFF + (rr0 % C::RING) * 4), 4, 0, 0);
     }
   };
