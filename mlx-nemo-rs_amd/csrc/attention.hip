@@ -20,6 +20,8 @@
 // Scores stay in fp32 registers; probabilities are rounded to the compute
 // dtype for the PV MFMA. Key tiles that no query of the block can see are
 // skipped, so a +-w local window costs O(T w) instead of O(T^2).
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -63,12 +65,14 @@ __device__ __forceinline__ int key_row(const AttnParams& p, int j) {
   return p.ring_len ? (p.ring_head + j) % p.ring_len : j;
 }
 
-// Keys [jbeg, jend) that can be visible to some query in [i0, i_end).
-__device__ __forceinline__ void key_range(const AttnParams& p, int bl, int i0, int i_end, int& jbeg,
-                                          int& jend) {
-  const int row_end = min(i_end, p.q_valid[bl]);
-  jbeg = max(p.key_lo[bl], 0);
-  jend = min(p.key_hi[bl], p.L);
+// Keys [jbeg, jend) that can be visible to some query in [i0, i_end)
+// (also evaluated on the host to size the bf16 kernel's position slack).
+__host__ __device__ inline int imin(int a, int b) { return a < b ? a : b; }
+__host__ __device__ inline int imax(int a, int b) { return a > b ? a : b; }
+__host__ __device__ inline void key_range(const AttnParams& p, int bl, int i0, int i_end, int& jbeg, int& jend) {
+  const int row_end = imin(i_end, p.q_valid[bl]);
+  jbeg = imax(p.key_lo[bl], 0);
+  jend = imin(p.key_hi[bl], p.L);
   if (row_end <= i0) {
     jend = jbeg;
     return;
@@ -79,11 +83,11 @@ __device__ __forceinline__ void key_range(const AttnParams& p, int bl, int i0, i
     const int chunk = p.right + 1;
     const int lc = p.left >= 0 ? p.left / chunk : 10000;
     const long lo = ((long)(a0 / chunk) - lc) * chunk;
-    jbeg = max(jbeg, (int)max(lo, 0L));
-    jend = min(jend, (a1 / chunk + 1) * chunk);
+    jbeg = imax(jbeg, (int)(lo > 0 ? lo : 0));
+    jend = imin(jend, (a1 / chunk + 1) * chunk);
   } else {
-    if (p.left >= 0) jbeg = max(jbeg, a0 - p.left);
-    if (!p.chunked && p.right >= 0) jend = min(jend, a1 + p.right + 1);
+    if (p.left >= 0) jbeg = imax(jbeg, a0 - p.left);
+    if (!p.chunked && p.right >= 0) jend = imin(jend, a1 + p.right + 1);
   }
 }
 
@@ -430,7 +434,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   const char* kbase = reinterpret_cast<const char*>(p.k) + ((int64_t)b * p.kv_bs + h * DK) * 2;
   const char* vtbase = reinterpret_cast<const char*>(p.vt) + ((int64_t)h * DK * p.vt_ld + (int64_t)b * p.vt_bs) * 2;
   const char* pbase = reinterpret_cast<const char*>(p.p) + h * DK * 2;
-  const float* pdh = p.pdiff + (int64_t)h * p.pdiff_ld + 4;  // row n at pdh[n], n in [-4, p_rows + 4)
+  const float* pdh = p.pdiff + (int64_t)h * p.pdiff_ld + p.p_pad;  // row n at pdh[n], |n| within the pad
 
   // Direct-to-LDS loads. Each lane's byte offsets from a per-tile base are
   // loop-invariant; the bases are uniform, so the loads take a scalar base and
@@ -453,61 +457,37 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
     roff[g] = (uint32_t)(lr * p.p_rs * 2 + 16 * ((lane % C::KCN) ^ (lr % C::KCN)));
   }
 
-  // Key tile j0 into buffer buf. Keys past the last one read the last row
-  // (their scores are masked).
+  // Key tile j0 into buffer buf. Rows past the item's last key belong to the
+  // next item or to the kv_pad slack after the last one: finite, and masked.
   auto load_tile = [&](int j0, int buf) {
     char* Ks = smem + C::K_OFF + buf * C::KBUF;
     char* Vt = smem + C::V_OFF + buf * C::VBUF;
-    if (j0 + NK <= p.L) {
-      const char* kt = kbase + (int64_t)j0 * p.kv_rs * 2;
+    const char* kt = kbase + (int64_t)j0 * p.kv_rs * 2;
 #pragma unroll
-      for (int g = 0; g < C::KDMA; ++g)
-        __builtin_amdgcn_global_load_lds(kt + (int64_t)koff[g], (lds_void*)(Ks + (w * C::KDMA + g) * 1024), 16, 0, 0);
-    } else {
-#pragma unroll
-      for (int g = 0; g < C::KDMA; ++g) {
-        const int pos = (w * C::KDMA + g) * 64 + lane, m = pos / C::KCN;
-        const char* src = kbase + (int64_t)min(j0 + swap23(m), p.L - 1) * p.kv_rs * 2 +
-                          16 * ((pos % C::KCN) ^ (m % C::KCN));
-        __builtin_amdgcn_global_load_lds(src, (lds_void*)(Ks + (w * C::KDMA + g) * 1024), 16, 0, 0);
-      }
-    }
+    for (int g = 0; g < C::KDMA; ++g)
+      __builtin_amdgcn_global_load_lds(kt + (int64_t)koff[g], (lds_void*)(Ks + (w * C::KDMA + g) * 1024), 16, 0, 0);
     const char* vt = vtbase + (int64_t)j0 * 2;
 #pragma unroll
     for (int g = 0; g < C::VDMA; ++g)
       __builtin_amdgcn_global_load_lds(vt + (int64_t)voff[g], (lds_void*)(Vt + (w * C::VDMA + g) * 1024), 16, 0, 0);
   };
   // Ring rows [rr0, rr0 + 64) (rr0 a multiple of 64): this wave's share of
-  // the position rows, and (wave 0) their offsets. Rows outside the table are
-  // clamped into it (offsets: into the zero pad rows). Every pair reading such
-  // a row lies outside its query's interval (past the last key or query, or
-  // beyond a window the table was checked to cover), so it is masked, and the
-  // finite values it reads cannot reach the output.
+  // the position rows, and (wave 0) their offsets. Rows outside the table
+  // read the p_pad slack around it (finite; the offsets there are zero).
+  // Every pair reading such a row lies outside its query's interval (past the
+  // last key or query, or beyond a window the table was checked to cover), so
+  // it is masked, and the values it reads cannot reach the output.
   auto load_ring = [&](int rr0) {
     char* ring = smem + C::P_OFF;
     const int n0 = R0 + rr0;
-    if (n0 >= 0 && n0 + 64 <= p.p_rows) {
-      const char* pt = pbase + (int64_t)n0 * p.p_rs * 2;
+    const char* pt = pbase + (int64_t)n0 * p.p_rs * 2;
 #pragma unroll
-      for (int g = 0; g < C::PDMA; ++g)
-        __builtin_amdgcn_global_load_lds(pt + (int64_t)roff[g],
-                                         (lds_void*)(ring + ((rr0 + (w * C::PDMA + g) * C::RPL) % C::RING) * RB),
-                                         16, 0, 0);
-    } else {
-#pragma unroll
-      for (int g = 0; g < C::PDMA; ++g) {
-        const int lr = (w * C::PDMA + g) * C::RPL + lane / C::KCN;
-        const int n = min(max(n0 + lr, 0), p.p_rows - 1);
-        const char* src = pbase + (int64_t)n * p.p_rs * 2 + 16 * ((lane % C::KCN) ^ (lr % C::KCN));
-        __builtin_amdgcn_global_load_lds(src,
-                                         (lds_void*)(ring + ((rr0 + (w * C::PDMA + g) * C::RPL) % C::RING) * RB),
-                                         16, 0, 0);
-      }
-    }
-    if (w == 0) {
-      const int n = min(max(n0 + lane, -4), p.p_rows + 3);
-      __builtin_amdgcn_global_load_lds(pdh + n, (lds_void*)(smem + C::D_OFF + (rr0 % C::RING) * 4), 4, 0, 0);
-    }
+    for (int g = 0; g < C::PDMA; ++g)
+      __builtin_amdgcn_global_load_lds(pt + (int64_t)roff[g],
+                                       (lds_void*)(ring + ((rr0 + (w * C::PDMA + g) * C::RPL) % C::RING) * RB), 16,
+                                       0, 0);
+    if (w == 0)
+      __builtin_amdgcn_global_load_lds(pdh + n0 + lane, (lds_void*)(smem + C::D_OFF + (rr0 % C::RING) * 4), 4, 0, 0);
   };
 
   // This lane's byte offset of the 16-byte chunk 2st + hh of row c in a
@@ -517,7 +497,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   for (int st = 0; st < NS; ++st) lo[st] = c * RB + 16 * ((2 * st + hh) ^ (c % C::KCN));
   // Band tile of 32 ring rows from rr (a multiple of 32): initial accumulator
   // (row rr + 8a + 4hh + e in register 4a + e) and MFMAs.
-  auto band_tile = [&](int rr) {
+  auto band_init = [&](int rr) {
     const float* dr = reinterpret_cast<const float*>(smem + C::D_OFF) + (rr % C::RING) + 4 * hh;
     floatx16 acc;
 #pragma unroll
@@ -526,15 +506,33 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 #pragma unroll
       for (int e = 0; e < 4; ++e) acc[4 * a + e] = v[e];
     }
+    return acc;
+  };
+  auto band_tile = [&](int rr) {
+    floatx16 acc = band_init(rr);
     const char* rb = smem + C::P_OFF + (rr % C::RING) * RB;
 #pragma unroll
     for (int st = 0; st < NS; ++st) acc = mma32(*reinterpret_cast<const bf16x8*>(rb + lo[st]), qu[st], acc);
     return acc;
   };
 
+  // Band tile t of the current key tile goes to remap strip columns
+  // 32t + [0, 32), rounded to bf16 (this lane: rows 8a + 4hh + [0, 4)).
+  auto pack = [&](const floatx16& bt) {
+    bf16x16 v;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = (bf16)bt[i];
+    return v;
+  };
+  auto put = [&](const bf16x16& v, int t) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+      *reinterpret_cast<bf16x4*>(Rm + 32 * t + 8 * a + 4 * hh) = bf16x4{v[4 * a], v[4 * a + 1], v[4 * a + 2], v[4 * a + 3]};
+  };
+
   // ring row of band tile 0 of this wave for key tile k: 64k + 96 - 32w
   int rrw = 96 - 32 * w;
-  floatx16 carry = floatx16{};
+  bf16x16 carry = bf16x16{};  // band tile 0 of the current key tile, as stored
   if (jfirst < jend) {
     load_tile(jfirst, 0);
     load_ring(0);
@@ -542,7 +540,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
     load_ring(128);
   }
   __syncthreads();
-  if (jfirst < jend) carry = band_tile(rrw);
+  if (jfirst < jend) carry = pack(band_tile(rrw));
 
   int buf = 0;
   for (int j0 = jfirst; j0 < jend; j0 += NK, buf ^= 1) {
@@ -553,6 +551,26 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
     load_tile(more ? j0 + NK : j0, buf ^ 1);
     load_ring(rrw + 32 * w + 96);
 
+    // Band tiles first, each stored to the remap strip as soon as it is
+    // done (rel_shift: strip column n of query column c pairs with key
+    // j0 + n - 31 + c), so few accumulators are live at once.
+    put(carry, 0);
+    {
+      // band tiles 1 and 2 as two interleaved MFMA chains
+      floatx16 b1 = band_init(rrw + 32), b2 = band_init(rrw + 64);
+      const char* r1 = smem + C::P_OFF + ((rrw + 32) % C::RING) * RB;
+      const char* r2 = smem + C::P_OFF + ((rrw + 64) % C::RING) * RB;
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+        b1 = mma32(*reinterpret_cast<const bf16x8*>(r1 + lo[st]), qu[st], b1);
+        b2 = mma32(*reinterpret_cast<const bf16x8*>(r2 + lo[st]), qu[st], b2);
+      }
+      put(pack(b1), 1);
+      carry = pack(b2);
+      put(carry, 2);
+    }
+    rrw += NK;
+
     // S = K . q_u: output row m of block u is key 32u + swap23(m)
     const char* Ks = smem + C::K_OFF + buf * C::KBUF;
     floatx16 s[2] = {floatx16{}, floatx16{}};
@@ -561,23 +579,6 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 #pragma unroll
       for (int u = 0; u < 2; ++u)
         s[u] = mma32(*reinterpret_cast<const bf16x8*>(Ks + 32 * u * RB + lo[st]), qu[st], s[u]);
-    const floatx16 bd1 = band_tile(rrw + 32), bd2 = band_tile(rrw + 64);
-
-    // rel_shift: band row n of query column c pairs with key j0 + n - 31 + c.
-    {
-      const floatx16 bt[3] = {carry, bd1, bd2};
-#pragma unroll
-      for (int t = 0; t < 3; ++t)
-#pragma unroll
-        for (int a = 0; a < 4; ++a) {
-          bf16x4 v4;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v4[e] = (bf16)bt[t][4 * a + e];
-          *reinterpret_cast<bf16x4*>(Rm + 32 * t + 8 * a + 4 * hh) = v4;
-        }
-    }
-    carry = bd2;
-    rrw += NK;
     __builtin_amdgcn_wave_barrier();
 
     // x = q_u k + bd for this lane's keys jl(u, r) = 32u + 16(r / 8) + 8hh + r % 8
@@ -596,13 +597,17 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
       }
     __builtin_amdgcn_wave_barrier();
     if (!__all(iv.x <= j0 && iv.y >= j0 + NK)) {  // some key of the tile is hidden from some query
+      // key j = j0 + 8hh + jl(u, r) is visible iff j - lo < hi - lo (unsigned);
+      // the opaque base keeps the 32 per-lane offsets from being hoisted out
+      // of the loop into registers
+      int jb = j0 + 8 * hh - iv.x;
+      asm volatile("" : "+v"(jb));
+      const unsigned span = (unsigned)(iv.y - iv.x);
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int j = j0 + 32 * u + 16 * (r >> 3) + 8 * hh + (r & 7);
-          if (!in_interval(j, iv)) s[u][r] = -INFINITY;
-        }
+        for (int r = 0; r < 16; ++r)
+          if ((unsigned)(jb + 32 * u + 16 * (r >> 3) + (r & 7)) >= span) s[u][r] = -INFINITY;
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u)
@@ -687,7 +692,7 @@ __global__ __launch_bounds__(256) void pos_bias_diff_kernel(const AttnParams p, 
   constexpr int LPR = DK / 8, RPB = 256 / LPR;  // lanes per row, rows per block
   const int h = blockIdx.y;
   const int sub = threadIdx.x % LPR;
-  const int n = (int)blockIdx.x * RPB + (int)threadIdx.x / LPR - 4;
+  const int n = (int)blockIdx.x * RPB + (int)threadIdx.x / LPR - p.p_pad;
   float acc = 0.f;
   if (n >= 0 && n < p.p_rows) {
     const bf16x8 v = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.p) + (int64_t)n * p.p_rs +
@@ -699,7 +704,7 @@ __global__ __launch_bounds__(256) void pos_bias_diff_kernel(const AttnParams p, 
   }
 #pragma unroll
   for (int m = LPR / 2; m > 0; m >>= 1) acc += __shfl_xor(acc, m, LPR);
-  if (sub == 0 && n < p.p_rows + 4) out[(int64_t)h * ld + n + 4] = -acc;
+  if (sub == 0 && n < p.p_rows + p.p_pad) out[(int64_t)h * ld + n + p.p_pad] = -acc;
 }
 
 template <typename T, int DK, int NW, bool DEBUG>
@@ -740,6 +745,26 @@ __global__ void pos_index_kernel(int T, int L, int qoff, int center, int32_t* ou
 
 }  // namespace
 
+int bf16_pos_pad(const AttnParams& p, int nb) {
+  constexpr int QB = Cfg2<128, 4>::QB, NK = Cfg2<128, 4>::NK;
+  static_assert(Cfg2<64, 4>::QB == QB, "one query block size");
+  int need = 0;
+  const int nqb = (p.T + QB - 1) / QB;
+  for (int bl = 0; bl < nb; ++bl)
+    for (int qb = 0; qb < nqb; ++qb) {
+      const int i0 = qb * QB;
+      int jbeg, jend;
+      key_range(p, bl, i0, imin(i0 + QB, p.T), jbeg, jend);
+      const int jfirst = jbeg / NK * NK;
+      if (jfirst >= jend) continue;
+      // the kernel reads ring rows rr in [0, 64 * tiles + 192): position rows R0 + rr
+      const int64_t R0 = (int64_t)p.center - p.qoff - (i0 + 31) + jfirst - 96;
+      const int64_t hi = R0 + (int64_t)(jend - jfirst + NK - 1) / NK * NK + 192;
+      need = (int)std::max<int64_t>(need, std::max<int64_t>(-R0, hi - p.p_rows));
+    }
+  return need;
+}
+
 hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStream_t s) {
   if (nb <= 0 || p.T <= 0) return hipSuccess;
   if (nb > kMaxBatch || p.L <= 0 || p.H <= 0 || p.p_rows <= 0) return hipErrorInvalidValue;
@@ -754,7 +779,8 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
   if (p.vt) {
     // V^T columns of each batch are read in whole 64-key tiles
     if (dt != kBF16 || p.ring_len || !aligned16(p.vt) || p.vt_ld % 8 || p.vt_bs % 64 || p.vt_bs < p.T ||
-        p.vt_ld < (int64_t)(p.b0 + nb) * p.vt_bs || p.L != p.T || !p.pdiff || p.pdiff_ld < p.p_rows + 8)
+        p.vt_ld < (int64_t)(p.b0 + nb) * p.vt_bs || p.L != p.T || !p.pdiff ||
+        p.pdiff_ld < p.p_rows + 2 * (int64_t)p.p_pad || p.kv_pad < 63 || p.p_pad < bf16_pos_pad(p, nb))
       return hipErrorInvalidValue;
     if (head_dim == 64) return dispatch_bf16<64>(p, nb, s);
     if (head_dim == 128) return dispatch_bf16<128>(p, nb, s);
@@ -772,11 +798,11 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
 
 hipError_t pos_bias_diff(int head_dim, const AttnParams& p, float* out, int64_t ld, hipStream_t s) {
   if (p.p_rows <= 0 || p.H <= 0) return hipSuccess;
-  if (!p.p || !p.bias_u || !p.bias_v || !out || ld < p.p_rows + 8 || !aligned16(p.p) || p.p_rs % 8 ||
-      p.p_rs < (int64_t)p.H * head_dim)
+  if (!p.p || !p.bias_u || !p.bias_v || !out || p.p_pad < 0 || ld < p.p_rows + 2 * (int64_t)p.p_pad ||
+      !aligned16(p.p) || p.p_rs % 8 || p.p_rs < (int64_t)p.H * head_dim)
     return hipErrorInvalidValue;
   const int rpb = 256 / (head_dim / 8);
-  const dim3 grid((p.p_rows + 8 + rpb - 1) / rpb, p.H);
+  const dim3 grid((p.p_rows + 2 * p.p_pad + rpb - 1) / rpb, p.H);
   if (head_dim == 64)
     hipLaunchKernelGGL(pos_bias_diff_kernel<64>, grid, dim3(256), 0, s, p, out, ld);
   else if (head_dim == 128)

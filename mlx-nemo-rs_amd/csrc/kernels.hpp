@@ -77,9 +77,13 @@ struct AttnParams {
   const void* vt = nullptr;
   int64_t vt_ld = 0, vt_bs = 0;
   // bf16 path: -(bias_u - bias_v) . P[n] per head ([H][pdiff_ld] fp32, row n
-  // at column n + 4, four zero rows on each side), from pos_bias_diff
+  // at column n + p_pad, zero on the pad rows), from pos_bias_diff
   const float* pdiff = nullptr;
   int64_t pdiff_ld = 0;
+  // bf16 path: rows readable (finite) around the position table, p_pad
+  // before row 0 and after row p_rows - 1 (at least bf16_pos_pad), and past
+  // the last key row of the last item (at least 63)
+  int p_pad = 0, kv_pad = 0;
   int T = 0, L = 0, qoff = 0, H = 0;
   float scale = 0.f, scale_bd = 0.f;
   int has_ctx = 0, left = -1, right = -1, chunked = 0;
@@ -89,9 +93,12 @@ struct AttnParams {
   int q_valid[kMaxBatch];
 };
 hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nbatch, hipStream_t s);
-// The bf16 kernel's position-term offset: out[h][n + 4] = -(bias_u[h] - bias_v[h]) . P[n, h]
-// for n in [0, p_rows), zero for the four pad rows on each side (ld >= p_rows + 8).
+// The bf16 kernel's position-term offset: out[h][n + p_pad] = -(bias_u[h] - bias_v[h]) . P[n, h]
+// for n in [0, p_rows), zero for the p_pad rows on each side (ld >= p_rows + 2 p_pad).
 hipError_t pos_bias_diff(int head_dim, const AttnParams& p, float* out, int64_t ld, hipStream_t s);
+// Position rows the bf16 kernel reads beyond the table on either side for
+// these items' key ranges (key_lo / key_hi / q_valid, context, T, center).
+int bf16_pos_pad(const AttnParams& p, int nbatch);
 
 // Visibility map [nbatch, T, L] (1 = visible) from the same predicate the
 // attention kernel applies.
@@ -109,6 +116,9 @@ hipError_t ring_write(DType dt, const void* src, void* ring, int B, int n, int D
                       int off, hipStream_t s);
 hipError_t ring_read(DType dt, const void* ring, void* dst, int B, int n, int D, int R, int64_t ld,
                      int off, hipStream_t s);
+
+// Zero-fill of device memory by a kernel (no memset node under graph capture).
+hipError_t fill_zero(void* ptr, size_t bytes, hipStream_t s);
 
 // Dequantised weight [N, K] as the GEMM's loader produces it, widened to fp32.
 hipError_t dequant_export(DType dt, const uint32_t* w, const float* sb, float* out, int N, int K,

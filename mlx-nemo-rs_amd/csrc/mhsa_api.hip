@@ -197,6 +197,8 @@ struct mhsa_layer {
   DevBuf gemm_partial;         // K-split partial sums of small GEMMs
   DevBuf vtbuf;                // bf16: transposed V [D][B * Tpad]
   DevBuf hbuf;                 // sublayer: LayerNorm output
+  const char* last_qkv = nullptr;  // where the last offline forward put [q|k|v] rows
+  const char* last_pos = nullptr;  // and its projected position rows (debug export)
   DevBuf ln_dev;               // sublayer: LayerNorm gamma, beta
   std::vector<float> ln_host;  // values currently in ln_dev
   // streaming position memo (attention.rs:749-761)
@@ -482,14 +484,43 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
 
   const int64_t M = (int64_t)B * T;
   const bool use_vt = L->dt == mhsa::kBF16;
-  const int64_t pd_ld = nrows + 8;  // bf16 kernel's position-term offsets, 4 pad rows each side
-  const size_t qkv_b = align_up(M * 3 * D * es, 256), p_b = align_up((int64_t)nrows * D * es, 256),
+  auto key_bounds = [&](int b, int& lo, int& hi, int& qv) {
+    lo = 0;
+    hi = lens ? std::min(std::max(lens[b], 1), T) : T;  // attention.rs:281-285
+    qv = T;
+  };
+  mhsa::AttnParams a;
+  fill_attn_common(L, a);
+  a.T = T;
+  a.L = T;
+  a.qoff = 0;
+  a.p_rows = nrows;
+  a.center = center;
+  set_ctx(a, ctx);
+  // bf16: position rows the kernel may read on either side of the table
+  // (they only meet masked pairs) and key rows past the last item, kept as
+  // finite slack in the workspace
+  int pad = 0;
+  const int kv_pad = use_vt ? 64 : 0;
+  if (use_vt)
+    for (int b0 = 0; b0 < B; b0 += mhsa::kMaxBatch) {
+      const int nb = std::min(mhsa::kMaxBatch, B - b0);
+      for (int i = 0; i < nb; ++i) key_bounds(b0 + i, a.key_lo[i], a.key_hi[i], a.q_valid[i]);
+      pad = std::max(pad, mhsa::bf16_pos_pad(a, nb));
+    }
+  pad = (int)align_up(pad, 8);
+  const int64_t pd_ld = nrows + 2 * (int64_t)pad;
+  const size_t qkv_b = align_up((M + kv_pad) * 3 * D * es, 256), p_b = align_up(pd_ld * D * es, 256),
                ctx_b = align_up(M * D * es, 256), pd_b = use_vt ? align_up(L->H * pd_ld * 4, 256) : 0;
+  const size_t ws_before = L->ws.n;
   HIPCHK(L->ws.ensure(qkv_b + p_b + ctx_b + pd_b));
+  if (L->ws.n != ws_before) HIPCHK(mhsa::fill_zero(L->ws.p, L->ws.n, s));  // slack rows start finite
   char* qkv = static_cast<char*>(L->ws.p);
-  char* P = qkv + qkv_b;
-  char* cx = P + p_b;
+  char* P = qkv + qkv_b + (size_t)pad * D * es;  // table rows [0, nrows) after `pad` slack rows
+  char* cx = qkv + qkv_b + p_b;
   float* pdiff = use_vt ? reinterpret_cast<float*>(cx + ctx_b) : nullptr;
+  L->last_qkv = qkv;
+  L->last_pos = P;
   // bf16: V also transposed per batch, [D][B * Tpad], for the MFMA PV operand;
   // zero-filled on allocation so padding columns are finite
   VtOut vt;
@@ -500,7 +531,7 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
     const size_t bytes = (size_t)D * vt.ld * 2;
     const size_t before = L->vtbuf.n;
     HIPCHK(L->vtbuf.ensure(bytes));
-    if (L->vtbuf.n != before) HIPCHK(hipMemsetAsync(L->vtbuf.p, 0, L->vtbuf.n, s));
+    if (L->vtbuf.n != before) HIPCHK(mhsa::fill_zero(L->vtbuf.p, L->vtbuf.n, s));
     vt.p = L->vtbuf.p;
   }
 
@@ -515,8 +546,6 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
       return rc;
   }
 
-  mhsa::AttnParams a;
-  fill_attn_common(L, a);
   a.q = qkv;
   a.k = qkv + (size_t)D * es;
   a.v = qkv + (size_t)2 * D * es;
@@ -524,8 +553,8 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   a.q_rs = a.kv_rs = 3 * D;
   a.p = P;
   a.p_rs = D;
-  a.p_rows = nrows;
-  a.center = center;
+  a.p_pad = pad;
+  a.kv_pad = kv_pad;
   a.o = cx;
   a.o_bs = (int64_t)T * D;
   a.o_rs = D;
@@ -539,20 +568,9 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
     ProfScope ps(L, "pos_bias_diff", s);
     HIPCHK(mhsa::pos_bias_diff(L->dk, a, pdiff, pd_ld, s));
   }
-  a.T = T;
-  a.L = T;
-  a.qoff = 0;
-  set_ctx(a, ctx);
   {
     ProfScope ps(L, "attention", s);
-    rc = run_attention(
-        L, a, B,
-        [&](int b, int& lo, int& hi, int& qv) {
-          lo = 0;
-          hi = lens ? std::min(std::max(lens[b], 1), T) : T;  // attention.rs:281-285
-          qv = T;
-        },
-        s);
+    rc = run_attention(L, a, B, key_bounds, s);
   }
   if (rc) return rc;
   if (!out) return MHSA_OK;
@@ -1087,13 +1105,11 @@ int32_t mhsa_debug_position_scores(mhsa_layer* L, const void* x, int32_t B, int3
   // position table (all pos_len rows: full attention projects every row)
   const size_t es = esz(L);
   const int64_t M = (int64_t)B * T;
-  const char* qkv = static_cast<const char*>(L->ws.p);
   if (q_out)
-    HIPCHK(hipMemcpy2DAsync(q_out, (size_t)L->D * es, qkv, (size_t)3 * L->D * es, (size_t)L->D * es, (size_t)M,
-                            hipMemcpyDeviceToDevice, s));
+    HIPCHK(hipMemcpy2DAsync(q_out, (size_t)L->D * es, L->last_qkv, (size_t)3 * L->D * es, (size_t)L->D * es,
+                            (size_t)M, hipMemcpyDeviceToDevice, s));
   if (p_out)
-    HIPCHK(hipMemcpyAsync(p_out, qkv + align_up(M * 3 * L->D * es, 256), (size_t)pos_len * L->D * es,
-                          hipMemcpyDeviceToDevice, s));
+    HIPCHK(hipMemcpyAsync(p_out, L->last_pos, (size_t)pos_len * L->D * es, hipMemcpyDeviceToDevice, s));
   HIPCHK(hipStreamSynchronize(s));
   return MHSA_OK;
 }

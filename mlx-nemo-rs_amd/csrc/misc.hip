@@ -2,6 +2,8 @@
 // sublayer (conformer.rs:1749), the streaming cache ring copies
 // (attention.rs:650, 670-684; conformer.rs:983-1016) and the dequantised
 // weight export used by the bit-exact checks.
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "quant.hpp"
@@ -95,7 +97,24 @@ __global__ void dequant_kernel(const uint32_t* w, const float* sb, float* out, i
 
 unsigned grid_for(int64_t n) { return (unsigned)std::min<int64_t>(std::max<int64_t>((n + 255) / 256, 1), 8192); }
 
+__global__ void zero_kernel(u32x4* p, int64_t n16, uint8_t* tail, int ntail) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = u32x4{0u, 0u, 0u, 0u};
+  if (blockIdx.x == 0 && (int)threadIdx.x < ntail) tail[threadIdx.x] = 0;
+}
+
 }  // namespace
+
+hipError_t fill_zero(void* ptr, size_t bytes, hipStream_t s) {
+  if (!bytes) return hipSuccess;
+  if (!ptr || (reinterpret_cast<uintptr_t>(ptr) & 15)) return hipErrorInvalidValue;
+  const int64_t n16 = (int64_t)(bytes / 16);
+  const int ntail = (int)(bytes % 16);
+  const int64_t blocks = std::min<int64_t>((n16 + 255) / 256 + 1, 4096);
+  hipLaunchKernelGGL(zero_kernel, dim3((unsigned)blocks), dim3(256), 0, s, static_cast<u32x4*>(ptr), n16,
+                     static_cast<uint8_t*>(ptr) + n16 * 16, ntail);
+  return hipGetLastError();
+}
 
 hipError_t layer_norm(DType dt, const void* x, void* y, const float* gamma, const float* beta, float eps, int rows,
                       int D, hipStream_t s) {
