@@ -418,15 +418,13 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   }
 
   floatx16 o[DK / 32];
-#pragma unroll
-  for (int d = 0; d < DK / 32; ++d) o[d] = floatx16{};
-  float m_run = -INFINITY, l_run = 0.f;
+  float l_run;
 
   int jbeg, jend;
   key_range(p, bl, i0, min(i0 + QB, p.T), jbeg, jend);
   const int2 iv = query_interval(p, bl, qi);
   const float sc = p.scale * kLog2e;
-  const float thr = 8.f / sc;  // lazy rescale threshold (2^8 in probability)
+  const float lim = 100.f / sc;  // largest (score - reference) kept in one pass: 2^100
   const int jfirst = (jbeg / NK) * NK;
   // ring row rr holds position row R0 + rr
   const int R0 = p.center - p.qoff - (i0 + 31) + jfirst - 96;
@@ -436,25 +434,39 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   const char* pbase = reinterpret_cast<const char*>(p.p) + h * DK * 2;
   const float* pdh = p.pdiff + (int64_t)h * p.pdiff_ld + p.p_pad;  // row n at pdh[n], |n| within the pad
 
-  // Direct-to-LDS loads. Each lane's byte offsets from a per-tile base are
-  // loop-invariant; the bases are uniform, so the loads take a scalar base and
-  // a 32-bit lane offset. Load g of this wave fills LDS chunks 64g' + [0, 64)
-  // of its buffer, g' = w * (loads per wave) + g.
-  uint32_t koff[C::KDMA], voff[C::VDMA], roff[C::PDMA];
+  // Direct-to-LDS loads (buffer_load ... lds): each stream has a buffer
+  // resource over its readable range, a uniform per-tile offset (soffset) and
+  // a loop-invariant 32-bit offset per lane. Load g of this wave fills LDS
+  // chunks 64g' + [0, 64) of its buffer, g' = w * (loads per wave) + g. Bytes
+  // past a resource's range read as zero.
+  constexpr int kRawBuffer = 0x00020000;  // descriptor dword 3: untyped 32-bit data
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)kbase, (short)0, (int)((int64_t)(p.T + p.kv_pad) * p.kv_rs * 2 - h * DK * 2), kRawBuffer);
+  const __amdgpu_buffer_rsrc_t rv =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vtbase, (short)0, (int)((int64_t)DK * p.vt_ld * 2), kRawBuffer);
+  const char* pslack = pbase - (int64_t)p.p_pad * p.p_rs * 2;  // first readable position row
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)pslack, (short)0, (int)((int64_t)(p.p_rows + 2 * p.p_pad) * p.p_rs * 2 - h * DK * 2), kRawBuffer);
+  const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)(pdh - p.p_pad), (short)0, (int)((int64_t)(p.p_rows + 2 * p.p_pad) * 4), kRawBuffer);
+  // (passed to the builtins as (int) prvalues: an argument naming a variable
+  // the lambda captured by reference makes the host compilation pass drop
+  // the kernel's launch stub)
+  int koff[C::KDMA], voff[C::VDMA], roff[C::PDMA];
 #pragma unroll
   for (int g = 0; g < C::KDMA; ++g) {
     const int pos = (w * C::KDMA + g) * 64 + lane, m = pos / C::KCN;
-    koff[g] = (uint32_t)(swap23(m) * p.kv_rs * 2 + 16 * ((pos % C::KCN) ^ (m % C::KCN)));
+    koff[g] = (int)(swap23(m) * p.kv_rs * 2 + 16 * ((pos % C::KCN) ^ (m % C::KCN)));
   }
 #pragma unroll
   for (int g = 0; g < C::VDMA; ++g) {
     const int pos = (w * C::VDMA + g) * 64 + lane, d = pos / C::VCN;
-    voff[g] = (uint32_t)(d * p.vt_ld * 2 + 16 * ((pos % C::VCN) ^ (d % C::VCN)));
+    voff[g] = (int)(d * p.vt_ld * 2 + 16 * ((pos % C::VCN) ^ (d % C::VCN)));
   }
 #pragma unroll
   for (int g = 0; g < C::PDMA; ++g) {
     const int lr = (w * C::PDMA + g) * C::RPL + lane / C::KCN;  // ring row - rr0
-    roff[g] = (uint32_t)(lr * p.p_rs * 2 + 16 * ((lane % C::KCN) ^ (lr % C::KCN)));
+    roff[g] = (int)(lr * p.p_rs * 2 + 16 * ((lane % C::KCN) ^ (lr % C::KCN)));
   }
 
   // Key tile j0 into buffer buf. Rows past the item's last key belong to the
@@ -462,14 +474,14 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   auto load_tile = [&](int j0, int buf) {
     char* Ks = smem + C::K_OFF + buf * C::KBUF;
     char* Vt = smem + C::V_OFF + buf * C::VBUF;
-    const char* kt = kbase + (int64_t)j0 * p.kv_rs * 2;
+    const int ks = j0 * (int)p.kv_rs * 2;
 #pragma unroll
     for (int g = 0; g < C::KDMA; ++g)
-      __builtin_amdgcn_global_load_lds(kt + (int64_t)koff[g], (lds_void*)(Ks + (w * C::KDMA + g) * 1024), 16, 0, 0);
-    const char* vt = vtbase + (int64_t)j0 * 2;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(Ks + (w * C::KDMA + g) * 1024), 16, (int)koff[g], ks, 0, 0);
 #pragma unroll
     for (int g = 0; g < C::VDMA; ++g)
-      __builtin_amdgcn_global_load_lds(vt + (int64_t)voff[g], (lds_void*)(Vt + (w * C::VDMA + g) * 1024), 16, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(Vt + (w * C::VDMA + g) * 1024), 16, (int)voff[g], j0 * 2, 0,
+                                               0);
   };
   // Ring rows [rr0, rr0 + 64) (rr0 a multiple of 64): this wave's share of
   // the position rows, and (wave 0) their offsets. Rows outside the table
@@ -479,15 +491,15 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   // it is masked, and the values it reads cannot reach the output.
   auto load_ring = [&](int rr0) {
     char* ring = smem + C::P_OFF;
-    const int n0 = R0 + rr0;
-    const char* pt = pbase + (int64_t)n0 * p.p_rs * 2;
+    const int n0 = R0 + rr0 + p.p_pad;  // row index from the first readable row
 #pragma unroll
     for (int g = 0; g < C::PDMA; ++g)
-      __builtin_amdgcn_global_load_lds(pt + (int64_t)roff[g],
-                                       (lds_void*)(ring + ((rr0 + (w * C::PDMA + g) * C::RPL) % C::RING) * RB), 16,
-                                       0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rp, (lds_void*)(ring + ((rr0 + (w * C::PDMA + g) * C::RPL) % C::RING) * RB), 16, (int)roff[g],
+          n0 * (int)p.p_rs * 2, 0, 0);
     if (w == 0)
-      __builtin_amdgcn_global_load_lds(pdh + n0 + lane, (lds_void*)(smem + C::D_OFF + (rr0 % C::RING) * 4), 4, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void*)(smem + C::D_OFF + (rr0 % C::RING) * 4), 4, lane * 4,
+                                               n0 * 4, 0, 0);
   };
 
   // This lane's byte offset of the 16-byte chunk 2st + hh of row c in a
@@ -530,6 +542,19 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
       *reinterpret_cast<bf16x4*>(Rm + 32 * t + 8 * a + 4 * hh) = bf16x4{v[4 * a], v[4 * a + 1], v[4 * a + 2], v[4 * a + 3]};
   };
 
+  // Softmax with a fixed reference per query: probabilities are
+  // 2^((x - m_ref) s log2 e), with m_ref the first finite tile maximum of the
+  // query (o and l are still zero until then), so the accumulators are only
+  // ever touched by MFMAs. A later maximum above m_ref makes probabilities
+  // larger than 1; up to 2^100 that stays far from fp32 overflow for any key
+  // count, and beyond it the whole pass is repeated with the true maximum as
+  // the reference. The final division by l removes the reference.
+  float m_ref = -INFINITY, m_max = -INFINITY;
+  for (int pass = 0;; ++pass) {
+#pragma unroll
+  for (int d = 0; d < DK / 32; ++d) o[d] = floatx16{};
+  l_run = 0.f;
+  bool redo = false;
   // ring row of band tile 0 of this wave for key tile k: 64k + 96 - 32w
   int rrw = 96 - 32 * w;
   bf16x16 carry = bf16x16{};  // band tile 0 of the current key tile, as stored
@@ -614,18 +639,10 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 #pragma unroll
       for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[u][r]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    // Lazy rescale: the running max moves only when a score exceeds it by
-    // more than thr, so probabilities stay below 2^8 and fp32 sums stay exact
-    // enough; the final normalisation divides by the same sum.
-    if (__any(tmax > m_run + thr)) {
-      const float m_new = fmaxf(m_run, tmax);
-      const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m_run - m_new) * sc);
-      m_run = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int d = 0; d < DK / 32; ++d) o[d] *= alpha;
-    }
-    const float msc = m_run == -INFINITY ? 0.f : m_run * sc;
+    m_max = fmaxf(m_max, tmax);
+    if (m_ref == -INFINITY) m_ref = tmax;
+    redo = redo || tmax > m_ref + lim;
+    const float msc = m_ref == -INFINITY ? 0.f : m_ref * sc;
     float psum = 0.f;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
@@ -653,6 +670,10 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
       }
 
     __syncthreads();  // waits for this wave's loads of the next tile first
+  }
+  // (a workgroup-wide decision: every wave takes the same passes and barriers)
+  if (pass == 1 || !__syncthreads_or(redo)) break;
+  m_ref = m_max;
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
