@@ -374,11 +374,13 @@ struct Cfg2 {
 __device__ __forceinline__ constexpr int swap23(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef __bf16 bf16x8_a2 __attribute__((ext_vector_type(8), aligned(2)));
 
 template <int DK, int NW, bool DEBUG>
 __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, int nb) {
   using C = Cfg2<DK, NW>;
   constexpr int QB = C::QB, NK = C::NK, NS = C::NS, RB = C::RB;
+  constexpr int PF = 3;  // MFMA steps an LDS operand read is issued ahead
   __shared__ __attribute__((aligned(16))) char smem[C::LDS];
 
   // Work order for 8 XCDs: workgroup L runs on XCD L % 8, so each XCD gets a
@@ -394,7 +396,10 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   const int i0 = (W % nqb) * QB;
   const int iw = i0 + 32 * w;  // first query of this wave
   const int qi = iw + c;       // this lane's query column
-  bf16* Rm = reinterpret_cast<bf16*>(smem + C::R_OFF) + (w * 32 + c) * C::RMP;
+  // Remap strip row of this query column: band value n at Rs[n], written 4
+  // rows at a time (8-byte aligned), read 8 keys at a time at n = 31 - c + 8k
+  // (2-byte aligned 16-byte reads, which the LDS serves unaligned).
+  bf16* Rs = reinterpret_cast<bf16*>(smem + C::R_OFF) + (w * 32 + c) * C::RMP;
 
   // q_u fragments (B operand): lane holds d_k values 16s + 8hh + [0, 8).
   // Rows past T read the last row (finite; their keys are all masked).
@@ -539,7 +544,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   auto put = [&](const bf16x16& v, int t) {
 #pragma unroll
     for (int a = 0; a < 4; ++a)
-      *reinterpret_cast<bf16x4*>(Rm + 32 * t + 8 * a + 4 * hh) = bf16x4{v[4 * a], v[4 * a + 1], v[4 * a + 2], v[4 * a + 3]};
+      *reinterpret_cast<bf16x4*>(Rs + 32 * t + 8 * a + 4 * hh) = bf16x4{v[4 * a], v[4 * a + 1], v[4 * a + 2], v[4 * a + 3]};
   };
 
   // Softmax with a fixed reference per query: probabilities are
@@ -585,10 +590,24 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
       floatx16 b1 = band_init(rrw + 32), b2 = band_init(rrw + 64);
       const char* r1 = smem + C::P_OFF + ((rrw + 32) % C::RING) * RB;
       const char* r2 = smem + C::P_OFF + ((rrw + 64) % C::RING) * RB;
+      // operand reads run PF steps ahead of the MFMAs; the sched_barriers pin
+      // that order (the LDS latency is several MFMAs long)
+      bf16x8 a1[PF], a2[PF];
+#pragma unroll
+      for (int st = 0; st < PF; ++st) {
+        a1[st] = *reinterpret_cast<const bf16x8*>(r1 + lo[st]);
+        a2[st] = *reinterpret_cast<const bf16x8*>(r2 + lo[st]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
-        b1 = mma32(*reinterpret_cast<const bf16x8*>(r1 + lo[st]), qu[st], b1);
-        b2 = mma32(*reinterpret_cast<const bf16x8*>(r2 + lo[st]), qu[st], b2);
+        b1 = mma32(a1[st % PF], qu[st], b1);
+        b2 = mma32(a2[st % PF], qu[st], b2);
+        if (st + PF < NS) {
+          a1[st % PF] = *reinterpret_cast<const bf16x8*>(r1 + lo[st + PF]);
+          a2[st % PF] = *reinterpret_cast<const bf16x8*>(r2 + lo[st + PF]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
       put(pack(b1), 1);
       carry = pack(b2);
@@ -599,26 +618,46 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
     // S = K . q_u: output row m of block u is key 32u + swap23(m)
     const char* Ks = smem + C::K_OFF + buf * C::KBUF;
     floatx16 s[2] = {floatx16{}, floatx16{}};
+    {
+      bf16x8 ka[PF][2];
 #pragma unroll
-    for (int st = 0; st < NS; ++st)
+      for (int st = 0; st < PF; ++st)
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-        s[u] = mma32(*reinterpret_cast<const bf16x8*>(Ks + 32 * u * RB + lo[st]), qu[st], s[u]);
+        for (int u = 0; u < 2; ++u) ka[st][u] = *reinterpret_cast<const bf16x8*>(Ks + 32 * u * RB + lo[st]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+#pragma unroll
+        for (int u = 0; u < 2; ++u) s[u] = mma32(ka[st % PF][u], qu[st], s[u]);
+        if (st + PF < NS)
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+            ka[st % PF][u] = *reinterpret_cast<const bf16x8*>(Ks + 32 * u * RB + lo[st + PF]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
     __builtin_amdgcn_wave_barrier();
 
-    // x = q_u k + bd for this lane's keys jl(u, r) = 32u + 16(r / 8) + 8hh + r % 8
-    const bf16* rq = Rm + 31 - c + 8 * hh;
+    // x = q_u k + bd for this lane's keys jl(u, r) = 32u + 16(r / 8) + 8hh + r % 8:
+    // 8 consecutive keys per 16-byte read
+    const bf16* rq = Rs + 31 - c + 8 * hh;
     float tmax = -INFINITY;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float bdv = (float)rq[32 * u + 16 * (r >> 3) + (r & 7)];
-        if (DEBUG) {
-          const int j = j0 + 32 * u + 16 * (r >> 3) + 8 * hh + (r & 7);
-          if (qi < p.T && j < p.L) p.dbg_bd[(((int64_t)b * p.H + h) * p.T + qi) * p.L + j] = p.scale_bd * bdv;
+      for (int g = 0; g < 2; ++g) {
+        // (read as bf16, the type the strip is written with, so no
+        // type-based alias analysis can move it across those writes)
+        const bf16x8 q8 = *reinterpret_cast<const bf16x8_a2*>(rq + 32 * u + 16 * g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float bdv = (float)q8[e];
+          if (DEBUG) {
+            const int j = j0 + 32 * u + 16 * g + 8 * hh + e;
+            if (qi < p.T && j < p.L) p.dbg_bd[(((int64_t)b * p.H + h) * p.T + qi) * p.L + j] = p.scale_bd * bdv;
+          }
+          s[u][8 * g + e] += bdv;
         }
-        s[u][r] += bdv;
       }
     __builtin_amdgcn_wave_barrier();
     if (!__all(iv.x <= j0 && iv.y >= j0 + NK)) {  // some key of the tile is hidden from some query
@@ -655,19 +694,29 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 
     // O^T += V^T P^T over 16-key steps (u, jj): k-slot e of lane (c, hh) is
     // key 32u + 16jj + 8hh + e, register 8jj + e of block u.
+    // (the V^T operands of the next 16-key step are read during this one)
     const char* Vrow = smem + C::V_OFF + buf * C::VBUF + c * (NK * 2);
+    {
+      bf16x8 vo[2][DK / 32];
+      auto vread = [&](int step, bf16x8* dst) {
+        const char* va = Vrow + 16 * ((2 * step + hh) ^ (c % C::VCN));  // step = 2u + jj
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+        for (int d = 0; d < DK / 32; ++d) dst[d] = *reinterpret_cast<const bf16x8*>(va + 32 * d * (NK * 2));
+      };
+      vread(0, vo[0]);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
+      for (int step = 0; step < 4; ++step) {
+        if (step + 1 < 4) vread(step + 1, vo[(step + 1) & 1]);
+        const int u = step >> 1, jj = step & 1;
         bf16x8 pb8;
 #pragma unroll
         for (int e = 0; e < 8; ++e) pb8[e] = (bf16)s[u][8 * jj + e];
-        const char* va = Vrow + 16 * ((4 * u + 2 * jj + hh) ^ (c % C::VCN));
 #pragma unroll
-        for (int d = 0; d < DK / 32; ++d)
-          o[d] = mma32(*reinterpret_cast<const bf16x8*>(va + 32 * d * (NK * 2)), pb8, o[d]);
+        for (int d = 0; d < DK / 32; ++d) o[d] = mma32(vo[step & 1][d], pb8, o[d]);
+        __builtin_amdgcn_sched_barrier(0);
       }
+    }
 
     __syncthreads();  // waits for this wave's loads of the next tile first
   }
