@@ -777,6 +777,190 @@ __global__ __launch_bounds__(256) void pos_bias_diff_kernel(const AttnParams p, 
   if (sub == 0 && n < p.p_rows + p.p_pad) out[(int64_t)h * ld + n + p.p_pad] = -acc;
 }
 
+// ---------------------------------------------------------------------------
+// fp32 chunk kernel for short query blocks (the cache-aware streaming step:
+// T <= 16 queries against L <= 96 keys of the cache ring). One workgroup of
+// four waves per (item, head) stages the visible key rows and the position
+// rows they reach in LDS once, then:
+//   S  = q_u K^T           (16 x keys)            fp32 16x16x4 MFMAs
+//   B' = q_v P'^T          (16 x (keys + 15))      over the rows
+//        P' = P[r0 + m], r0 = center - qoff - 15 + jbeg; rel_shift reads
+//        bd(i, j) = B'[i][j - jbeg + 15 - i]
+//   softmax per query row (fp32, exact max), probabilities in LDS
+//   O  = probs . V         (16 x d_k), V^T staged over the consumed K rows
+// The work items are few (items x heads), so every wave takes whole 16x16
+// output tiles and nothing waits on another workgroup.
+// ---------------------------------------------------------------------------
+template <int DK>
+struct CfgS {
+  static constexpr int NT = 256, NQ = 16, LMAX = 96, PMAX = LMAX + NQ - 1;
+  static constexpr int RP = DK * 4 + 16;                                // K / V / position row pitch (bytes)
+  static constexpr int K_OFF = 0;                                       // K rows, later V rows
+  static constexpr int P_OFF = LMAX * RP;                               // position rows
+  static constexpr int PROWS = (PMAX + 15) / 16 * 16;
+  static constexpr int S_OFF = P_OFF + PROWS * RP;                      // scores / probabilities [NQ][LMAX]
+  static constexpr int B_OFF = S_OFF + NQ * LMAX * 4;                   // band products [NQ][PROWS]
+  static constexpr int LDS = B_OFF + NQ * PROWS * 4;
+  static constexpr int RPI = NT / (DK / 4);                             // rows per pass of the workgroup
+  static constexpr int KCH = LMAX / RPI;                                // K / V chunks per thread
+  static constexpr int PCH = PROWS / RPI;                               // position chunks per thread
+  static_assert(KCH * RPI == LMAX && PCH * RPI == PROWS, "row split");
+  static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+template <int DK>
+__global__ __launch_bounds__(256) void attn_chunk_f32_kernel(const AttnParams p) {
+  using C = CfgS<DK>;
+  constexpr int NQ = C::NQ, LMAX = C::LMAX, NS = DK / 16;
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int rl = lane & 15, g = lane >> 4;  // MFMA row / column in the tile, k group
+  const int h = blockIdx.x, bl = blockIdx.y, b = p.b0 + bl;
+  float* out = reinterpret_cast<float*>(p.o) + (int64_t)b * p.o_bs + h * DK;
+
+  int jbeg, jend;
+  key_range(p, bl, 0, p.T, jbeg, jend);
+  const int nk = max(jend - jbeg, 0);  // visible keys (<= LMAX)
+  if (nk == 0) {                       // no query of this item sees a key: zeros
+    for (int e = tid; e < p.T * DK; e += C::NT) out[(int64_t)(e / DK) * p.o_rs + e % DK] = 0.f;
+    return;
+  }
+  const int nkt = (nk + 15) / 16;   // 16-key tiles
+  const int np = nk + NQ - 1;       // position rows
+  const int npt = (np + 15) / 16;
+  const int r0 = p.center - p.qoff - (NQ - 1) + jbeg;
+  const float* kb = reinterpret_cast<const float*>(p.k) + (int64_t)b * p.kv_bs + h * DK;
+  const float* vb = reinterpret_cast<const float*>(p.v) + (int64_t)b * p.kv_bs + h * DK;
+  const float* pb = reinterpret_cast<const float*>(p.p) + h * DK;
+
+  // This thread's rows (tid / (DK/4) + RPI i) and 16-byte column chunk. Rows
+  // past the last visible key repeat it (their scores are masked and their
+  // probabilities are zero); every load is issued before the first store.
+  const int row0 = tid / (DK / 4), cb = (tid % (DK / 4)) * 4;
+  int64_t koff[C::KCH];
+  {
+    int rr = key_row(p, jbeg + min(row0, nk - 1));
+#pragma unroll
+    for (int i = 0; i < C::KCH; ++i) {
+      const int row = row0 + C::RPI * i;
+      koff[i] = (int64_t)(row < nk ? rr : key_row(p, jend - 1)) * p.kv_rs + cb;
+      rr += C::RPI;  // the next row of this thread: key + RPI (ring: mod ring_len)
+      if (p.ring_len && rr >= p.ring_len) rr -= p.ring_len;
+    }
+  }
+  u32x4 kr[C::KCH], vr[C::KCH], pr[C::PCH];
+#pragma unroll
+  for (int i = 0; i < C::KCH; ++i) kr[i] = *reinterpret_cast<const u32x4*>(kb + koff[i]);
+#pragma unroll
+  for (int i = 0; i < C::PCH; ++i) {
+    // rows outside the table meet only masked pairs: clamped (finite)
+    const int n = min(max(r0 + row0 + C::RPI * i, 0), p.p_rows - 1);
+    pr[i] = *reinterpret_cast<const u32x4*>(pb + (int64_t)n * p.p_rs + cb);
+  }
+#pragma unroll
+  for (int i = 0; i < C::KCH; ++i) vr[i] = *reinterpret_cast<const u32x4*>(vb + koff[i]);
+  // q_u, q_v A fragments: row rl, d_k values 16s + 4g + [0, 4); rows past T read row T - 1
+  floatx4 qu[NS], qv[NS];
+  {
+    const float* qr = reinterpret_cast<const float*>(p.q) + (int64_t)b * p.q_bs + (int64_t)min(rl, p.T - 1) * p.q_rs +
+                      h * DK;
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+      const int d = 16 * st + 4 * g;
+      const floatx4 x = *reinterpret_cast<const floatx4*>(qr + d);
+      qu[st] = x + *reinterpret_cast<const floatx4*>(p.bias_u + h * DK + d);
+      qv[st] = x + *reinterpret_cast<const floatx4*>(p.bias_v + h * DK + d);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < C::KCH; ++i)
+    *reinterpret_cast<u32x4*>(smem + C::K_OFF + (row0 + C::RPI * i) * C::RP + cb * 4) = kr[i];
+#pragma unroll
+  for (int i = 0; i < C::PCH; ++i)
+    *reinterpret_cast<u32x4*>(smem + C::P_OFF + (row0 + C::RPI * i) * C::RP + cb * 4) = pr[i];
+  __syncthreads();
+
+  // score tiles (keys) and band tiles (position rows), spread over the waves
+  float* Sl = reinterpret_cast<float*>(smem + C::S_OFF);
+  float* Bl = reinterpret_cast<float*>(smem + C::B_OFF);
+  for (int t = w; t < nkt + npt; t += 4) {
+    const bool is_s = t < nkt;
+    const int tt = is_s ? t : t - nkt;
+    const char* rows = smem + (is_s ? C::K_OFF : C::P_OFF) + (tt * 16 + rl) * C::RP + 16 * g;
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (is_s) {
+#pragma unroll
+      for (int st = 0; st < NS; ++st) acc = mma16(qu[st], *reinterpret_cast<const floatx4*>(rows + 64 * st), acc);
+    } else {
+#pragma unroll
+      for (int st = 0; st < NS; ++st) acc = mma16(qv[st], *reinterpret_cast<const floatx4*>(rows + 64 * st), acc);
+    }
+    // C layout: lane holds rows 4g + e of column rl
+    float* dst = is_s ? Sl + 4 * g * LMAX + tt * 16 + rl : Bl + 4 * g * C::PROWS + tt * 16 + rl;
+    const int ld = is_s ? LMAX : C::PROWS;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[e * ld] = acc[e];
+  }
+  __syncthreads();
+
+  // V rows over the K rows (all K reads are done)
+#pragma unroll
+  for (int i = 0; i < C::KCH; ++i)
+    *reinterpret_cast<u32x4*>(smem + C::K_OFF + (row0 + C::RPI * i) * C::RP + cb * 4) = vr[i];
+
+  // softmax per query row: wave w takes rows 4w + lane / 16, each row split
+  // over 16 lanes (keys jl = lane % 16 + 16k), so the reductions stay inside
+  // 16-lane rows (DPP, no LDS round trips)
+  {
+    const int i = 4 * w + (lane >> 4), q = lane & 15;
+    const int2 iv = query_interval(p, bl, i);
+    float x[LMAX / 16];
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < LMAX / 16; ++k) {
+      const int jl = q + 16 * k;
+      x[k] = -INFINITY;
+      if (jl < nk && in_interval(jbeg + jl, iv))
+        x[k] = Sl[i * LMAX + jl] * p.scale + Bl[i * C::PROWS + jl + NQ - 1 - i] * p.scale_bd;
+      m = fmaxf(m, x[k]);
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < LMAX / 16; ++k) {
+      x[k] = m == -INFINITY ? 0.f : __expf(x[k] - m);
+      sum += x[k];
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 16);
+    const float inv = sum > 0.f ? 1.f / sum : 0.f;  // a row that sees no key gives 0
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int k = 0; k < LMAX / 16; ++k) Sl[i * LMAX + q + 16 * k] = x[k] * inv;
+  }
+  __syncthreads();
+
+  // O = probs . V: wave w takes d_k tiles w, w + 4, ...; the B operand is
+  // V[key 16kt + 4g + s][16dt + rl], one float per MFMA
+  const float* Vl = reinterpret_cast<const float*>(smem + C::K_OFF);
+  for (int dt = w; dt < DK / 16; dt += 4) {
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int kt = 0; kt < nkt; ++kt) {
+      const floatx4 a = *reinterpret_cast<const floatx4*>(Sl + rl * LMAX + kt * 16 + 4 * g);
+      floatx4 bv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bv[e] = Vl[(kt * 16 + 4 * g + e) * (C::RP / 4) + dt * 16 + rl];
+      acc = mma16(a, bv, acc);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 4 * g + e;
+      if (i < p.T) out[(int64_t)i * p.o_rs + dt * 16 + rl] = acc[e];
+    }
+  }
+}
+
 template <typename T, int DK, int NW, bool DEBUG>
 hipError_t launch(const AttnParams& p, int nb, hipStream_t s) {
   using C = Cfg<T, DK, NW>;
@@ -857,6 +1041,13 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
     return hipErrorInvalidValue;
   }
   if (dt == kF32) {
+    if (p.T <= CfgS<128>::NQ && p.L <= CfgS<128>::LMAX && !p.dbg_bd) {
+      const dim3 grid(p.H, nb);
+      if (head_dim == 64) hipLaunchKernelGGL(attn_chunk_f32_kernel<64>, grid, dim3(256), 0, s, p);
+      else if (head_dim == 128) hipLaunchKernelGGL(attn_chunk_f32_kernel<128>, grid, dim3(256), 0, s, p);
+      else return hipErrorInvalidValue;
+      return hipGetLastError();
+    }
     if (head_dim == 64) return dispatch_nw<float, 64>(p, nb, s);
     if (head_dim == 128) return dispatch_nw<float, 128>(p, nb, s);
   } else {
