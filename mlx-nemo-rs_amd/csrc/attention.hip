@@ -429,7 +429,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   key_range(p, bl, i0, min(i0 + QB, p.T), jbeg, jend);
   const int2 iv = query_interval(p, bl, qi);
   const float sc = p.scale * kLog2e;
-  const float lim = 100.f / sc;  // largest (score - reference) kept in one pass: 2^100
+  const float lim = 100.f / sc;  // largest (score - reference) kept without rescaling: 2^100
   const int jfirst = (jbeg / NK) * NK;
   // ring row rr holds position row R0 + rr
   const int R0 = p.center - p.qoff - (i0 + 31) + jfirst - 96;
@@ -547,19 +547,18 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
       *reinterpret_cast<bf16x4*>(Rs + 32 * t + 8 * a + 4 * hh) = bf16x4{v[4 * a], v[4 * a + 1], v[4 * a + 2], v[4 * a + 3]};
   };
 
-  // Softmax with a fixed reference per query: probabilities are
+  // Softmax with a lazily moved reference per query: probabilities are
   // 2^((x - m_ref) s log2 e), with m_ref the first finite tile maximum of the
-  // query (o and l are still zero until then), so the accumulators are only
-  // ever touched by MFMAs. A later maximum above m_ref makes probabilities
-  // larger than 1; up to 2^100 that stays far from fp32 overflow for any key
-  // count, and beyond it the whole pass is repeated with the true maximum as
-  // the reference. The final division by l removes the reference.
-  float m_ref = -INFINITY, m_max = -INFINITY;
-  for (int pass = 0;; ++pass) {
+  // query (o and l are still zero until then). A later maximum above m_ref
+  // makes probabilities larger than 1; up to 2^100 that stays far from fp32
+  // and bf16 overflow for any key count, so o and l are only rescaled (to the
+  // new tile maximum) when a tile maximum exceeds the reference by more than
+  // that, which ordinary inputs never do. The final division by l removes the
+  // reference.
+  float m_ref = -INFINITY;
 #pragma unroll
   for (int d = 0; d < DK / 32; ++d) o[d] = floatx16{};
   l_run = 0.f;
-  bool redo = false;
   // ring row of band tile 0 of this wave for key tile k: 64k + 96 - 32w
   int rrw = 96 - 32 * w;
   bf16x16 carry = bf16x16{};  // band tile 0 of the current key tile, as stored
@@ -678,9 +677,16 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 #pragma unroll
       for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[u][r]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    m_max = fmaxf(m_max, tmax);
     if (m_ref == -INFINITY) m_ref = tmax;
-    redo = redo || tmax > m_ref + lim;
+    if (__any(tmax > m_ref + lim)) {
+      // (o holds only this lane's query: its column of O^T)
+      const bool up = tmax > m_ref + lim;
+      const float a = up ? __builtin_amdgcn_exp2f((m_ref - tmax) * sc) : 1.f;
+      m_ref = up ? tmax : m_ref;
+#pragma unroll
+      for (int d = 0; d < DK / 32; ++d) o[d] *= a;
+      l_run *= a;
+    }
     const float msc = m_ref == -INFINITY ? 0.f : m_ref * sc;
     float psum = 0.f;
 #pragma unroll
@@ -719,10 +725,6 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
     }
 
     __syncthreads();  // waits for this wave's loads of the next tile first
-  }
-  // (a workgroup-wide decision: every wave takes the same passes and barriers)
-  if (pass == 1 || !__syncthreads_or(redo)) break;
-  m_ref = m_max;
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);

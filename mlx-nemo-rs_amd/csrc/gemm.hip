@@ -318,9 +318,309 @@ __global__ __launch_bounds__(256) void gemm_reduce(const GemmParams p, int split
 }
 
 template <int BM>
-int64_t m_tiles(const GemmParams& p) {
+__host__ __device__ int64_t m_tiles(const GemmParams& p) {
   if (p.seg_T > 0) return (int64_t)(p.M / p.seg_T) * ((p.seg_T + BM - 1) / BM);
   return (p.M + BM - 1) / BM;
+}
+
+// ---------------------------------------------------------------------------
+// bf16 tile kernel for the large projections (QKV, output and position
+// projections of long inputs).
+//
+// One workgroup of 4 waves (2 x 2) computes a BM x BN tile; each wave holds a
+// (BM/2) x (BN/2) block of fp32 accumulators (up to 128 x 128, in AGPRs) fed
+// by 32x32x16 bf16 MFMAs, so every 16-byte operand fragment read from LDS
+// serves BM/64 or BN/64 MFMAs. Operands stream through two LDS stages of 64
+// k-columns (128 bytes per row): A (and dense B) with direct-to-LDS buffer
+// loads (no VGPR staging; rows past the matrix read as zero), quantized B as
+// u8 codes dequantised in registers on their way into LDS. A stage row's
+// eight 16-byte chunks are stored XOR-permuted by (row / 2) % 8, which puts
+// the 32 rows of one fragment read on all 64 banks. Within a stage the
+// fragment reads of k-step s + 1 are issued before the MFMAs of step s
+// (sched_barrier-pinned), and the first reads of the next stage are issued
+// right after the stage barrier, ahead of the stage's last MFMAs.
+//
+// The MFMA takes the weight fragment as its first operand, so a lane's
+// accumulators hold four consecutive output columns of one output row. The
+// epilogue stages the bf16-rounded tile row-major in LDS and writes whole
+// 16-byte runs: rows to C (bias, residual and the ring row remap applied per
+// run), or, for columns at or past vt_col0, 8-token runs of V^T read down the
+// staged columns.
+template <int BM, int BN, bool QUANT>
+struct TileCfg {
+  static constexpr int WM = BM / 2, WN = BN / 2;  // per-wave block
+  static constexpr int TM = WM / 32, TN = WN / 32;
+  static constexpr int ABYTES = BM * 128, STAGE = (BM + BN) * 128;
+  static constexpr int NA = BM / 32;               // A loads per wave per stage (1 KB each)
+  static constexpr int NB = QUANT ? 0 : BN / 32;   // dense B loads per wave per stage
+  static constexpr int QB = BN / 64;               // quantized 16-code chunks per thread per stage
+  static constexpr int OP = WN * 2 + 16;           // staged output row pitch (bytes)
+  static constexpr int LDS = 2 * STAGE > 4 * WM * OP ? 2 * STAGE : 4 * WM * OP;
+  static_assert(LDS <= 160 * 1024, "tile exceeds LDS");
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+constexpr int kRawBuffer = 0x00020000;  // buffer descriptor dword 3: untyped 32-bit data
+
+template <int BM, int BN, bool QUANT>
+__global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
+  using C = TileCfg<BM, BN, QUANT>;
+  __shared__ __attribute__((aligned(1024))) char smem[C::LDS];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w >> 1, wn = w & 1;
+
+  // Contiguous tile ranges per XCD (workgroup i runs on XCD i % 8), walked
+  // 8 M tiles at a time so concurrently running tiles share A and B rows.
+  const int tilesM = (int)m_tiles<BM>(p), tilesN = p.N / BN, nt = tilesM * tilesN;
+  const int per = (nt + 7) / 8;
+  const int W = (int)(blockIdx.x % 8) * per + (int)(blockIdx.x / 8);
+  if (W >= nt) return;
+  constexpr int GM = 8;
+  const int gsz = GM * tilesN, first = W / gsz * GM, gm = min(tilesM - first, GM);
+  const int tmi = first + (W % gsz) % gm, n0 = (W % gsz) / gm * BN;
+  int m0, m_end, seg;
+  tile_rows<BM>(p, tmi, m0, m_end, seg);
+
+  const char* Ab = reinterpret_cast<const char*>(p.A) + (int64_t)m0 * p.lda * 2;
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc((void*)Ab, (short)0, (int)((int64_t)(p.M - m0) * p.lda * 2), kRawBuffer);
+  // load g of wave w fills LDS chunks 64 (w NA + g) + [0, 64): row pos / 8,
+  // stored chunk pos % 8, which holds k-chunk (pos % 8) ^ ((row / 2) % 8)
+  int aoff[C::NA];
+#pragma unroll
+  for (int g = 0; g < C::NA; ++g) {
+    const int pos = (w * C::NA + g) * 64 + lane, row = pos >> 3;
+    aoff[g] = (int)(row * p.lda * 2 + 16 * ((pos & 7) ^ ((row >> 1) & 7)));
+  }
+  const char* Bb = reinterpret_cast<const char*>(p.W) + (int64_t)n0 * p.K * (QUANT ? 1 : 2);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc((void*)Bb, (short)0, (int)((int64_t)BN * p.K * (QUANT ? 1 : 2)), kRawBuffer);
+  int boff[C::NB > 0 ? C::NB : 1];
+#pragma unroll
+  for (int g = 0; g < C::NB; ++g) {
+    const int pos = (w * C::NB + g) * 64 + lane, row = pos >> 3;
+    boff[g] = (int)(row * p.K * 2 + 16 * ((pos & 7) ^ ((row >> 1) & 7)));
+  }
+  auto issue = [&](int kt, int buf) {
+    char* S = smem + buf * C::STAGE;
+#pragma unroll
+    for (int g = 0; g < C::NA; ++g)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(S + (w * C::NA + g) * 1024), 16, (int)aoff[g],
+                                               (int)(kt * 128), 0, 0);
+    if constexpr (!QUANT) {
+#pragma unroll
+      for (int g = 0; g < C::NB; ++g)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(S + C::ABYTES + (w * C::NB + g) * 1024), 16,
+                                                 (int)boff[g], (int)(kt * 128), 0, 0);
+    }
+  };
+  // quantized B: chunk q = tid + 256 i holds codes 16 (q % 4) .. + 16 of row q / 4
+  u32x4 qr[C::QB];
+  floatx2 qs[C::QB];
+  const int groups = p.K / 64;
+  auto qload = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < C::QB; ++i) {
+      const int q = tid + 256 * i, r = q >> 2;
+      qr[i] = *reinterpret_cast<const u32x4*>(Bb + (int64_t)r * p.K + kt * 64 + (q & 3) * 16);
+      qs[i] = *reinterpret_cast<const floatx2*>(p.sb + 2 * ((int64_t)(n0 + r) * groups + kt));
+    }
+  };
+  auto qstore = [&](int buf) {
+    char* Bs = smem + buf * C::STAGE + C::ABYTES;
+#pragma unroll
+    for (int i = 0; i < C::QB; ++i) {
+      const int q = tid + 256 * i, r = q >> 2, c2 = 2 * (q & 3);
+      bf16 v[16];
+      dequant16<bf16>(qr[i], qs[i].x, qs[i].y, v);
+      *reinterpret_cast<u32x4*>(Bs + r * 128 + 16 * (c2 ^ ((r >> 1) & 7))) = reinterpret_cast<const u32x4*>(v)[0];
+      *reinterpret_cast<u32x4*>(Bs + r * 128 + 16 * ((c2 + 1) ^ ((r >> 1) & 7))) = reinterpret_cast<const u32x4*>(v)[1];
+    }
+  };
+
+  // fragment (t, s): rows 32 t + lane % 32 of this wave's block, k-chunk
+  // 2 s + lane / 32 of the stage
+  const int arow = (wm * C::WM + (lane & 31)) * 128;
+  const int brow = C::ABYTES + (wn * C::WN + (lane & 31)) * 128;
+  int so[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) so[s] = 16 * ((2 * s + (lane >> 5)) ^ ((lane >> 1) & 7));
+
+  floatx16 acc[C::TN][C::TM];
+#pragma unroll
+  for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) acc[j][i] = floatx16{};
+
+  const int nk = p.K / 64;
+  issue(0, 0);
+  if constexpr (QUANT) {
+    qload(0);
+    qstore(0);
+  }
+  __syncthreads();
+
+  bf16x8 fa[2][C::TM], fb[2][C::TN];
+  auto rd = [&](const char* S, int s, int b) {
+#pragma unroll
+    for (int i = 0; i < C::TM; ++i) fa[b][i] = *reinterpret_cast<const bf16x8*>(S + arow + i * 4096 + so[s]);
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) fb[b][j] = *reinterpret_cast<const bf16x8*>(S + brow + j * 4096 + so[s]);
+  };
+  rd(smem, 0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    const char* S = smem + (kt & 1) * C::STAGE;
+    if constexpr (QUANT) {
+      if (kt + 1 < nk) qload(kt + 1);
+    }
+    if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (s < 3) {
+        rd(S, s + 1, (s + 1) & 1);
+      } else {
+        if constexpr (QUANT) {
+          if (kt + 1 < nk) qstore((kt + 1) & 1);
+        }
+        // this wave's operand reads and its loads of stage kt + 1 are done;
+        // after the barrier every wave's are
+        __builtin_amdgcn_s_waitcnt(7 << 4);  // vmcnt(0) lgkmcnt(0)
+        asm volatile("s_barrier" ::: "memory");
+        if (kt + 1 < nk) rd(smem + ((kt + 1) & 1) * C::STAGE, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+        for (int i = 0; i < C::TM; ++i) acc[j][i] = mma32(fb[s & 1][j], fa[s & 1][i], acc[j][i]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // Stage T(acc) row-major: lane holds row 32 i + lane % 32 of the block and
+  // columns 32 j + 8 q + 4 (lane / 32) + [0, 4).
+  __syncthreads();
+  char* st = smem + w * (C::WM * C::OP);
+#pragma unroll
+  for (int i = 0; i < C::TM; ++i)
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (bf16)acc[j][i][4 * q + e];
+        *reinterpret_cast<bf16x4*>(st + (i * 32 + (lane & 31)) * C::OP + (j * 32 + 8 * q + 4 * (lane >> 5)) * 2) = v;
+      }
+  const int row0 = m0 + wm * C::WM, col0 = n0 + wn * C::WN;
+  // columns [col0, col0 + ncn) go to C, the rest of the block to V^T
+  const int ncn = p.vt ? min(max(p.vt_col0 - col0, 0), C::WN) : C::WN;
+  constexpr int CPR = C::WN / 8;
+  if (ncn > 0) {
+#pragma unroll
+    for (int it = 0; it < (C::WM * CPR + 63) / 64; ++it) {
+      const int id = it * 64 + lane;
+      const int r = id / CPR, c = id % CPR;
+      if ((C::WM * CPR) % 64 && id >= C::WM * CPR) break;
+      const int row = row0 + r;
+      if (c * 8 >= ncn || row >= m_end) continue;
+      const int col = col0 + c * 8;
+      bf16x8 v = *reinterpret_cast<const bf16x8*>(st + r * C::OP + c * 16);
+      if (p.bias || p.R) {
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = (float)v[e];
+        if (p.bias) {
+          const floatx4 b0 = *reinterpret_cast<const floatx4*>(p.bias + col);
+          const floatx4 b1 = *reinterpret_cast<const floatx4*>(p.bias + col + 4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            f[e] = round_to<bf16>(f[e] + b0[e]);
+            f[e + 4] = round_to<bf16>(f[e + 4] + b1[e]);
+          }
+        }
+        if (p.R) {
+          const bf16x8 rv = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.R) + (int64_t)row * p.ldr + col);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) f[e] = round_to<bf16>((float)rv[e] + f[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (bf16)f[e];
+      }
+      *reinterpret_cast<bf16x8*>(reinterpret_cast<bf16*>(p.C) + row_offset(p, row) + col) = v;
+    }
+  }
+  if (ncn < C::WN) {
+    // V^T: 8-token runs down column n of the block; tokens at or past vt_Tpad
+    // belong to the next utterance and are dropped
+    constexpr int MCH = C::WM / 8;
+    const int t0 = m0 - seg * p.seg_T + wm * C::WM;  // token of block row 0
+    bf16* VT = reinterpret_cast<bf16*>(p.vt) + (int64_t)seg * p.vt_Tpad;
+    const int nvt = (C::WN - ncn) * MCH;
+    for (int id = lane; id < nvt; id += 64) {
+      const int nl = ncn + id / MCH, mc = id % MCH;
+      const int tok = t0 + mc * 8;
+      if (tok >= p.vt_Tpad) continue;
+      const int col = col0 + nl;
+      const float b = p.bias ? p.bias[col] : 0.f;
+      bf16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bf16 x = *reinterpret_cast<const bf16*>(st + (mc * 8 + e) * C::OP + nl * 2);
+        v[e] = p.bias ? (bf16)((float)x + b) : x;
+      }
+      *reinterpret_cast<bf16x8*>(VT + (int64_t)(col - p.vt_col0) * p.vt_ld + tok) = v;
+    }
+  }
+}
+
+// Estimated duration of one launch of the tile kernel, in units of one
+// 192 x 192 tile pass at K = 1024 (measured per-tile times: 256 x 256 1.33,
+// 128 x 128 0.46 alone on a CU and 0.77 for two sharing one).
+template <int BM, int BN>
+double tile_cost(const GemmParams& p) {
+  const int64_t tiles = m_tiles<BM>(p) * (p.N / BN);
+  double c;
+  if (BM == 128 && BN == 128) c = tiles <= 256 ? 0.46 : (double)((tiles + 511) / 512) * 0.77;
+  else c = (double)((tiles + 255) / 256) * (BM * BN == 256 * 256 ? 1.33 : 1.0);
+  return c * p.K / 1024.0;
+}
+
+template <int BM, int BN, bool QUANT>
+hipError_t launch_tile(const GemmParams& p, hipStream_t s) {
+  const int64_t tiles = m_tiles<BM>(p) * (p.N / BN);
+  const unsigned grid = (unsigned)((tiles + 7) / 8 * 8);
+  hipLaunchKernelGGL((gemm_tile_kernel<BM, BN, QUANT>), dim3(grid), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+// The tile kernel's shape requirements: 16-byte runs in every operand and
+// output row, and V^T runs of 8 tokens inside each utterance's span.
+bool tile_ok(const GemmParams& p) {
+  if (p.K % 64 || p.lda % 8 || p.ldc % 8 || (p.R && p.ldr % 8) || (p.vt && p.R)) return false;
+  if ((reinterpret_cast<uintptr_t>(p.A) | reinterpret_cast<uintptr_t>(p.C) | reinterpret_cast<uintptr_t>(p.W)) & 15)
+    return false;
+  if (p.R && (reinterpret_cast<uintptr_t>(p.R) & 15)) return false;
+  if (p.bias && (reinterpret_cast<uintptr_t>(p.bias) & 15)) return false;
+  if (p.vt && (p.vt_col0 % 8 || p.vt_Tpad % 8)) return false;
+  if ((int64_t)p.M * p.lda * 2 >= ((int64_t)1 << 31) || (int64_t)p.N * p.K * 2 >= ((int64_t)1 << 31)) return false;
+  return true;
+}
+
+// bf16 projections with at least ~100 tiles of 128 x 128 go to the tile
+// kernel, at the tile shape with the lowest estimated time.
+template <bool QUANT>
+bool dispatch_tile(const GemmParams& p, hipStream_t s, hipError_t& err) {
+  if (!tile_ok(p) || m_tiles<128>(p) * (p.N / 128) < 96 || p.N % 128) return false;
+  double best = tile_cost<128, 128>(p);
+  int pick = 128;
+  if (p.N % 192 == 0 && tile_cost<192, 192>(p) < best) best = tile_cost<192, 192>(p), pick = 192;
+  if (p.N % 256 == 0 && tile_cost<256, 256>(p) < best) best = tile_cost<256, 256>(p), pick = 256;
+  if (pick == 256) err = launch_tile<256, 256, QUANT>(p, s);
+  else if (pick == 192) err = launch_tile<192, 192, QUANT>(p, s);
+  else err = launch_tile<128, 128, QUANT>(p, s);
+  return true;
 }
 
 template <typename T, bool QUANT, int BM, int BN, int NWM, int NWN>
@@ -338,6 +638,10 @@ hipError_t launch(const GemmParams& p, int splits, hipStream_t s) {
 template <typename T, bool QUANT>
 hipError_t dispatch(const GemmParams& p, hipStream_t s) {
   const int bk = ROWB / (int)sizeof(T);
+  if constexpr (sizeof(T) == 2) {
+    hipError_t err;
+    if (dispatch_tile<QUANT>(p, s, err)) return err;
+  }
   // 256x256 (8 waves) when it still fills the GPU about twice over: it
   // halves the LDS and L2 traffic per flop of 128x128 (measured 1.15x on
   // M = 15000, N = 3072); bf16 only (fp32 accumulators would not fit).

@@ -240,6 +240,82 @@ def test_forward_xl_offline_bf16():
     assert err < BF16_TOL
 
 
+def _biased_weights(seed, d_model, n_heads, sigma):
+    rng = np.random.default_rng(seed)
+    w = W.make_layer_weights(rng, d_model, n_heads, True, False)
+    for name in ("linear_q", "linear_k", "linear_v", "linear_out"):
+        w[f"{name}.bias"] = rng.normal(0.0, sigma, size=d_model).astype(np.float32)
+    return w, rng
+
+
+@pytest.mark.parametrize("rows", [3000, 1537])
+def test_linear_bf16_bias_large(rows):
+    """y = T(T(x W^T) + b) (quantization.rs:126-162) on row counts that take
+    the tiled bf16 GEMM, including a ragged last tile. The fp32 sum may round
+    T(x W^T) one ulp away from the float64 product before the bias add, so each
+    output is within one ulp of the pre-bias value, one ulp of the result and
+    one fp32 rounding unit of sum |x||w| of the oracle."""
+    D, H = 1024, 8
+    w, rng = _biased_weights(21, D, H, 0.5)
+    p = oracle_params(w, D, H)
+    layer = gpu_layer(w, D, H, True, O.BF16)
+    x = O.bf16_round(rng.normal(size=(rows, D)))
+    for name in ("linear_q", "linear_out"):
+        got = host(layer.debug_linear(name, dev(x, O.BF16)))
+        lin = getattr(p, name)
+        ref = lin.forward(x, O.BF16)
+        wd = lin.dense_weight(O.BF16)
+        pre = x @ wd.T
+
+        def ulp(a):
+            return np.ldexp(1.0, np.frexp(np.abs(a))[1] - 8)
+
+        bound = ulp(pre) + ulp(ref) + np.abs(x) @ np.abs(wd).T * 2.0 ** -24
+        d = np.abs(got - ref)
+        print(f"{name} rows={rows}: worst |d|/bound {np.max(d / bound):.3f}")
+        assert np.all(d <= bound), name
+
+
+def test_forward_bf16_with_biases():
+    """The offline bf16 layer with non-zero linear biases (the V bias enters
+    through the transposed V epilogue), B=2, T=375, key padding; biases of
+    scale 0.1 keep the outputs at the magnitude the bf16 bound is stated for."""
+    D, H, T = 1024, 8, 375
+    w, rng = _biased_weights(22, D, H, 0.1)
+    x = rng.normal(size=(2, T, D))
+    lengths = [T, 301]
+    p = oracle_params(w, D, H)
+    pos = O.RelPositionalEncoding(D, 5000, True).get_encoding(T)
+    ref = O.mhsa_forward(p, O.bf16_round(x), O.bf16_round(pos), None, O.key_padding_mask(lengths, T), dtype=O.BF16)
+    layer = gpu_layer(w, D, H, True, O.BF16)
+    got = host(layer.forward(dev(x, O.BF16), dev(pos, O.BF16), None, M.key_padding_mask(lengths, T)))
+    err = abs_err(got, ref)
+    print(f"bf16 with biases: max abs error {err:.3e} (max |ref| {np.max(np.abs(ref)):.2f})")
+    assert err < BF16_TOL
+
+
+def test_bf16_scores_growing_far_past_first_tile():
+    """Scores that grow along the keys by thousands (x_t = g(t) z + noise with
+    g rising to 31, so q_i . k_j scales with g(i) g(j)) exceed the first key
+    tile's maximum by far more than 2^100 in exp2 units; the kernel then moves
+    its softmax reference and rescales its sums mid-row. The output matches the
+    oracle's exact softmax to bf16 precision of the output scale."""
+    D, H, T = 1024, 8, 375
+    rng = np.random.default_rng(23)
+    w = W.make_layer_weights(rng, D, H, False, False)
+    z = rng.normal(size=D)
+    g = 1.0 + 30.0 * np.arange(T) / T
+    x = (g[:, None] * z[None, :] + 0.1 * rng.normal(size=(T, D)))[None]
+    p = oracle_params(w, D, H)
+    pos = O.RelPositionalEncoding(D, 5000, True).get_encoding(T)
+    ref = O.mhsa_forward(p, O.bf16_round(x), O.bf16_round(pos), None, None, dtype=O.BF16)
+    layer = gpu_layer(w, D, H, False, O.BF16)
+    got = host(layer.forward(dev(x, O.BF16), dev(pos, O.BF16), None))
+    rel = abs_err(got, ref) / np.max(np.abs(ref))
+    print(f"growing scores: max abs error / max|ref| {rel:.3e} (max |ref| {np.max(np.abs(ref)):.1f})")
+    assert rel < 1e-2
+
+
 def test_padded_keys_are_ignored_gpu():
     """attention.rs:1025-1064 on the GPU: a padded row attends like the row unpadded."""
     cfg = W.CONFIGS["xl_offline_bf16"]
