@@ -355,6 +355,7 @@ struct TileCfg {
   static constexpr int NB = QUANT ? 0 : BN / 32;   // dense B loads per wave per stage
   static constexpr int QB = BN / 64;               // quantized 16-code chunks per thread per stage
   static constexpr int OP = WN * 2 + 16;           // staged output row pitch (bytes)
+  static constexpr bool ILV = BM * BN >= 192 * 192;  // loads spread between MFMAs (one workgroup per CU)
   static constexpr int LDS = 2 * STAGE > 4 * WM * OP ? 2 * STAGE : 4 * WM * OP;
   static_assert(LDS <= 160 * 1024, "tile exceeds LDS");
 };
@@ -415,6 +416,15 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
                                                  (int)boff[g], (int)(kt * 128), 0, 0);
     }
   };
+  auto issue1 = [&](int g, int kt, int buf) {  // load g of this wave's stage stream
+    char* S = smem + buf * C::STAGE;
+    if (g < C::NA)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(S + (w * C::NA + g) * 1024), 16, (int)aoff[g],
+                                               (int)(kt * 128), 0, 0);
+    else if constexpr (!QUANT)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(S + C::ABYTES + (w * C::NB + g - C::NA) * 1024), 16,
+                                               (int)boff[g - C::NA], (int)(kt * 128), 0, 0);
+  };
   // quantized B: chunk q = tid + 256 i holds codes 16 (q % 4) .. + 16 of row q / 4
   u32x4 qr[C::QB];
   floatx2 qs[C::QB];
@@ -429,6 +439,10 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
   };
   auto qstore = [&](int buf) {
     char* Bs = smem + buf * C::STAGE + C::ABYTES;
+    // (opaque redefinition here: keeps the compiler from hoisting the
+    // dequantisation, and the wait for the codes, up to the loads)
+#pragma unroll
+    for (int i = 0; i < C::QB; ++i) asm volatile("" : "+v"(qr[i]), "+v"(qs[i]));
 #pragma unroll
     for (int i = 0; i < C::QB; ++i) {
       const int q = tid + 256 * i, r = q >> 2, c2 = 2 * (q & 3);
@@ -471,29 +485,43 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
   rd(smem, 0, 0);
   for (int kt = 0; kt < nk; ++kt) {
     const char* S = smem + (kt & 1) * C::STAGE;
-    if constexpr (QUANT) {
-      if (kt + 1 < nk) qload(kt + 1);
-    }
-    if (kt + 1 < nk) issue(kt + 1, (kt + 1) & 1);
+    // Loads of the next stage into the other buffer (free since the last
+    // barrier). The last stage reloads itself, unused, so that every pass
+    // has the same loads in flight and no wait count depends on a branch.
+    const int ktn = min(kt + 1, nk - 1), nb = (kt + 1) & 1;
+    if constexpr (QUANT) qload(ktn);
+    if constexpr (!C::ILV) issue(ktn, nb);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (s < 3) {
         rd(S, s + 1, (s + 1) & 1);
       } else {
-        if constexpr (QUANT) {
-          if (kt + 1 < nk) qstore((kt + 1) & 1);
-        }
+        if constexpr (QUANT) qstore(nb);
         // this wave's operand reads and its loads of stage kt + 1 are done;
         // after the barrier every wave's are
         __builtin_amdgcn_s_waitcnt(7 << 4);  // vmcnt(0) lgkmcnt(0)
         asm volatile("s_barrier" ::: "memory");
-        if (kt + 1 < nk) rd(smem + ((kt + 1) & 1) * C::STAGE, 0, 0);
+        rd(smem + nb * C::STAGE, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (C::ILV) {
+        // one workgroup per CU: issuing a stage's loads in one burst stalls
+        // the wave while the memory pipe takes them, so sub-steps 0-2 each
+        // place a third of them between their MFMAs
+        constexpr int NM = C::TM * C::TN, ND = C::NA + C::NB, DQ = (ND + 2) / 3, EV = NM / DQ > 0 ? NM / DQ : 1;
 #pragma unroll
-      for (int j = 0; j < C::TN; ++j)
+        for (int m = 0; m < NM; ++m) {
+          const int j = m / C::TM, i = m % C::TM;
+          acc[j][i] = mma32(fb[s & 1][j], fa[s & 1][i], acc[j][i]);
+          if (s < 3 && m % EV == EV - 1 && m / EV < DQ && s * DQ + m / EV < ND) issue1(s * DQ + m / EV, ktn, nb);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
 #pragma unroll
-        for (int i = 0; i < C::TM; ++i) acc[j][i] = mma32(fb[s & 1][j], fa[s & 1][i], acc[j][i]);
+        for (int j = 0; j < C::TN; ++j)
+#pragma unroll
+          for (int i = 0; i < C::TM; ++i) acc[j][i] = mma32(fb[s & 1][j], fa[s & 1][i], acc[j][i]);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -576,14 +604,14 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
 }
 
 // Estimated duration of one launch of the tile kernel, in units of one
-// 192 x 192 tile pass at K = 1024 (measured per-tile times: 256 x 256 1.33,
-// 128 x 128 0.46 alone on a CU and 0.77 for two sharing one).
+// 192 x 192 tile pass at K = 1024 with every CU busy (measured: a 256 x 256
+// pass 1.35, 128 x 128 0.46 alone on a CU and 0.77 for two sharing one).
 template <int BM, int BN>
 double tile_cost(const GemmParams& p) {
   const int64_t tiles = m_tiles<BM>(p) * (p.N / BN);
   double c;
   if (BM == 128 && BN == 128) c = tiles <= 256 ? 0.46 : (double)((tiles + 511) / 512) * 0.77;
-  else c = (double)((tiles + 255) / 256) * (BM * BN == 256 * 256 ? 1.33 : 1.0);
+  else c = (double)((tiles + 255) / 256) * (BM * BN == 256 * 256 ? 1.35 : 1.0);
   return c * p.K / 1024.0;
 }
 
