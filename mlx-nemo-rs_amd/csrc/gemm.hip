@@ -603,6 +603,215 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Split-K kernel for projections with few rows (streaming chunks, short
+// utterances, the position table): too few output tiles to fill 256 CUs, so
+// the contraction is split. Workgroup (tile, z) takes a 64 x 64 output tile
+// over k-columns [z KS, (z + 1) KS), with KS the k-columns of one 512-byte LDS
+// row (128 fp32 or 256 bf16):
+//  * its whole A and B slices (64 rows x 512 bytes each) go to LDS in one
+//    burst of direct-to-LDS loads (quantized B: codes to registers,
+//    dequantised, written), so the workgroup waits on memory once;
+//  * 4 waves of 32 x 32 each, 16x16 MFMAs (fp32 16x16x4 or bf16 16x16x32),
+//    one 16-byte fragment per lane and operand per step; 16-byte chunk c of
+//    LDS row r sits at c ^ (r % 16), which spreads a fragment read's 16 rows
+//    over all 64 banks;
+//  * the raw fp32 sums go to partial[z][M][N], and gemm_reduce sums the
+//    splits in order z = 0, 1, ... and applies the epilogue. (Reducing in the
+//    last workgroup to arrive instead needs agent-scope fences, which on this
+//    chip write back and invalidate the whole L2 per workgroup: measured
+//    20x slower.)
+template <typename T, bool QUANT>
+__global__ __launch_bounds__(256) void gemm_split_kernel(const GemmParams p, int splits) {
+  constexpr int ES = sizeof(T);
+  constexpr int KS = 512 / ES;  // k-columns per workgroup
+  __shared__ __attribute__((aligned(1024))) char smem[2 * 64 * 512];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = w >> 1, wn = w & 1;
+  const int tile = (int)blockIdx.x / splits, z = (int)blockIdx.x % splits;
+  const int tilesN = p.N / 64;
+  const int m0 = tile / tilesN * 64, n0 = tile % tilesN * 64, k0 = z * KS;
+
+  // A rows [m0, M): 8 loads per wave of 64 x 16 bytes (rows past M read zero)
+  const char* Ab = reinterpret_cast<const char*>(p.A) + ((int64_t)m0 * p.lda + k0) * ES;
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)Ab, (short)0, (int)(((int64_t)(p.M - m0) * p.lda - k0) * ES), kRawBuffer);
+#pragma unroll
+  for (int g = 0; g < 8; ++g) {
+    const int pos = (w * 8 + g) * 64 + lane, row = pos >> 5;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(smem + (w * 8 + g) * 1024), 16,
+                                             (int)(row * p.lda * ES + 16 * ((pos & 31) ^ (row & 15))), 0, 0, 0);
+  }
+  char* Bs = smem + 64 * 512;
+  if constexpr (!QUANT) {
+    const char* Bb = reinterpret_cast<const char*>(p.W) + ((int64_t)n0 * p.K + k0) * ES;
+    const __amdgpu_buffer_rsrc_t rb =
+        __builtin_amdgcn_make_buffer_rsrc((void*)Bb, (short)0, (int)(((int64_t)64 * p.K - k0) * ES), kRawBuffer);
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const int pos = (w * 8 + g) * 64 + lane, row = pos >> 5;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(Bs + (w * 8 + g) * 1024), 16,
+                                               (int)(row * p.K * ES + 16 * ((pos & 31) ^ (row & 15))), 0, 0, 0);
+    }
+  } else {
+    // 16 codes -> 16 values = ES 16-byte LDS chunks; KS / 16 code chunks per row
+    constexpr int CPR = KS / 16, QN = 64 * CPR / 256;
+    const unsigned char* Wq = reinterpret_cast<const unsigned char*>(p.W);
+    const int groups = p.K / 64;
+    u32x4 qr[QN];
+    floatx2 qs[QN];
+#pragma unroll
+    for (int i = 0; i < QN; ++i) {
+      const int q = tid + 256 * i, r = q / CPR, k = k0 + (q % CPR) * 16;
+      qr[i] = *reinterpret_cast<const u32x4*>(Wq + (int64_t)(n0 + r) * p.K + k);
+      qs[i] = *reinterpret_cast<const floatx2*>(p.sb + 2 * ((int64_t)(n0 + r) * groups + k / 64));
+    }
+#pragma unroll
+    for (int i = 0; i < QN; ++i) {
+      const int q = tid + 256 * i, r = q / CPR, cc = q % CPR;
+      T v[16];
+      dequant16<T>(qr[i], qs[i].x, qs[i].y, v);
+#pragma unroll
+      for (int e = 0; e < ES; ++e)
+        *reinterpret_cast<u32x4*>(Bs + r * 512 + 16 * ((cc * ES + e) ^ (r & 15))) = reinterpret_cast<const u32x4*>(v)[e];
+    }
+  }
+  __syncthreads();  // (waits for this wave's loads first)
+
+  // wave (wm, wn): rows 32 wm + 16 i + lane % 16 of A, 32 wn + 16 j + lane % 16
+  // of B; step s reads logical chunk 4 s + lane / 16 of each row
+  using F = typename Frag<T>::type;
+  floatx4 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{};
+  const char* Ar = smem + (wm * 32 + (lane & 15)) * 512;
+  const char* Br = Bs + (wn * 32 + (lane & 15)) * 512;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int off = 16 * ((4 * s + (lane >> 4)) ^ (lane & 15));
+    F a[2], b[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      a[t] = *reinterpret_cast<const F*>(Ar + t * 16 * 512 + off);
+      b[t] = *reinterpret_cast<const F*>(Br + t * 16 * 512 + off);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) acc[i][j] = mma16(a[i], b[j], acc[i][j]);
+  }
+
+  // raw fp32 sums to partial[z][M][N]; gemm_reduce sums the splits in order
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int row = m0 + wm * 32 + i * 16 + 4 * (lane >> 4) + e;
+      if (row >= p.M) continue;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        p.partial[((int64_t)z * p.M + row) * p.N + n0 + wn * 32 + j * 16 + (lane & 15)] = acc[i][j][e];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 projections with few rows (the streaming chunk's 224 rows, one short
+// utterance): fp32 MFMA throughput bounds them (157 TFLOP/s), so every SIMD
+// must take an equal share, with no second kernel to sum K splits. A
+// workgroup of NW = K / 64 waves computes a 32 x 32 output tile; wave w takes
+// k-columns [64 w, 64 w + 64):
+//  * its A and B fragments for 16x16x4 MFMAs (lane l: row l % 16, k 4 (l / 16)
+//    + [0, 4) of each 16-wide step) load straight into registers, all
+//    32 loads issued at once (rows past M read row M - 1 and are not stored);
+//    quantized B loads 4 codes per lane and step and dequantises them;
+//  * 64 MFMAs per wave (2 x 2 tiles of 16 x 16, 4 steps of 16);
+//  * the waves' accumulators meet in LDS and thread t sums element t over
+//    the waves in order w = 0, 1, ..., then applies the epilogue.
+template <bool QUANT>
+__global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
+  __shared__ __attribute__((aligned(16))) float red[16][64 * 16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), nw = (int)blockDim.x >> 6;
+  const int tilesN = p.N / 32;
+  const int m0 = (int)blockIdx.x / tilesN * 32, n0 = (int)blockIdx.x % tilesN * 32;
+  const int k0 = w * 64 + 4 * (lane >> 4);
+  floatx4 a[2][4], b[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const float* ar = reinterpret_cast<const float*>(p.A) + (int64_t)min(m0 + 16 * t + (lane & 15), p.M - 1) * p.lda + k0;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) a[t][s] = *reinterpret_cast<const floatx4*>(ar + 16 * s);
+  }
+  if constexpr (!QUANT) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const float* br = reinterpret_cast<const float*>(p.W) + (int64_t)(n0 + 16 * u + (lane & 15)) * p.K + k0;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) b[u][s] = *reinterpret_cast<const floatx4*>(br + 16 * s);
+    }
+  } else {
+    // the wave's 64 k-columns are one quantization group
+    const int groups = p.K / 64;
+    uint32_t q[2][4];
+    floatx2 sb[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int n = n0 + 16 * u + (lane & 15);
+      const unsigned char* cr = reinterpret_cast<const unsigned char*>(p.W) + (int64_t)n * p.K + k0;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) q[u][s] = *reinterpret_cast<const uint32_t*>(cr + 16 * s);
+      sb[u] = *reinterpret_cast<const floatx2*>(p.sb + 2 * ((int64_t)n * groups + w));
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) b[u][s][e] = __builtin_fmaf(sb[u].x, (float)((q[u][s] >> (8 * e)) & 0xFFu), sb[u].y);
+  }
+  floatx4 acc[2][2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      acc[t][u] = floatx4{};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) acc[t][u] = mma16(a[t][s], b[u][s], acc[t][u]);
+    }
+  // element r = 4 (2 t + u) + e of lane l: row 16 t + 4 (l / 16) + e, column 16 u + l % 16
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int u = 0; u < 2; ++u) *reinterpret_cast<floatx4*>(&red[w][lane * 16 + 4 * (2 * t + u)]) = acc[t][u];
+  __syncthreads();
+  for (int idx = tid; idx < 64 * 16; idx += (int)blockDim.x) {
+    float v = 0.f;
+    for (int ww = 0; ww < nw; ++ww) v += red[ww][idx];
+    const int l = idx >> 4, r = idx & 15, tu = r >> 2, e = r & 3;
+    const int row = m0 + 16 * (tu >> 1) + 4 * (l >> 4) + e, col = n0 + 16 * (tu & 1) + (l & 15);
+    if (row < p.M) reinterpret_cast<float*>(p.C)[row_offset(p, row) + col] = epilogue_value<float>(p, row, col, v);
+  }
+}
+
+// The split kernel applies when the scratch holds every split's sums and its
+// operand rows can be loaded as 16-byte chunks.
+template <typename T>
+int split_count(const GemmParams& p) {
+  constexpr int KS = 512 / (int)sizeof(T);
+  if (!p.partial || p.vt || p.K % KS || p.N % 64) return 0;
+  if ((p.lda * (int64_t)sizeof(T)) % 16 || (p.K * (int64_t)sizeof(T)) % 16) return 0;
+  if ((reinterpret_cast<uintptr_t>(p.A) | reinterpret_cast<uintptr_t>(p.W)) & 15) return 0;
+  if ((int64_t)p.M * p.lda * (int64_t)sizeof(T) >= ((int64_t)1 << 31) ||
+      (int64_t)p.N * p.K * (int64_t)sizeof(T) >= ((int64_t)1 << 31))
+    return 0;
+  const int splits = p.K / KS;
+  if ((int64_t)splits * p.M * p.N > p.partial_elems) return 0;
+  return splits;
+}
+
 // Estimated duration of one launch of the tile kernel, in units of one
 // 192 x 192 tile pass at K = 1024 with every CU busy (measured: a 256 x 256
 // pass 1.35, 128 x 128 0.46 alone on a CU and 0.77 for two sharing one).
@@ -678,6 +887,27 @@ hipError_t dispatch(const GemmParams& p, hipStream_t s) {
     return launch<T, QUANT, 256, 256, 4, 2>(p, 1, s);
   if (m_tiles<128>(p) * (p.N / 128) >= 384 && p.N % 128 == 0) return launch<T, QUANT, 128, 128, 2, 2>(p, 1, s);
   if (p.vt) return launch<T, QUANT, 128, 128, 2, 2>(p, 1, s);  // V^T epilogue needs whole 128-row tiles
+  if constexpr (sizeof(T) == 4) {
+    // few rows of fp32: K-parallel workgroups, no second kernel
+    if (p.K % 64 == 0 && p.K <= 1024 && p.N % 32 == 0 && !p.vt && p.lda % 4 == 0 && p.K % 4 == 0 &&
+        ((reinterpret_cast<uintptr_t>(p.A) | reinterpret_cast<uintptr_t>(p.W)) & 15) == 0 &&
+        (int64_t)((p.M + 31) / 32) * (p.N / 32) <= 4096) {
+      const unsigned grid = (unsigned)(((p.M + 31) / 32) * (p.N / 32));
+      hipLaunchKernelGGL((gemm_kpar_kernel<QUANT>), dim3(grid), dim3(64 * (p.K / 64)), 0, s, p);
+      return hipGetLastError();
+    }
+  }
+  if (const int splits = split_count<T>(p)) {
+    const int64_t tiles = (int64_t)((p.M + 63) / 64) * (p.N / 64);
+    hipLaunchKernelGGL((gemm_split_kernel<T, QUANT>), dim3((unsigned)(tiles * splits)), dim3(256), 0, s, p, splits);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // (also for one split: the reduce kernel applies the epilogue)
+    const int64_t total = (int64_t)p.M * p.N;
+    const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 4096);
+    hipLaunchKernelGGL(gemm_reduce<T>, dim3(blocks), dim3(256), 0, s, p, splits);
+    return hipGetLastError();
+  }
   // Small problem: 64x64 tiles, and K splits until ~512 workgroups.
   const int64_t tiles = m_tiles<64>(p) * (p.N / 64);
   int splits = 1;
