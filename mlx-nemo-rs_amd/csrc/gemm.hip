@@ -3,22 +3,26 @@
 // Replaces `LinearLayer::forward` (quantization.rs:126-162): y = x W^T + b for
 // standard weights and MLX `quantized_matmul(transpose=true, group 64, 8 bit)`
 // + b for affine-u8 weights, where the u8 codes are dequantised in registers
-// on their way into LDS and feed the same MFMA tiles as dense weights.
+// on their way to the MFMAs and no dequantised weight reaches HBM.
 //
-// Tiling (gfx950): a BM x BN output tile per workgroup of NWM x NWN waves. One
-// K step moves 128 bytes per row (64 bf16 or 32 fp32), double-buffered in LDS
-// with a 16-byte row pad (no pad costs 1.7x in bank conflicts); the next
-// step's global loads are in flight while the MFMAs of the current one run.
-// bf16 uses 32x32x16 MFMAs (one 16-byte A and B fragment per 32x32x16 step),
-// fp32 four 16x16x4 MFMAs per 16-byte fragment pair. Tile shapes by size:
-// 256x256 with 8 waves for large problems, 128x128 with 4 waves otherwise, and
-// 64x64 tiles with a deterministic split over K when even those cannot fill
-// 256 CUs (short sequences, streaming chunks, the position table): each split
-// writes fp32 partials and a second kernel sums them in split order.
+// Kernels, by problem (gfx950, 256 CUs):
+//  * gemm_tile_kernel: bf16 projections with enough rows to fill the GPU
+//    (128x128, 192x192 or 256x256 tiles on 4 waves, direct-to-LDS operand
+//    streams, LDS-staged epilogue; described at its definition).
+//  * gemm_kpar_kernel: fp32 projections of few rows (the streaming chunk,
+//    one short utterance): the contraction split over the 16 waves of a
+//    workgroup and summed in LDS.
+//  * gemm_split_kernel + gemm_reduce: bf16 projections of few rows (the
+//    position table of a short utterance): K split over workgroups, the
+//    partial sums added in split order by a second kernel.
+//  * gemm_kernel: everything else (large fp32 problems; bf16 shapes the tile
+//    kernel does not take): BM x BN tiles on NWM x NWN waves, one 128-byte
+//    K step per LDS stage, double-buffered with a 16-byte row pad; an
+//    optional deterministic K split with gemm_reduce.
 //
 // With seg_T > 0 the M tiles are laid out per utterance (rows b*seg_T ..
 // (b+1)*seg_T, never straddling two), so the V projection can be written
-// transposed ([D][B*Tpad], tokens contiguous) through LDS with 16-byte stores.
+// transposed ([D][B*Tpad], tokens contiguous) with 16-byte stores.
 #include <type_traits>
 
 #include "common.hpp"
