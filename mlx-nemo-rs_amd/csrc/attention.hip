@@ -367,6 +367,7 @@ struct Cfg2 {
   static constexpr int RPL = 1024 / RB;              // position rows per 1 KB load
   static constexpr int PDMA = 64 / RPL / NW;         // position loads per wave for 64 rows
   static_assert(KDMA * NW * 1024 == KBUF && VDMA * NW * 1024 == VBUF && PDMA * NW * RPL == 64, "tile split");
+  static_assert(KDMA + VDMA <= NS && PDMA + 1 <= NS, "one load per band / score MFMA step");
   static_assert(LDS <= 160 * 1024, "LDS");
 };
 
@@ -488,6 +489,27 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(Vt + (w * C::VDMA + g) * 1024), 16, (int)voff[g], j0 * 2, 0,
                                                0);
   };
+  // single loads of the same streams: load g of this wave's K and V^T share
+  // of key tile jn into buffer bn; load g of its ring share (g == PDMA: the
+  // offsets, wave 0)
+  auto dma_kv = [&](int g, int jn, int bn) {
+    if (g < C::KDMA)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(smem + C::K_OFF + bn * C::KBUF + (w * C::KDMA + g) * 1024), 16,
+                                               (int)koff[g], jn * (int)p.kv_rs * 2, 0, 0);
+    else
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(smem + C::V_OFF + bn * C::VBUF + (w * C::VDMA + g - C::KDMA) * 1024),
+                                               16, (int)voff[g - C::KDMA], jn * 2, 0, 0);
+  };
+  auto dma_ring = [&](int g, int rr0) {
+    const int n0 = R0 + rr0 + p.p_pad;
+    if (g < C::PDMA)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rp, (lds_void*)(smem + C::P_OFF + ((rr0 + (w * C::PDMA + g) * C::RPL) % C::RING) * RB), 16, (int)roff[g],
+          n0 * (int)p.p_rs * 2, 0, 0);
+    else if (w == 0)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void*)(smem + C::D_OFF + (rr0 % C::RING) * 4), 4, lane * 4,
+                                               n0 * 4, 0, 0);
+  };
   // Ring rows [rr0, rr0 + 64) (rr0 a multiple of 64): this wave's share of
   // the position rows, and (wave 0) their offsets. Rows outside the table
   // read the p_pad slack around it (finite; the offsets there are zero).
@@ -575,10 +597,11 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   for (int j0 = jfirst; j0 < jend; j0 += NK, buf ^= 1) {
     const bool more = j0 + NK < jend;
     // the next key tile and its 64 new ring rows (last read before the
-    // previous barrier; awaited at the next one). The last tile reloads
-    // itself, unused, so that every iteration issues the same loads.
-    load_tile(more ? j0 + NK : j0, buf ^ 1);
-    load_ring(rrw + 32 * w + 96);
+    // previous barrier; awaited at the next one), issued one load per MFMA
+    // step of the band and score loops below: in one burst they stall the
+    // wave while the memory pipe takes them. The last tile reloads itself,
+    // unused, so that every iteration issues the same loads.
+    const int jn = more ? j0 + NK : j0, rr0n = rrw + 32 * w + 96;
 
     // Band tiles first, each stored to the remap strip as soon as it is
     // done (rel_shift: strip column n of query column c pairs with key
@@ -606,6 +629,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
           a1[st % PF] = *reinterpret_cast<const bf16x8*>(r1 + lo[st + PF]);
           a2[st % PF] = *reinterpret_cast<const bf16x8*>(r2 + lo[st + PF]);
         }
+        if (st < C::KDMA + C::VDMA) dma_kv(st, jn, buf ^ 1);
         __builtin_amdgcn_sched_barrier(0);
       }
       put(pack(b1), 1);
@@ -632,6 +656,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 #pragma unroll
           for (int u = 0; u < 2; ++u)
             ka[st % PF][u] = *reinterpret_cast<const bf16x8*>(Ks + 32 * u * RB + lo[st + PF]);
+        if (st <= C::PDMA) dma_ring(st, rr0n);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
