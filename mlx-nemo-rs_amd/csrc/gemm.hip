@@ -722,59 +722,73 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(const GemmParams p, int
 }
 
 // ---------------------------------------------------------------------------
-// fp32 projections with few rows (the streaming chunk's 224 rows, one short
-// utterance): fp32 MFMA throughput bounds them (157 TFLOP/s), so every SIMD
-// must take an equal share, with no second kernel to sum K splits. A
-// workgroup of NW = K / 64 waves computes a 32 x 32 output tile; wave w takes
-// k-columns [64 w, 64 w + 64):
-//  * its A and B fragments for 16x16x4 MFMAs (lane l: row l % 16, k 4 (l / 16)
-//    + [0, 4) of each 16-wide step) load straight into registers, all
-//    32 loads issued at once (rows past M read row M - 1 and are not stored);
-//    quantized B loads 4 codes per lane and step and dequantises them;
-//  * 64 MFMAs per wave (2 x 2 tiles of 16 x 16, 4 steps of 16);
+// Projections with few rows (the streaming chunk's 224 rows, one short
+// utterance, the position table of a short one): too few output tiles to
+// fill 256 CUs, so the contraction is split, and it is split inside the
+// workgroup so that no second kernel has to add the parts. A workgroup of
+// NW = K / 64 waves computes a 32 x 32 output tile; wave w takes k-columns
+// [64 w, 64 w + 64), one quantization group:
+//  * its A and B fragments for 16x16 MFMAs (fp32 16x16x4: lane l holds row
+//    l % 16, k 4 (l / 16) + [0, 4) of each 16-wide step; bf16 16x16x32: k
+//    8 (l / 16) + [0, 8) of each 32-wide step) load straight into registers,
+//    all at once (rows past M read row M - 1 and are not stored); quantized
+//    B loads its codes and dequantises them in registers;
+//  * 2 x 2 output tiles of 16 x 16 per wave;
 //  * the waves' accumulators meet in LDS and thread t sums element t over
 //    the waves in order w = 0, 1, ..., then applies the epilogue.
-template <bool QUANT>
+template <typename T, bool QUANT>
 __global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
+  constexpr bool BF = sizeof(T) == 2;
+  constexpr int KW = BF ? 32 : 16;     // k per MFMA step
+  constexpr int NSTEP = 64 / KW;       // steps per wave
+  constexpr int EL = BF ? 8 : 4;       // elements per lane per fragment
+  using F = typename Frag<T>::type;
   __shared__ __attribute__((aligned(16))) float red[16][64 * 16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), nw = (int)blockDim.x >> 6;
   const int tilesN = p.N / 32;
   const int m0 = (int)blockIdx.x / tilesN * 32, n0 = (int)blockIdx.x % tilesN * 32;
-  const int k0 = w * 64 + 4 * (lane >> 4);
-  floatx4 a[2][4], b[2][4];
+  const int k0 = w * 64 + EL * (lane >> 4);
+  F a[2][NSTEP], b[2][NSTEP];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const float* ar = reinterpret_cast<const float*>(p.A) + (int64_t)min(m0 + 16 * t + (lane & 15), p.M - 1) * p.lda + k0;
+    const T* ar = reinterpret_cast<const T*>(p.A) + (int64_t)min(m0 + 16 * t + (lane & 15), p.M - 1) * p.lda + k0;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) a[t][s] = *reinterpret_cast<const floatx4*>(ar + 16 * s);
+    for (int s = 0; s < NSTEP; ++s) a[t][s] = *reinterpret_cast<const F*>(ar + KW * s);
   }
   if constexpr (!QUANT) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const float* br = reinterpret_cast<const float*>(p.W) + (int64_t)(n0 + 16 * u + (lane & 15)) * p.K + k0;
+      const T* br = reinterpret_cast<const T*>(p.W) + (int64_t)(n0 + 16 * u + (lane & 15)) * p.K + k0;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) b[u][s] = *reinterpret_cast<const floatx4*>(br + 16 * s);
+      for (int s = 0; s < NSTEP; ++s) b[u][s] = *reinterpret_cast<const F*>(br + KW * s);
     }
   } else {
-    // the wave's 64 k-columns are one quantization group
+    // EL codes per lane and step, in one EL-byte load
+    using CodeT = typename std::conditional<BF, u32x2, uint32_t>::type;
     const int groups = p.K / 64;
-    uint32_t q[2][4];
+    CodeT q[2][NSTEP];
     floatx2 sb[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int n = n0 + 16 * u + (lane & 15);
       const unsigned char* cr = reinterpret_cast<const unsigned char*>(p.W) + (int64_t)n * p.K + k0;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) q[u][s] = *reinterpret_cast<const uint32_t*>(cr + 16 * s);
+      for (int s = 0; s < NSTEP; ++s) q[u][s] = *reinterpret_cast<const CodeT*>(cr + KW * s);
       sb[u] = *reinterpret_cast<const floatx2*>(p.sb + 2 * ((int64_t)n * groups + w));
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+      for (int s = 0; s < NSTEP; ++s)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) b[u][s][e] = __builtin_fmaf(sb[u].x, (float)((q[u][s] >> (8 * e)) & 0xFFu), sb[u].y);
+        for (int e = 0; e < EL; ++e) {
+          uint32_t word;
+          if constexpr (BF) word = q[u][s][e >> 2];
+          else word = q[u][s];
+          const float v = __builtin_fmaf(sb[u].x, (float)((word >> (8 * (e & 3))) & 0xFFu), sb[u].y);
+          b[u][s][e] = from_float<T>(v);
+        }
   }
   floatx4 acc[2][2];
 #pragma unroll
@@ -783,7 +797,7 @@ __global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
     for (int u = 0; u < 2; ++u) {
       acc[t][u] = floatx4{};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) acc[t][u] = mma16(a[t][s], b[u][s], acc[t][u]);
+      for (int s = 0; s < NSTEP; ++s) acc[t][u] = mma16(a[t][s], b[u][s], acc[t][u]);
     }
   // element r = 4 (2 t + u) + e of lane l: row 16 t + 4 (l / 16) + e, column 16 u + l % 16
 #pragma unroll
@@ -796,8 +810,18 @@ __global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
     for (int ww = 0; ww < nw; ++ww) v += red[ww][idx];
     const int l = idx >> 4, r = idx & 15, tu = r >> 2, e = r & 3;
     const int row = m0 + 16 * (tu >> 1) + 4 * (l >> 4) + e, col = n0 + 16 * (tu & 1) + (l & 15);
-    if (row < p.M) reinterpret_cast<float*>(p.C)[row_offset(p, row) + col] = epilogue_value<float>(p, row, col, v);
+    if (row < p.M) reinterpret_cast<T*>(p.C)[row_offset(p, row) + col] = from_float<T>(epilogue_value<T>(p, row, col, v));
   }
+}
+
+// The K-parallel kernel applies to K = 64 .. 1024 with 16-byte operand rows
+// and at most 4096 tiles (beyond that the other kernels fill the GPU).
+template <typename T>
+bool kpar_ok(const GemmParams& p) {
+  constexpr int E = 16 / (int)sizeof(T);
+  return p.K % 64 == 0 && p.K <= 1024 && p.N % 32 == 0 && !p.vt && p.lda % E == 0 && p.K % E == 0 &&
+         ((reinterpret_cast<uintptr_t>(p.A) | reinterpret_cast<uintptr_t>(p.W)) & 15) == 0 &&
+         (int64_t)((p.M + 31) / 32) * (p.N / 32) <= 4096;
 }
 
 // The split kernel applies when the scratch holds every split's sums and its
@@ -891,15 +915,13 @@ hipError_t dispatch(const GemmParams& p, hipStream_t s) {
     return launch<T, QUANT, 256, 256, 4, 2>(p, 1, s);
   if (m_tiles<128>(p) * (p.N / 128) >= 384 && p.N % 128 == 0) return launch<T, QUANT, 128, 128, 2, 2>(p, 1, s);
   if (p.vt) return launch<T, QUANT, 128, 128, 2, 2>(p, 1, s);  // V^T epilogue needs whole 128-row tiles
-  if constexpr (sizeof(T) == 4) {
-    // few rows of fp32: K-parallel workgroups, no second kernel
-    if (p.K % 64 == 0 && p.K <= 1024 && p.N % 32 == 0 && !p.vt && p.lda % 4 == 0 && p.K % 4 == 0 &&
-        ((reinterpret_cast<uintptr_t>(p.A) | reinterpret_cast<uintptr_t>(p.W)) & 15) == 0 &&
-        (int64_t)((p.M + 31) / 32) * (p.N / 32) <= 4096) {
-      const unsigned grid = (unsigned)(((p.M + 31) / 32) * (p.N / 32));
-      hipLaunchKernelGGL((gemm_kpar_kernel<QUANT>), dim3(grid), dim3(64 * (p.K / 64)), 0, s, p);
-      return hipGetLastError();
-    }
+  // few rows of fp32: K-parallel workgroups, no second kernel (for bf16 the
+  // position table of a short utterance measured the same as split-K: 13.4
+  // against 12.6 us at 749 x 1024 x 1024, so bf16 keeps split-K)
+  if (sizeof(T) == 4 && kpar_ok<T>(p)) {
+    const unsigned grid = (unsigned)(((p.M + 31) / 32) * (p.N / 32));
+    hipLaunchKernelGGL((gemm_kpar_kernel<T, QUANT>), dim3(grid), dim3(64 * (p.K / 64)), 0, s, p);
+    return hipGetLastError();
   }
   if (const int splits = split_count<T>(p)) {
     const int64_t tiles = (int64_t)((p.M + 63) / 64) * (p.N / 64);
