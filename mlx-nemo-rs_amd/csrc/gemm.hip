@@ -429,32 +429,30 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(S + C::ABYTES + (w * C::NB + g - C::NA) * 1024), 16,
                                                (int)boff[g - C::NA], (int)(kt * 128), 0, 0);
   };
-  // quantized B: chunk q = tid + 256 i holds codes 16 (q % 4) .. + 16 of row q / 4
-  u32x4 qr[C::QB];
-  floatx2 qs[C::QB];
+  // quantized B: chunk q = tid + 256 i holds codes 16 (q % 4) .. + 16 of row q / 4.
+  // Codes of stage s load into register set s % 2 two stages ahead and are
+  // dequantised into LDS during stage s - 1, between its MFMAs.
+  u32x4 qr[2][C::QB];
+  floatx2 qs[2][C::QB];
   const int groups = p.K / 64;
-  auto qload = [&](int kt) {
+  auto qload = [&](int kt, int set) {
 #pragma unroll
     for (int i = 0; i < C::QB; ++i) {
       const int q = tid + 256 * i, r = q >> 2;
-      qr[i] = *reinterpret_cast<const u32x4*>(Bb + (int64_t)r * p.K + kt * 64 + (q & 3) * 16);
-      qs[i] = *reinterpret_cast<const floatx2*>(p.sb + 2 * ((int64_t)(n0 + r) * groups + kt));
+      qr[set][i] = *reinterpret_cast<const u32x4*>(Bb + (int64_t)r * p.K + kt * 64 + (q & 3) * 16);
+      qs[set][i] = *reinterpret_cast<const floatx2*>(p.sb + 2 * ((int64_t)(n0 + r) * groups + kt));
     }
   };
-  auto qstore = [&](int buf) {
+  auto qstore = [&](int i, int set, int buf) {
     char* Bs = smem + buf * C::STAGE + C::ABYTES;
     // (opaque redefinition here: keeps the compiler from hoisting the
     // dequantisation, and the wait for the codes, up to the loads)
-#pragma unroll
-    for (int i = 0; i < C::QB; ++i) asm volatile("" : "+v"(qr[i]), "+v"(qs[i]));
-#pragma unroll
-    for (int i = 0; i < C::QB; ++i) {
-      const int q = tid + 256 * i, r = q >> 2, c2 = 2 * (q & 3);
-      bf16 v[16];
-      dequant16<bf16>(qr[i], qs[i].x, qs[i].y, v);
-      *reinterpret_cast<u32x4*>(Bs + r * 128 + 16 * (c2 ^ ((r >> 1) & 7))) = reinterpret_cast<const u32x4*>(v)[0];
-      *reinterpret_cast<u32x4*>(Bs + r * 128 + 16 * ((c2 + 1) ^ ((r >> 1) & 7))) = reinterpret_cast<const u32x4*>(v)[1];
-    }
+    asm volatile("" : "+v"(qr[set][i]), "+v"(qs[set][i]));
+    const int q = tid + 256 * i, r = q >> 2, c2 = 2 * (q & 3);
+    bf16 v[16];
+    dequant16<bf16>(qr[set][i], qs[set][i].x, qs[set][i].y, v);
+    *reinterpret_cast<u32x4*>(Bs + r * 128 + 16 * (c2 ^ ((r >> 1) & 7))) = reinterpret_cast<const u32x4*>(v)[0];
+    *reinterpret_cast<u32x4*>(Bs + r * 128 + 16 * ((c2 + 1) ^ ((r >> 1) & 7))) = reinterpret_cast<const u32x4*>(v)[1];
   };
 
   // fragment (t, s): rows 32 t + lane % 32 of this wave's block, k-chunk
@@ -474,8 +472,10 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
   const int nk = p.K / 64;
   issue(0, 0);
   if constexpr (QUANT) {
-    qload(0);
-    qstore(0);
+    qload(0, 0);
+    qload(min(1, nk - 1), 1);
+#pragma unroll
+    for (int i = 0; i < C::QB; ++i) qstore(i, 0, 0);
   }
   __syncthreads();
 
@@ -486,49 +486,72 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
 #pragma unroll
     for (int j = 0; j < C::TN; ++j) fb[b][j] = *reinterpret_cast<const bf16x8*>(S + brow + j * 4096 + so[s]);
   };
-  rd(smem, 0, 0);
-  for (int kt = 0; kt < nk; ++kt) {
-    const char* S = smem + (kt & 1) * C::STAGE;
-    // Loads of the next stage into the other buffer (free since the last
-    // barrier). The last stage reloads itself, unused, so that every pass
-    // has the same loads in flight and no wait count depends on a branch.
-    const int ktn = min(kt + 1, nk - 1), nb = (kt + 1) & 1;
-    if constexpr (QUANT) qload(ktn);
+  // Stage kt (par = kt % 2, a literal at each call so register sets stay
+  // static). Loads of the next stage go to the other buffer (free since the
+  // last barrier); the last stage reloads itself, unused, so that every pass
+  // has the same loads in flight and no wait count depends on a branch.
+  auto stage = [&](int kt, int par) {
+    const char* S = smem + par * C::STAGE;
+    const int ktn = min(kt + 1, nk - 1), nb = par ^ 1;
+    if constexpr (QUANT) qload(min(kt + 2, nk - 1), par);  // set par held stage kt, stored during kt - 1
     if constexpr (!C::ILV) issue(ktn, nb);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (s < 3) {
         rd(S, s + 1, (s + 1) & 1);
       } else {
-        if constexpr (QUANT) qstore(nb);
-        // this wave's operand reads and its loads of stage kt + 1 are done;
-        // after the barrier every wave's are
+        // this wave's operand reads and its loads and stores of stage kt + 1
+        // are done; after the barrier every wave's are
         __builtin_amdgcn_s_waitcnt(7 << 4);  // vmcnt(0) lgkmcnt(0)
         asm volatile("s_barrier" ::: "memory");
         rd(smem + nb * C::STAGE, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
+      // quantized chunks of stage kt + 1 dequantised in sub-steps 0-2, after
+      // the first half of the sub-step's MFMAs (chunk i in sub-step i % 3)
+      auto qpart = [&]() {
+        if constexpr (QUANT) {
+#pragma unroll
+          for (int i = 0; i < C::QB; ++i)
+            if (s < 3 && i % 3 == s) qstore(i, par ^ 1, nb);
+        }
+      };
+      constexpr int NM = C::TM * C::TN;
       if constexpr (C::ILV) {
         // one workgroup per CU: issuing a stage's loads in one burst stalls
         // the wave while the memory pipe takes them, so sub-steps 0-2 each
         // place a third of them between their MFMAs
-        constexpr int NM = C::TM * C::TN, ND = C::NA + C::NB, DQ = (ND + 2) / 3, EV = NM / DQ > 0 ? NM / DQ : 1;
+        constexpr int ND = C::NA + C::NB, DQ = (ND + 2) / 3, EV = NM / DQ > 0 ? NM / DQ : 1;
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
           const int j = m / C::TM, i = m % C::TM;
           acc[j][i] = mma32(fb[s & 1][j], fa[s & 1][i], acc[j][i]);
           if (s < 3 && m % EV == EV - 1 && m / EV < DQ && s * DQ + m / EV < ND) issue1(s * DQ + m / EV, ktn, nb);
+          if (m == NM / 2 - 1) qpart();
           __builtin_amdgcn_sched_barrier(0);
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < C::TN; ++j)
-#pragma unroll
-          for (int i = 0; i < C::TM; ++i) acc[j][i] = mma32(fb[s & 1][j], fa[s & 1][i], acc[j][i]);
+        for (int m = 0; m < NM; ++m) {
+          const int j = m / C::TM, i = m % C::TM;
+          acc[j][i] = mma32(fb[s & 1][j], fa[s & 1][i], acc[j][i]);
+          if (m == NM / 2 - 1) {
+            __builtin_amdgcn_sched_barrier(0);
+            qpart();
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+  };
+  rd(smem, 0, 0);
+  int kt = 0;
+  for (; kt + 1 < nk; kt += 2) {
+    stage(kt, 0);
+    stage(kt + 1, 1);
   }
+  if (kt < nk) stage(kt, 0);
 
   // Stage T(acc) row-major: lane holds row 32 i + lane % 32 of the block and
   // columns 32 j + 8 q + 4 (lane / 32) + [0, 4).
