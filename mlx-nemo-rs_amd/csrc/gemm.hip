@@ -350,8 +350,10 @@ __host__ __device__ int64_t m_tiles(const GemmParams& p) {
 // 16-byte runs: rows to C (bias, residual and the ring row remap applied per
 // run), or, for columns at or past vt_col0, 8-token runs of V^T read down the
 // staged columns.
-template <int BM, int BN, bool QUANT>
+template <int BM, int BN, bool QUANT, int NS_>
 struct TileCfg {
+  static constexpr int NS = NS_;                   // LDS stages; loads run NS - 1 stages ahead
+  static constexpr int DIST = NS - 1;
   static constexpr int WM = BM / 2, WN = BN / 2;  // per-wave block
   static constexpr int TM = WM / 32, TN = WN / 32;
   static constexpr int ABYTES = BM * 128, STAGE = (BM + BN) * 128;
@@ -359,17 +361,18 @@ struct TileCfg {
   static constexpr int NB = QUANT ? 0 : BN / 32;   // dense B loads per wave per stage
   static constexpr int QB = BN / 64;               // quantized 16-code chunks per thread per stage
   static constexpr int OP = WN * 2 + 16;           // staged output row pitch (bytes)
-  static constexpr bool ILV = BM * BN >= 192 * 192;  // loads spread between MFMAs (one workgroup per CU)
-  static constexpr int LDS = 2 * STAGE > 4 * WM * OP ? 2 * STAGE : 4 * WM * OP;
+  // loads spread between MFMAs whenever the tile has a CU to itself
+  static constexpr bool ILV = BM * BN >= 192 * 192 || NS > 2;
+  static constexpr int LDS = NS * STAGE > 4 * WM * OP ? NS * STAGE : 4 * WM * OP;
   static_assert(LDS <= 160 * 1024, "tile exceeds LDS");
 };
 
 typedef __attribute__((address_space(3))) void lds_void;
 constexpr int kRawBuffer = 0x00020000;  // buffer descriptor dword 3: untyped 32-bit data
 
-template <int BM, int BN, bool QUANT>
+template <int BM, int BN, bool QUANT, int NS>
 __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
-  using C = TileCfg<BM, BN, QUANT>;
+  using C = TileCfg<BM, BN, QUANT, NS>;
   __shared__ __attribute__((aligned(1024))) char smem[C::LDS];
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -454,6 +457,25 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
     *reinterpret_cast<u32x4*>(Bs + r * 128 + 16 * (c2 ^ ((r >> 1) & 7))) = reinterpret_cast<const u32x4*>(v)[0];
     *reinterpret_cast<u32x4*>(Bs + r * 128 + 16 * ((c2 + 1) ^ ((r >> 1) & 7))) = reinterpret_cast<const u32x4*>(v)[1];
   };
+  // The same work cut into 9 pieces per chunk (8 pairs of codes, then the two
+  // stores), so that it can sit between MFMAs without starving them.
+  bf16 qv[C::QB][16];
+  auto qpiece = [&](int i, int k, int set, int buf) {
+    if (k == 0) asm volatile("" : "+v"(qr[set][i]), "+v"(qs[set][i]));
+    if (k < 8) {
+#pragma unroll
+      for (int e = 2 * k; e < 2 * k + 2; ++e) {
+        const float code = (float)((qr[set][i][e >> 2] >> (8 * (e & 3))) & 0xFFu);
+        qv[i][e] = (bf16)__builtin_fmaf(qs[set][i].x, code, qs[set][i].y);
+      }
+    } else {
+      char* Bs = smem + buf * C::STAGE + C::ABYTES;
+      const int q = tid + 256 * i, r = q >> 2, c2 = 2 * (q & 3);
+      *reinterpret_cast<u32x4*>(Bs + r * 128 + 16 * (c2 ^ ((r >> 1) & 7))) = reinterpret_cast<const u32x4*>(qv[i])[0];
+      *reinterpret_cast<u32x4*>(Bs + r * 128 + 16 * ((c2 + 1) ^ ((r >> 1) & 7))) =
+          reinterpret_cast<const u32x4*>(qv[i])[1];
+    }
+  };
 
   // fragment (t, s): rows 32 t + lane % 32 of this wave's block, k-chunk
   // 2 s + lane / 32 of the stage
@@ -470,7 +492,8 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
     for (int i = 0; i < C::TM; ++i) acc[j][i] = floatx16{};
 
   const int nk = p.K / 64;
-  issue(0, 0);
+#pragma unroll
+  for (int st = 0; st < C::DIST; ++st) issue(min(st, nk - 1), st);
   if constexpr (QUANT) {
     qload(0, 0);
     qload(min(1, nk - 1), 1);
@@ -491,32 +514,40 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
   // last barrier); the last stage reloads itself, unused, so that every pass
   // has the same loads in flight and no wait count depends on a branch.
   auto stage = [&](int kt, int par) {
-    const char* S = smem + par * C::STAGE;
-    const int ktn = min(kt + 1, nk - 1), nb = par ^ 1;
+    const int cur = kt % C::NS, nb = (kt + 1) % C::NS;
+    const char* S = smem + cur * C::STAGE;
+    // stage kt + DIST streams into buffer (kt - 1) % NS, read last in stage kt - 1
+    const int ktn = min(kt + C::DIST, nk - 1), nd = (kt + C::DIST) % C::NS;
     if constexpr (QUANT) qload(min(kt + 2, nk - 1), par);  // set par held stage kt, stored during kt - 1
-    if constexpr (!C::ILV) issue(ktn, nb);
+    if constexpr (!C::ILV) issue(ktn, nd);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (s < 3) {
         rd(S, s + 1, (s + 1) & 1);
       } else {
         // this wave's operand reads and its loads and stores of stage kt + 1
-        // are done; after the barrier every wave's are
-        __builtin_amdgcn_s_waitcnt(7 << 4);  // vmcnt(0) lgkmcnt(0)
+        // are done (the memory operations issued after stage kt + 1's
+        // loads, those of DIST - 1 later stages, may still be in flight);
+        // after the barrier every wave's are
+        constexpr int vm = (C::DIST - 1) * (C::NA + C::NB + (QUANT ? 2 * C::QB : 0));
+        static_assert(vm < 64, "vmcnt range");
+        __builtin_amdgcn_s_waitcnt((vm & 15) | ((vm >> 4) << 14) | (7 << 4));  // lgkmcnt(0)
         asm volatile("s_barrier" ::: "memory");
         rd(smem + nb * C::STAGE, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
-      // quantized chunks of stage kt + 1 dequantised in sub-steps 0-2, after
-      // the first half of the sub-step's MFMAs (chunk i in sub-step i % 3)
-      auto qpart = [&]() {
+      // quantized chunks of stage kt + 1 dequantised in sub-steps 0-2 (chunk
+      // i in sub-step i % 3), in pieces spread evenly between the MFMAs
+      constexpr int NM = C::TM * C::TN;
+      const int nq = (s < 3 && QUANT) ? (C::QB - s + 2) / 3 : 0;  // chunks of this sub-step
+      auto qpart = [&](int m) {
         if constexpr (QUANT) {
+          const int P = 9 * nq;
 #pragma unroll
-          for (int i = 0; i < C::QB; ++i)
-            if (s < 3 && i % 3 == s) qstore(i, par ^ 1, nb);
+          for (int pc = 0; pc < 9 * ((C::QB + 2) / 3); ++pc)
+            if (pc < P && pc * NM / P == m) qpiece(s + 3 * (pc / 9), pc % 9, par ^ 1, nb);
         }
       };
-      constexpr int NM = C::TM * C::TN;
       if constexpr (C::ILV) {
         // one workgroup per CU: issuing a stage's loads in one burst stalls
         // the wave while the memory pipe takes them, so sub-steps 0-2 each
@@ -526,8 +557,8 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
         for (int m = 0; m < NM; ++m) {
           const int j = m / C::TM, i = m % C::TM;
           acc[j][i] = mma32(fb[s & 1][j], fa[s & 1][i], acc[j][i]);
-          if (s < 3 && m % EV == EV - 1 && m / EV < DQ && s * DQ + m / EV < ND) issue1(s * DQ + m / EV, ktn, nb);
-          if (m == NM / 2 - 1) qpart();
+          if (s < 3 && m % EV == EV - 1 && m / EV < DQ && s * DQ + m / EV < ND) issue1(s * DQ + m / EV, ktn, nd);
+          qpart(m);
           __builtin_amdgcn_sched_barrier(0);
         }
       } else {
@@ -535,9 +566,8 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
         for (int m = 0; m < NM; ++m) {
           const int j = m / C::TM, i = m % C::TM;
           acc[j][i] = mma32(fb[s & 1][j], fa[s & 1][i], acc[j][i]);
-          if (m == NM / 2 - 1) {
-            __builtin_amdgcn_sched_barrier(0);
-            qpart();
+          if constexpr (QUANT) {
+            qpart(m);
             __builtin_amdgcn_sched_barrier(0);
           }
         }
@@ -865,21 +895,22 @@ int split_count(const GemmParams& p) {
 
 // Estimated duration of one launch of the tile kernel, in units of one
 // 192 x 192 tile pass at K = 1024 with every CU busy (measured: a 256 x 256
-// pass 1.35, 128 x 128 0.46 alone on a CU and 0.77 for two sharing one).
+// pass 1.45; 128 x 128 0.5 alone on a CU with four stages, 0.75 for a pass of
+// two per CU with two stages).
 template <int BM, int BN>
 double tile_cost(const GemmParams& p) {
   const int64_t tiles = m_tiles<BM>(p) * (p.N / BN);
   double c;
-  if (BM == 128 && BN == 128) c = tiles <= 256 ? 0.46 : (double)((tiles + 511) / 512) * 0.77;
-  else c = (double)((tiles + 255) / 256) * (BM * BN == 256 * 256 ? 1.35 : 1.0);
+  if (BM == 128 && BN == 128) c = tiles <= 256 ? 0.5 : (double)((tiles + 511) / 512) * 0.75;
+  else c = (double)((tiles + 255) / 256) * (BM * BN == 256 * 256 ? 1.45 : 1.0);
   return c * p.K / 1024.0;
 }
 
-template <int BM, int BN, bool QUANT>
+template <int BM, int BN, bool QUANT, int NS>
 hipError_t launch_tile(const GemmParams& p, hipStream_t s) {
   const int64_t tiles = m_tiles<BM>(p) * (p.N / BN);
   const unsigned grid = (unsigned)((tiles + 7) / 8 * 8);
-  hipLaunchKernelGGL((gemm_tile_kernel<BM, BN, QUANT>), dim3(grid), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((gemm_tile_kernel<BM, BN, QUANT, NS>), dim3(grid), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
@@ -905,9 +936,12 @@ bool dispatch_tile(const GemmParams& p, hipStream_t s, hipError_t& err) {
   int pick = 128;
   if (p.N % 192 == 0 && tile_cost<192, 192>(p) < best) best = tile_cost<192, 192>(p), pick = 192;
   if (p.N % 256 == 0 && tile_cost<256, 256>(p) < best) best = tile_cost<256, 256>(p), pick = 256;
-  if (pick == 256) err = launch_tile<256, 256, QUANT>(p, s);
-  else if (pick == 192) err = launch_tile<192, 192, QUANT>(p, s);
-  else err = launch_tile<128, 128, QUANT>(p, s);
+  // stages: three (loads two ahead) for 192 x 192; four for a 128 x 128 tile
+  // that has its CU to itself, two when two share one; 256 x 256 fits two
+  if (pick == 256) err = launch_tile<256, 256, QUANT, 2>(p, s);
+  else if (pick == 192) err = launch_tile<192, 192, QUANT, 3>(p, s);
+  else if (m_tiles<128>(p) * (p.N / 128) <= 256) err = launch_tile<128, 128, QUANT, 4>(p, s);
+  else err = launch_tile<128, 128, QUANT, 2>(p, s);
   return true;
 }
 
