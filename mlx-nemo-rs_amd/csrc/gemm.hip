@@ -361,8 +361,9 @@ struct TileCfg {
   static constexpr int NB = QUANT ? 0 : BN / 32;   // dense B loads per wave per stage
   static constexpr int QB = BN / 64;               // quantized 16-code chunks per thread per stage
   static constexpr int OP = WN * 2 + 16;           // staged output row pitch (bytes)
-  // loads spread between MFMAs whenever the tile has a CU to itself
-  static constexpr bool ILV = BM * BN >= 192 * 192 || NS > 2;
+  // loads spread between MFMAs whenever a tile of at least 128 x 128 has a
+  // CU to itself (a 64 x 64 tile has one MFMA per wave and k-step)
+  static constexpr bool ILV = BM * BN >= 192 * 192 || (NS > 2 && BM * BN >= 128 * 128);
   static constexpr int LDS = NS * STAGE > 4 * WM * OP ? NS * STAGE : 4 * WM * OP;
   static_assert(LDS <= 160 * 1024, "tile exceeds LDS");
 };
@@ -927,11 +928,18 @@ bool tile_ok(const GemmParams& p) {
   return true;
 }
 
-// bf16 projections with at least ~100 tiles of 128 x 128 go to the tile
-// kernel, at the tile shape with the lowest estimated time.
+// bf16 projections go to the tile kernel: with at least ~100 tiles of
+// 128 x 128 at the tile shape with the lowest estimated time, below that
+// (short inputs, a short position table) as 64 x 64 tiles with four stages
+// (749 x 1024 x 1024: 6.6 us against 12 us for split-K and its reduce).
 template <bool QUANT>
 bool dispatch_tile(const GemmParams& p, hipStream_t s, hipError_t& err) {
-  if (!tile_ok(p) || m_tiles<128>(p) * (p.N / 128) < 96 || p.N % 128) return false;
+  if (!tile_ok(p) || p.N % 64) return false;
+  if (p.N % 128 || m_tiles<128>(p) * (p.N / 128) < 96) {
+    if (m_tiles<64>(p) * (p.N / 64) < 16) return false;
+    err = launch_tile<64, 64, QUANT, 4>(p, s);
+    return true;
+  }
   double best = tile_cost<128, 128>(p);
   int pick = 128;
   if (p.N % 192 == 0 && tile_cost<192, 192>(p) < best) best = tile_cost<192, 192>(p), pick = 192;
