@@ -51,10 +51,83 @@ __global__ __launch_bounds__(256) void ln_kernel(const T* x, T* y, const float* 
   }
 }
 
+// The same with 16-byte accesses: lane l holds chunks l + 64 j of the row
+// (D a multiple of 64 chunks), gamma and beta read as float4.
+template <typename T, int NCH>
+__global__ __launch_bounds__(256) void ln_vec_kernel(const T* x, T* y, const float* gamma, const float* beta,
+                                                     float eps, int rows, int D) {
+  constexpr int E = 16 / sizeof(T);  // elements per chunk
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const T* xr = x + (int64_t)row * D;
+  float v[NCH][E];
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const u32x4 raw = *reinterpret_cast<const u32x4*>(xr + (lane + 64 * j) * E);
+    const T* t = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      v[j][e] = (float)t[e];
+      s += v[j][e];
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+  const float mean = s / (float)D;
+  float q = 0.f;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j)
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float d = v[j][e] - mean;
+      q += d * d;
+    }
+  for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
+  const float rstd = rsqrtf(q / (float)D + eps);
+  T* yr = y + (int64_t)row * D;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int c0 = (lane + 64 * j) * E;
+    T out[E];
+#pragma unroll
+    for (int e4 = 0; e4 < E; e4 += 4) {
+      const floatx4 g = gamma ? *reinterpret_cast<const floatx4*>(gamma + c0 + e4) : floatx4{1.f, 1.f, 1.f, 1.f};
+      const floatx4 b = beta ? *reinterpret_cast<const floatx4*>(beta + c0 + e4) : floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float t = (v[j][e4 + e] - mean) * rstd;
+        if (gamma) t *= g[e];
+        if (beta) t += b[e];
+        out[e4 + e] = from_float<T>(t);
+      }
+    }
+    *reinterpret_cast<u32x4*>(yr + c0) = *reinterpret_cast<const u32x4*>(out);
+  }
+}
+
 template <typename T>
 hipError_t ln_launch(const void* x, void* y, const float* g, const float* b, float eps, int rows, int D,
                      hipStream_t s) {
   dim3 grid((rows + 3) / 4);
+  constexpr int E = 16 / sizeof(T);
+  const bool aligned = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(y) |
+                         reinterpret_cast<uintptr_t>(g) | reinterpret_cast<uintptr_t>(b)) & 15) == 0;
+  if (aligned && D % (64 * E) == 0) {
+    switch (D / (64 * E)) {
+      case 1:
+        hipLaunchKernelGGL((ln_vec_kernel<T, 1>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
+        return hipGetLastError();
+      case 2:
+        hipLaunchKernelGGL((ln_vec_kernel<T, 2>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
+        return hipGetLastError();
+      case 4:
+        hipLaunchKernelGGL((ln_vec_kernel<T, 4>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
+        return hipGetLastError();
+      default:
+        break;
+    }
+  }
   if (D <= 512)
     hipLaunchKernelGGL((ln_kernel<T, 8>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
   else

@@ -467,6 +467,28 @@ def test_streaming_equals_offline_last_rows():
     assert rel_err(got, full[:, C:]) < 1e-5
 
 
+@pytest.mark.parametrize("d_model,n_heads,T", [(256, 2, 50), (1024, 8, 40)])
+def test_sublayer_f32_against_oracle(d_model, n_heads, T):
+    """x + MHSA(LayerNorm(x)) (conformer.rs:1747-1780) in fp32 with LayerNorm
+    gamma/beta and key padding: the LayerNorm kernel's statistics and affine,
+    the attention and the residual-fused output GEMM, within the fp32 bound."""
+    rng = np.random.default_rng(31)
+    w = random_weights(rng, d_model, n_heads)
+    p = oracle_params(w, d_model, n_heads)
+    x = rng.normal(size=(2, T, d_model)) * 3.0 + 0.5
+    gamma = rng.uniform(0.5, 1.5, d_model).astype(np.float32)
+    beta = rng.normal(0, 0.1, d_model).astype(np.float32)
+    lengths = [T, T - 7]
+    pos = O.RelPositionalEncoding(d_model, 5000, False).get_encoding(T)
+    ref = O.mhsa_sublayer(p, x, pos, None, O.key_padding_mask(lengths, T), gamma=gamma, beta=beta, dtype=O.F32)
+    layer = gpu_layer(w, d_model, n_heads, True, O.F32)
+    xd = dev(x, O.F32)
+    layer.sublayer_forward_(xd, dev(pos, O.F32), None, M.key_padding_mask(lengths, T), gamma=gamma, beta=beta)
+    got = host(xd)
+    vis = visible_rows(2, T, None, lengths)
+    assert rel_err(got[vis], ref[vis]) < F32_TOL
+
+
 # ---------------------------------------------------------------------------
 # quantized 24-layer stack
 # ---------------------------------------------------------------------------
