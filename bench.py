@@ -67,7 +67,7 @@ def kernel_work(cfg, tag, lengths, fills):
             band = 2 * (C + T) - 1
             vis = sum(T + f for f in fills)
             return (4.0 * (2 * B * T * D + 2 * vis * D + band * D), "GB/s", "hbm")
-        rows = {"gemm_q": 1, "gemm_kv": 2, "gemm_out": 1}.get(tag)
+        rows = {"gemm_qkv": 3, "gemm_q": 1, "gemm_kv": 2, "gemm_out": 1}.get(tag)
         if rows:
             return (2.0 * B * T * D * D * rows, "TFLOP/s", "mfma")
         return None

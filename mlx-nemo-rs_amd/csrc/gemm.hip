@@ -101,13 +101,16 @@ struct BLoad<T, true, BN, NT> {
   }
 };
 
-// C offset of one output row (computed once per row).
-__device__ __forceinline__ int64_t row_offset(const GemmParams& p, int row) {
+// Output row of input row `row` under the seg/ring mapping.
+__device__ __forceinline__ int64_t mapped_row(const GemmParams& p, int row) {
   int orow = row;
   if (p.seg_rows < p.M || p.ring_off)
     orow = (row / p.seg_rows) * p.seg_stride + (p.ring_off + row % p.seg_rows) % p.ring_len;
-  return (int64_t)orow * p.ldc;
+  return orow;
 }
+
+// C offset of one output row (computed once per row).
+__device__ __forceinline__ int64_t row_offset(const GemmParams& p, int row) { return mapped_row(p, row) * p.ldc; }
 
 // The reference's op order: round the product, add the bias, round, add the
 // residual, round.
@@ -810,6 +813,18 @@ __global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
 #pragma unroll
     for (int s = 0; s < NSTEP; ++s) a[t][s] = *reinterpret_cast<const F*>(ar + KW * s);
   }
+  if (p.acopy && n0 == 0) {
+    // the first column tile's workgroups copy A's rows (each element once)
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int row = m0 + 16 * t + (lane & 15);
+      if (row < p.M) {
+        T* dst = reinterpret_cast<T*>(p.acopy) + mapped_row(p, row) * p.acopy_ld + k0;
+#pragma unroll
+        for (int s = 0; s < NSTEP; ++s) *reinterpret_cast<F*>(dst + KW * s) = a[t][s];
+      }
+    }
+  }
   if constexpr (!QUANT) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -864,7 +879,14 @@ __global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
     for (int ww = 0; ww < nw; ++ww) v += red[ww][idx];
     const int l = idx >> 4, r = idx & 15, tu = r >> 2, e = r & 3;
     const int row = m0 + 16 * (tu >> 1) + 4 * (l >> 4) + e, col = n0 + 16 * (tu & 1) + (l & 15);
-    if (row < p.M) reinterpret_cast<T*>(p.C)[row_offset(p, row) + col] = from_float<T>(epilogue_value<T>(p, row, col, v));
+    if (row >= p.M) continue;
+    const T y = from_float<T>(epilogue_value<T>(p, row, col, v));
+    if (!p.C2)
+      reinterpret_cast<T*>(p.C)[row_offset(p, row) + col] = y;
+    else if (col < p.c2_col0)
+      reinterpret_cast<T*>(p.C)[(int64_t)row * p.ldc + col] = y;
+    else
+      reinterpret_cast<T*>(p.C2)[mapped_row(p, row) * p.ldc2 + col - p.c2_col0] = y;
   }
 }
 
@@ -968,6 +990,11 @@ hipError_t launch(const GemmParams& p, int splits, hipStream_t s) {
 template <typename T, bool QUANT>
 hipError_t dispatch(const GemmParams& p, hipStream_t s) {
   const int bk = ROWB / (int)sizeof(T);
+  if (sizeof(T) == 4 && (p.C2 || p.acopy)) {  // (validated by gemm())
+    const unsigned grid = (unsigned)(((p.M + 31) / 32) * (p.N / 32));
+    hipLaunchKernelGGL((gemm_kpar_kernel<T, QUANT>), dim3(grid), dim3(64 * (p.K / 64)), 0, s, p);
+    return hipGetLastError();
+  }
   if constexpr (sizeof(T) == 2) {
     hipError_t err;
     if (dispatch_tile<QUANT>(p, s, err)) return err;
@@ -982,8 +1009,9 @@ hipError_t dispatch(const GemmParams& p, hipStream_t s) {
   if (p.vt) return launch<T, QUANT, 128, 128, 2, 2>(p, 1, s);  // V^T epilogue needs whole 128-row tiles
   // few rows of fp32: K-parallel workgroups, no second kernel (for bf16 the
   // position table of a short utterance measured the same as split-K: 13.4
-  // against 12.6 us at 749 x 1024 x 1024, so bf16 keeps split-K)
-  if (sizeof(T) == 4 && kpar_ok<T>(p)) {
+  // against 12.6 us at 749 x 1024 x 1024, so bf16 keeps split-K); the split
+  // output and row copy only exist there
+  if (sizeof(T) == 4 && (kpar_ok<T>(p) || p.C2 || p.acopy)) {
     const unsigned grid = (unsigned)(((p.M + 31) / 32) * (p.N / 32));
     hipLaunchKernelGGL((gemm_kpar_kernel<T, QUANT>), dim3(grid), dim3(64 * (p.K / 64)), 0, s, p);
     return hipGetLastError();
@@ -1010,13 +1038,21 @@ hipError_t dispatch(const GemmParams& p, hipStream_t s) {
 
 }  // namespace
 
+bool gemm_split_fused_ok(DType dt, const GemmParams& p) {
+  if (dt != kF32 || p.vt || !kpar_ok<float>(p)) return false;
+  if (p.C2 && (p.c2_col0 <= 0 || p.c2_col0 >= p.N || p.c2_col0 % 32 || p.ldc2 < p.N - p.c2_col0)) return false;
+  if (p.acopy && (p.acopy_ld < p.K || (p.acopy_ld % 4) || (reinterpret_cast<uintptr_t>(p.acopy) & 15))) return false;
+  return true;
+}
+
 hipError_t gemm(DType dt, bool quantized, const GemmParams& p, hipStream_t s) {
   const int bk = ROWB / dtype_size(dt);
   if (p.M <= 0) return hipSuccess;
+  if ((p.C2 || p.acopy) && !gemm_split_fused_ok(dt, p)) return hipErrorInvalidValue;
   if (p.N <= 0 || p.N % 64 || p.K <= 0 || p.K % bk || (quantized && p.K % 64)) return hipErrorInvalidValue;
   if (!p.A || !p.W || !p.C || (quantized && !p.sb)) return hipErrorInvalidValue;
   if (p.seg_rows <= 0 || p.ring_len <= 0) return hipErrorInvalidValue;
-  if (p.lda < p.K || p.ldc < p.N || (p.R && p.ldr < p.N)) return hipErrorInvalidValue;
+  if (p.lda < p.K || p.ldc < (p.C2 ? p.c2_col0 : p.N) || (p.R && p.ldr < p.N)) return hipErrorInvalidValue;
   if (p.seg_T < 0 || (p.seg_T > 0 && p.M % p.seg_T)) return hipErrorInvalidValue;
   if (p.vt) {
     // V^T: per-utterance tiles, whole 16-byte token runs inside each padded row

@@ -43,11 +43,23 @@ struct GemmParams {
   // > 0: M tiles per utterance of seg_T rows (M a multiple of seg_T);
   // required with vt, where utterance b's tokens start at column b * vt_Tpad
   int seg_T = 0;
+  // Optional split output (the streaming chunk's fused Q|K|V projection):
+  // columns [c2_col0, N) go to C2 (leading dimension ldc2) at the rows the
+  // seg/ring fields map to, columns below c2_col0 to C at rows as they are.
+  // With acopy, A's rows are also copied to acopy (leading dimension
+  // acopy_ld) at the mapped rows. Only gemm_split_fused_ok() shapes take them.
+  void* C2 = nullptr;
+  int64_t ldc2 = 0;
+  int c2_col0 = 0;
+  void* acopy = nullptr;
+  int64_t acopy_ld = 0;
 };
 // Scratch the K-split path can use: 64x64 tiles x splits stays <= ~512
 // workgroups, so M*N*splits <= kGemmPartialElems.
 constexpr int64_t kGemmPartialElems = (int64_t)1 << 22;
 hipError_t gemm(DType dt, bool quantized, const GemmParams& p, hipStream_t s);
+// Whether gemm() takes this problem with C2 / acopy set (fp32, few rows).
+bool gemm_split_fused_ok(DType dt, const GemmParams& p);
 
 constexpr int kMaxBatch = 64;
 

@@ -905,20 +905,48 @@ int32_t mhsa_forward_with_cache(mhsa_layer* L, mhsa_stream* S, const void* x, co
   char* kv = static_cast<char*>(S->ring_kv.p);
   const int slot = (S->head + C) % R;  // ring rows of this chunk
 
-  {
-    ProfScope ps(L, "gemm_q", s);
-    if ((rc = run_gemm(L, L->dev[0], D, x, D, (int)M, q, D, nullptr, 0, s))) return rc;
-  }
-  ProfScope ps_kv(L, "gemm_kv", s);
+  // One launch when the layer holds the stacked [3D, D] weight: Q to `q`, K|V
+  // to the cache ring's rows of this chunk, and the chunk's input rows copied
+  // into the input ring by the workgroups of the first column tile.
+  mhsa::GemmParams fp;
   if (L->qkv_fused) {
-    if ((rc = run_gemm(L, L->dev[1], 2 * D, x, D, (int)M, kv, 2 * D, nullptr, 0, s, T, R, slot, R))) return rc;
-  } else {
-    if ((rc = run_gemm(L, L->dev[1], D, x, D, (int)M, kv, 2 * D, nullptr, 0, s, T, R, slot, R))) return rc;
-    if ((rc = run_gemm(L, L->dev[2], D, x, D, (int)M, kv + (size_t)D * 4, 2 * D, nullptr, 0, s, T, R, slot, R)))
-      return rc;
+    fp.A = x;
+    fp.lda = D;
+    fp.W = L->dev[0].w;
+    fp.sb = L->dev[0].sb;
+    fp.bias = L->dev[0].bias;
+    fp.C = q;
+    fp.ldc = D;
+    fp.C2 = kv;
+    fp.ldc2 = 2 * D;
+    fp.c2_col0 = D;
+    fp.acopy = S->ring_h.p;
+    fp.acopy_ld = D;
+    fp.M = (int)M;
+    fp.N = 3 * D;
+    fp.K = D;
+    fp.seg_rows = T;
+    fp.seg_stride = R;
+    fp.ring_off = slot;
+    fp.ring_len = R;
   }
-  ps_kv.next("ring_write");
-  HIPCHK(mhsa::ring_write(mhsa::kF32, x, S->ring_h.p, B, T, D, R, D, slot, s));
+  const bool one_launch = L->qkv_fused && mhsa::gemm_split_fused_ok(mhsa::kF32, fp);
+  ProfScope ps_kv(L, one_launch ? "gemm_qkv" : "gemm_q", s);
+  if (one_launch) {
+    HIPCHK(mhsa::gemm(mhsa::kF32, L->dev[0].quantized, fp, s));
+  } else {
+    if ((rc = run_gemm(L, L->dev[0], D, x, D, (int)M, q, D, nullptr, 0, s))) return rc;
+    ps_kv.next("gemm_kv");
+    if (L->qkv_fused) {
+      if ((rc = run_gemm(L, L->dev[1], 2 * D, x, D, (int)M, kv, 2 * D, nullptr, 0, s, T, R, slot, R))) return rc;
+    } else {
+      if ((rc = run_gemm(L, L->dev[1], D, x, D, (int)M, kv, 2 * D, nullptr, 0, s, T, R, slot, R))) return rc;
+      if ((rc = run_gemm(L, L->dev[2], D, x, D, (int)M, kv + (size_t)D * 4, 2 * D, nullptr, 0, s, T, R, slot, R)))
+        return rc;
+    }
+    ps_kv.next("ring_write");
+    HIPCHK(mhsa::ring_write(mhsa::kF32, x, S->ring_h.p, B, T, D, R, D, slot, s));
+  }
   ps_kv.next("attention");
 
   std::vector<int32_t> used(B);

@@ -467,6 +467,52 @@ def test_streaming_equals_offline_last_rows():
     assert rel_err(got, full[:, C:]) < 1e-5
 
 
+@pytest.mark.parametrize("d_model,n_heads,kind", [(256, 4, "u8"), (256, 4, "mixed"), (1280, 10, "u8"),
+                                                  (512, 8, "dense")])
+def test_streaming_projection_kinds_with_biases(d_model, n_heads, kind):
+    """Cache-aware steps with q/k/v/out biases and u8, dense or mixed q/k/v.
+    Same-kind q/k/v with D <= 1024 take one launch for the chunk's Q, its K|V
+    rows of the cache ring and its copy into the input ring; mixed kinds and
+    D = 1280 take separate launches. Four steps against the oracle (fp32
+    bound) and the exported cache bit-equal to the oracle's."""
+    rng = np.random.default_rng(51)
+    quant = kind != "dense"
+    w = W.make_layer_weights(rng, d_model, n_heads, True, quant, centred=True)
+    for name in ("linear_q", "linear_k", "linear_v", "linear_out", "linear_pos"):
+        if quant:  # |W| ~ 0.04: scores stay O(1)
+            s = rng.uniform(1e-4, 1e-3, size=w[f"{name}.scales"].shape)
+            w[f"{name}.scales"] = s.astype(np.float16)
+            b = -128.0 * w[f"{name}.scales"].astype(np.float64) + rng.normal(0, 1e-3, size=s.shape)
+            w[f"{name}.biases"] = b.astype(np.float16)
+        if name != "linear_pos":
+            w[f"{name}.bias"] = rng.normal(0, 0.1, d_model).astype(w[f"{name}.bias"].dtype)
+    if kind == "mixed":  # dense V beside u8 Q and K
+        del w["linear_v.scales"], w["linear_v.biases"]
+        w["linear_v.weight"] = W.xavier(rng, d_model, d_model)
+        w["linear_v.bias"] = w["linear_v.bias"].astype(np.float32)
+    p = oracle_params(w, d_model, n_heads)
+    B, C, T = 3, 70, 14
+    cache = rng.standard_normal((B, C, d_model)).astype(np.float32)
+    pos = O.RelPositionalEncoding(d_model, 5000, False).get_encoding(C + T)
+    layer = gpu_layer(w, d_model, n_heads, True, O.F32)
+    st = layer.stream(B, C, T)
+    fills = [70, 23, 0]
+    st.load_cache(dev(cache, O.F32), fills)
+    pos_d = dev(pos, O.F32)
+    caches = [cache[b:b + 1].astype(np.float64) for b in range(B)]
+    for step in range(4):
+        x = rng.standard_normal((B, T, d_model)).astype(np.float32)
+        got = host(st.step(dev(x, O.F32), pos_d, M.StreamingMask((70, 13), "chunked_limited")))
+        for b in range(B):
+            mask = O.streaming_mask((70, 13), "chunked_limited", C, fills[b], T, T)
+            ref, _ = O.mhsa_forward_with_cache(p, x[b:b + 1], pos, caches[b], mask)
+            assert rel_err(got[b:b + 1], ref) < F32_TOL, (step, b)
+            caches[b] = O.cache_update(caches[b], x[b:b + 1].astype(np.float64), 0)
+            fills[b] = O.next_fill(fills[b], T, 0, C)
+        assert st.fill() == fills
+    assert np.array_equal(st.read_cache().cpu().numpy(), np.concatenate(caches, 0).astype(np.float32))
+
+
 @pytest.mark.parametrize("d_model,n_heads,T", [(256, 2, 50), (1024, 8, 40)])
 def test_sublayer_f32_against_oracle(d_model, n_heads, T):
     """x + MHSA(LayerNorm(x)) (conformer.rs:1747-1780) in fp32 with LayerNorm
