@@ -10,8 +10,9 @@
 //    (128x128, 192x192 or 256x256 tiles on 4 waves, direct-to-LDS operand
 //    streams, LDS-staged epilogue; described at its definition).
 //  * gemm_kpar_kernel: fp32 projections of few rows (the streaming chunk,
-//    one short utterance): the contraction split over the 16 waves of a
-//    workgroup and summed in LDS.
+//    one short utterance): persistent workgroups over 32 x 32 tiles, each
+//    tile's contraction split over the K / 64 waves of a workgroup and summed
+//    in LDS.
 //  * gemm_split_kernel + gemm_reduce: bf16 projections of few rows (the
 //    position table of a short utterance): K split over workgroups, the
 //    partial sums added in split order by a second kernel.
@@ -779,124 +780,216 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(const GemmParams p, int
 }
 
 // ---------------------------------------------------------------------------
-// Projections with few rows (the streaming chunk's 224 rows, one short
-// utterance, the position table of a short one): too few output tiles to
-// fill 256 CUs, so the contraction is split, and it is split inside the
-// workgroup so that no second kernel has to add the parts. A workgroup of
-// NW = K / 64 waves computes a 32 x 32 output tile; wave w takes k-columns
+// fp32 projections with few rows (the streaming chunk's 224 rows, one short
+// utterance, the position table of a short one): too few 32 x 32 output
+// tiles to give every CU several, so each tile's contraction is split over
+// the waves of one workgroup, and the workgroups are persistent. Workgroup g
+// of G (at most one per CU) takes tiles [g T / G, (g + 1) T / G) of the T
+// tiles in row-tile-major order; wave w of NW = K / 64 owns k-columns
 // [64 w, 64 w + 64), one quantization group:
-//  * its A and B fragments for 16x16 MFMAs (fp32 16x16x4: lane l holds row
-//    l % 16, k 4 (l / 16) + [0, 4) of each 16-wide step; bf16 16x16x32: k
-//    8 (l / 16) + [0, 8) of each 32-wide step) load straight into registers,
-//    all at once (rows past M read row M - 1 and are not stored); quantized
-//    B loads its codes and dequantises them in registers;
-//  * 2 x 2 output tiles of 16 x 16 per wave;
-//  * the waves' accumulators meet in LDS and thread t sums element t over
-//    the waves in order w = 0, 1, ..., then applies the epilogue.
-template <typename T, bool QUANT>
+//  * the A fragments of the current row tile stay in registers across its
+//    column tiles, and the next tile's W loads are in flight while the
+//    current tile's MFMAs run (always issued: the last tile reloads itself,
+//    so no load sits on a conditional path and no wait is widened);
+//  * dense rows load with four consecutive lanes on one 64 B run (lane l:
+//    row l / 4, 16 B chunk l % 4 of each 64 B step), which the address unit
+//    serves in a quarter of the cycles that MFMA-layout loads (16 rows per 16
+//    lanes) take, measured 5.8 against 1.7 us for 256 KB on one CU; each
+//    1 KB load reaches MFMA layout through 1 KB of the wave's own LDS, stored
+//    as 16 rows x 64 B with chunk j of row r at 16 (j ^ (r / 4 % 4)), which is
+//    conflict-free for the contiguous write and the 16-row read;
+//  * quantized W loads its codes in MFMA layout (a quarter of the bytes)
+//    with its group's {scale, bias} and dequantises in registers;
+//  * the waves' 32 x 32 partial tiles meet in LDS (two buffers by tile
+//    parity: one barrier per tile) and thread t sums element t over the
+//    waves in order w = 0, 1, ..., then applies the epilogue.
+// fp32 16x16x4 MFMA: lane l holds row l % 16 and k 4 (l / 16) + e of each
+// 16-wide step, e = 0..3. Operands are addressed through buffer descriptors
+// (one VGPR offset each, the tile and step in SGPRs); A rows past M read as
+// zero and are not stored.
+__device__ __forceinline__ void kpar_xpose(char* slot, int wr, int rd, floatx4& v) {
+  *reinterpret_cast<floatx4*>(slot + wr) = v;
+  v = *reinterpret_cast<const floatx4*>(slot + rd);
+}
+
+__device__ __forceinline__ floatx4 kpar_load(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+template <bool QUANT>
 __global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
-  constexpr bool BF = sizeof(T) == 2;
-  constexpr int KW = BF ? 32 : 16;     // k per MFMA step
-  constexpr int NSTEP = 64 / KW;       // steps per wave
-  constexpr int EL = BF ? 8 : 4;       // elements per lane per fragment
-  using F = typename Frag<T>::type;
-  __shared__ __attribute__((aligned(16))) float red[16][64 * 16];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), nw = (int)blockDim.x >> 6;
-  const int tilesN = p.N / 32;
-  const int m0 = (int)blockIdx.x / tilesN * 32, n0 = (int)blockIdx.x % tilesN * 32;
-  const int k0 = w * 64 + EL * (lane >> 4);
-  F a[2][NSTEP], b[2][NSTEP];
+  __shared__ __attribute__((aligned(16))) float red[2][16][1024];  // [tile parity][wave][element]
+  __shared__ __attribute__((aligned(16))) char xsm[16][2048];       // two 1 KB transpose slots per wave
+  const int tid = threadIdx.x, lane = tid & 63, nt_threads = (int)blockDim.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), nw = nt_threads >> 6;
+  const int tilesN = p.N / 32, T = (p.M + 31) / 32 * tilesN, G = (int)gridDim.x;
+  const int v0 = (int)((int64_t)blockIdx.x * T / G), v1 = (int)((int64_t)(blockIdx.x + 1) * T / G);
+  if (v0 >= v1) return;  // (whole workgroup)
+  const int kq = w * 64 + 4 * (lane & 3);   // quad-run chunk of the wave's k-columns
+  const int kf = w * 64 + 4 * (lane >> 4);  // MFMA-layout chunk
+  char* xs = xsm[w];
+  const int xw = (lane >> 2) * 64 + 16 * ((lane & 3) ^ ((lane >> 4) & 3));
+  const int xr = (lane & 15) * 64 + 16 * ((lane >> 4) ^ ((lane >> 2) & 3));
+  // (A rows are addressed from the row tile's first row in the range-checked
+  // VGPR offset, so rows past M read as zero)
+  const int voa0 = ((lane >> 2) * (int)p.lda + kq) * 4, voa1 = voa0 + 16 * (int)p.lda * 4;
+  const int groups = p.K / 64;
+
+  floatx4 a[2][4];
+  auto loadA = [&](int mt) {
+    const __amdgpu_buffer_rsrc_t ra =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(reinterpret_cast<const float*>(p.A) + (int64_t)mt * 32 * p.lda),
+                                          (short)0, (int)((int64_t)(p.M - mt * 32) * p.lda * 4), kRawBuffer);
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const T* ar = reinterpret_cast<const T*>(p.A) + (int64_t)min(m0 + 16 * t + (lane & 15), p.M - 1) * p.lda + k0;
+    for (int s = 0; s < 4; ++s) {
+      a[0][s] = kpar_load(ra, voa0 + 64 * s, 0);
+      a[1][s] = kpar_load(ra, voa1 + 64 * s, 0);
+    }
+    if (p.acopy && mt * tilesN >= v0 && mt * tilesN < v1) {
+      // the workgroup holding the row tile's first column tile copies its
+      // rows (each element once)
 #pragma unroll
-    for (int s = 0; s < NSTEP; ++s) a[t][s] = *reinterpret_cast<const F*>(ar + KW * s);
-  }
-  if (p.acopy && n0 == 0) {
-    // the first column tile's workgroups copy A's rows (each element once)
+      for (int t = 0; t < 2; ++t) {
+        const int row = mt * 32 + 16 * t + (lane >> 2);
+        if (row < p.M) {
+          float* dst = reinterpret_cast<float*>(p.acopy) + mapped_row(p, row) * p.acopy_ld + kq;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int row = m0 + 16 * t + (lane & 15);
-      if (row < p.M) {
-        T* dst = reinterpret_cast<T*>(p.acopy) + mapped_row(p, row) * p.acopy_ld + k0;
-#pragma unroll
-        for (int s = 0; s < NSTEP; ++s) *reinterpret_cast<F*>(dst + KW * s) = a[t][s];
+          for (int s = 0; s < 4; ++s) *reinterpret_cast<floatx4*>(dst + 16 * s) = a[t][s];
+        }
       }
     }
-  }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      kpar_xpose(xs, xw, xr, a[0][s]);
+      kpar_xpose(xs + 1024, xw, xr, a[1][s]);
+    }
+  };
+
+  // W chunk (u, s) of the tile being computed (dense: quad-run layout; quant:
+  // the codes), replaced by the next tile's chunk as soon as step s has taken
+  // it, so the next tile's loads overlap this tile's MFMAs
+  floatx4 wd[2][4];
+  uint32_t wq[2][4];
+  floatx2 wsb[2], wsb_next[2];
+  __amdgpu_buffer_rsrc_t rw, rs;
+  int vow = 0, vos = 0;
   if constexpr (!QUANT) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const T* br = reinterpret_cast<const T*>(p.W) + (int64_t)(n0 + 16 * u + (lane & 15)) * p.K + k0;
-#pragma unroll
-      for (int s = 0; s < NSTEP; ++s) b[u][s] = *reinterpret_cast<const F*>(br + KW * s);
-    }
+    rw = __builtin_amdgcn_make_buffer_rsrc((void*)p.W, (short)0, (int)((int64_t)p.N * p.K * 4), kRawBuffer);
+    vow = ((lane >> 2) * p.K + kq) * 4;
   } else {
-    // EL codes per lane and step, in one EL-byte load
-    using CodeT = typename std::conditional<BF, u32x2, uint32_t>::type;
-    const int groups = p.K / 64;
-    CodeT q[2][NSTEP];
-    floatx2 sb[2];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int n = n0 + 16 * u + (lane & 15);
-      const unsigned char* cr = reinterpret_cast<const unsigned char*>(p.W) + (int64_t)n * p.K + k0;
-#pragma unroll
-      for (int s = 0; s < NSTEP; ++s) q[u][s] = *reinterpret_cast<const CodeT*>(cr + KW * s);
-      sb[u] = *reinterpret_cast<const floatx2*>(p.sb + 2 * ((int64_t)n * groups + w));
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-#pragma unroll
-      for (int s = 0; s < NSTEP; ++s)
-#pragma unroll
-        for (int e = 0; e < EL; ++e) {
-          uint32_t word;
-          if constexpr (BF) word = q[u][s][e >> 2];
-          else word = q[u][s];
-          const float v = __builtin_fmaf(sb[u].x, (float)((word >> (8 * (e & 3))) & 0xFFu), sb[u].y);
-          b[u][s][e] = from_float<T>(v);
-        }
+    rw = __builtin_amdgcn_make_buffer_rsrc((void*)p.W, (short)0, (int)((int64_t)p.N * p.K), kRawBuffer);
+    rs = __builtin_amdgcn_make_buffer_rsrc((void*)p.sb, (short)0, (int)((int64_t)p.N * groups * 8), kRawBuffer);
+    vow = (lane & 15) * p.K + kf;
+    vos = ((lane & 15) * groups + w) * 8;
   }
-  floatx4 acc[2][2];
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      acc[t][u] = floatx4{};
-#pragma unroll
-      for (int s = 0; s < NSTEP; ++s) acc[t][u] = mma16(a[t][s], b[u][s], acc[t][u]);
-    }
-  // element r = 4 (2 t + u) + e of lane l: row 16 t + 4 (l / 16) + e, column 16 u + l % 16
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int u = 0; u < 2; ++u) *reinterpret_cast<floatx4*>(&red[w][lane * 16 + 4 * (2 * t + u)]) = acc[t][u];
-  __syncthreads();
-  for (int idx = tid; idx < 64 * 16; idx += (int)blockDim.x) {
-    float v = 0.f;
-    for (int ww = 0; ww < nw; ++ww) v += red[ww][idx];
-    const int l = idx >> 4, r = idx & 15, tu = r >> 2, e = r & 3;
-    const int row = m0 + 16 * (tu >> 1) + 4 * (l >> 4) + e, col = n0 + 16 * (tu & 1) + (l & 15);
-    if (row >= p.M) continue;
-    const T y = from_float<T>(epilogue_value<T>(p, row, col, v));
-    if (!p.C2)
-      reinterpret_cast<T*>(p.C)[row_offset(p, row) + col] = y;
-    else if (col < p.c2_col0)
-      reinterpret_cast<T*>(p.C)[(int64_t)row * p.ldc + col] = y;
+  auto loadW = [&](int nt, int u, int s) {
+    if constexpr (!QUANT)
+      wd[u][s] = kpar_load(rw, vow, (nt * 32 + 16 * u) * p.K * 4 + 64 * s);
     else
-      reinterpret_cast<T*>(p.C2)[mapped_row(p, row) * p.ldc2 + col - p.c2_col0] = y;
+      wq[u][s] = __builtin_amdgcn_raw_buffer_load_b32(rw, vow, (nt * 32 + 16 * u) * p.K + 16 * s, 0);
+  };
+  auto loadSB = [&](int nt, floatx2 (&d)[2]) {
+    if constexpr (QUANT) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        d[u] = __builtin_bit_cast(floatx2, __builtin_amdgcn_raw_buffer_load_b64(rs, vos, (nt * 32 + 16 * u) * groups * 8, 0));
+    }
+  };
+
+  int mt_cur = v0 / tilesN;
+  loadA(mt_cur);
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) loadW(v0 % tilesN, u, s);
+  loadSB(v0 % tilesN, wsb);
+  for (int v = v0; v < v1; ++v) {
+    const int mt = v / tilesN, nt = v % tilesN;
+    const int nn = min(v + 1, v1 - 1) % tilesN;  // the next tile's columns (the last tile reloads its own)
+    loadSB(nn, wsb_next);
+    floatx4 acc[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) acc[t][u] = floatx4{};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      floatx4 bf[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        if constexpr (!QUANT) {
+          kpar_xpose(xs + 1024 * u, xw, xr, wd[u][s]);
+          bf[u] = wd[u][s];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            bf[u][e] = __builtin_fmaf(wsb[u].x, (float)((wq[u][s] >> (8 * e)) & 0xFFu), wsb[u].y);
+        }
+        loadW(nn, u, s);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int u = 0; u < 2; ++u)
+            acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][s][j], bf[u][j], acc[t][u], 0, 0, 0);
+    }
+    if constexpr (QUANT) {
+      wsb[0] = wsb_next[0];
+      wsb[1] = wsb_next[1];
+    }
+    // element 4 (2 t + u) + e of lane l: row 16 t + 4 (l / 16) + e, column 16 u + l % 16
+    float (&rb)[16][1024] = red[v & 1];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) *reinterpret_cast<floatx4*>(&rb[w][lane * 16 + 4 * (2 * t + u)]) = acc[t][u];
+    __syncthreads();
+    // (this buffer is written again two tiles on, after the next tile's
+    // barrier, which every thread reaches only after its sums here)
+    for (int idx = tid; idx < 1024; idx += nt_threads) {
+      float sum = 0.f;
+      for (int ww = 0; ww < nw; ++ww) sum += rb[ww][idx];
+      const int l = idx >> 4, tu = (idx >> 2) & 3, e = idx & 3;
+      const int row = mt * 32 + 16 * (tu >> 1) + 4 * (l >> 4) + e, col = nt * 32 + 16 * (tu & 1) + (l & 15);
+      if (row >= p.M) continue;
+      const float y = epilogue_value<float>(p, row, col, sum);
+      if (!p.C2)
+        reinterpret_cast<float*>(p.C)[row_offset(p, row) + col] = y;
+      else if (col < p.c2_col0)
+        reinterpret_cast<float*>(p.C)[(int64_t)row * p.ldc + col] = y;
+      else
+        reinterpret_cast<float*>(p.C2)[mapped_row(p, row) * p.ldc2 + col - p.c2_col0] = y;
+    }
+    if (v + 1 < v1 && (v + 1) / tilesN != mt_cur) loadA(mt_cur = (v + 1) / tilesN);
   }
 }
 
-// The K-parallel kernel applies to K = 64 .. 1024 with 16-byte operand rows
-// and at most 4096 tiles (beyond that the other kernels fill the GPU).
+// Workgroups of the K-parallel kernel: as many tiles each as the tiles over
+// the CUs need, spread so that no workgroup has more.
+int kpar_grid(const GemmParams& p) {
+  static int cus = 0;
+  if (!cus) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                                  hipSuccess || n <= 0)
+      n = 256;
+    cus = n;
+  }
+  const int T = (p.M + 31) / 32 * (p.N / 32);
+  const int per = (T + cus - 1) / cus;
+  return (T + per - 1) / per;
+}
+
+// The K-parallel kernel applies to fp32, K = 64 .. 1024, 16-byte operand
+// rows, operands addressable by 32-bit buffer offsets and at most 4096 tiles
+// (beyond that the other kernels fill the GPU).
 template <typename T>
 bool kpar_ok(const GemmParams& p) {
-  constexpr int E = 16 / (int)sizeof(T);
-  return p.K % 64 == 0 && p.K <= 1024 && p.N % 32 == 0 && !p.vt && p.lda % E == 0 && p.K % E == 0 &&
+  return sizeof(T) == 4 && p.K % 64 == 0 && p.K <= 1024 && p.N % 32 == 0 && !p.vt && p.lda % 4 == 0 &&
          ((reinterpret_cast<uintptr_t>(p.A) | reinterpret_cast<uintptr_t>(p.W)) & 15) == 0 &&
+         (int64_t)p.M * p.lda * 4 < ((int64_t)1 << 31) && (int64_t)p.N * p.K * 4 < ((int64_t)1 << 31) &&
          (int64_t)((p.M + 31) / 32) * (p.N / 32) <= 4096;
 }
 
@@ -990,10 +1083,11 @@ hipError_t launch(const GemmParams& p, int splits, hipStream_t s) {
 template <typename T, bool QUANT>
 hipError_t dispatch(const GemmParams& p, hipStream_t s) {
   const int bk = ROWB / (int)sizeof(T);
-  if (sizeof(T) == 4 && (p.C2 || p.acopy)) {  // (validated by gemm())
-    const unsigned grid = (unsigned)(((p.M + 31) / 32) * (p.N / 32));
-    hipLaunchKernelGGL((gemm_kpar_kernel<T, QUANT>), dim3(grid), dim3(64 * (p.K / 64)), 0, s, p);
-    return hipGetLastError();
+  if constexpr (sizeof(T) == 4) {
+    if (p.C2 || p.acopy) {  // (validated by gemm())
+      hipLaunchKernelGGL((gemm_kpar_kernel<QUANT>), dim3(kpar_grid(p)), dim3(p.K), 0, s, p);
+      return hipGetLastError();
+    }
   }
   if constexpr (sizeof(T) == 2) {
     hipError_t err;
@@ -1011,10 +1105,11 @@ hipError_t dispatch(const GemmParams& p, hipStream_t s) {
   // position table of a short utterance measured the same as split-K: 13.4
   // against 12.6 us at 749 x 1024 x 1024, so bf16 keeps split-K); the split
   // output and row copy only exist there
-  if (sizeof(T) == 4 && (kpar_ok<T>(p) || p.C2 || p.acopy)) {
-    const unsigned grid = (unsigned)(((p.M + 31) / 32) * (p.N / 32));
-    hipLaunchKernelGGL((gemm_kpar_kernel<T, QUANT>), dim3(grid), dim3(64 * (p.K / 64)), 0, s, p);
-    return hipGetLastError();
+  if constexpr (sizeof(T) == 4) {
+    if (kpar_ok<T>(p)) {
+      hipLaunchKernelGGL((gemm_kpar_kernel<QUANT>), dim3(kpar_grid(p)), dim3(p.K), 0, s, p);
+      return hipGetLastError();
+    }
   }
   if (const int splits = split_count<T>(p)) {
     const int64_t tiles = (int64_t)((p.M + 63) / 64) * (p.N / 64);
