@@ -807,8 +807,10 @@ __global__ __launch_bounds__(256) void pos_bias_diff_kernel(const AttnParams p, 
 // ---------------------------------------------------------------------------
 // fp32 chunk kernel for short query blocks (the cache-aware streaming step:
 // T <= 16 queries against L <= 96 keys of the cache ring). One workgroup of
-// four waves per (item, head) stages the visible key rows and the position
-// rows they reach in LDS once, then:
+// eight waves per (item, head) stages the visible key rows and the position
+// rows they reach in LDS once (eight waves, not four: a wave with some 60
+// loads in flight waits about twice as long per byte as one with 20, measured
+// 2.0 against 1.0 us for 152 KB on one CU), then:
 //   S  = q_u K^T           (16 x keys)            fp32 16x16x4 MFMAs
 //   B' = q_v P'^T          (16 x (keys + 15))      over the rows
 //        P' = P[r0 + m], r0 = center - qoff - 15 + jbeg; rel_shift reads
@@ -820,25 +822,26 @@ __global__ __launch_bounds__(256) void pos_bias_diff_kernel(const AttnParams p, 
 // ---------------------------------------------------------------------------
 template <int DK>
 struct CfgS {
-  static constexpr int NT = 256, NQ = 16, LMAX = 96, PMAX = LMAX + NQ - 1;
+  static constexpr int NT = 512, NW = NT / 64, NQ = 16, LMAX = 96, PMAX = LMAX + NQ - 1;
   static constexpr int RP = DK * 4 + 16;                                // K / V / position row pitch (bytes)
   static constexpr int K_OFF = 0;                                       // K rows, later V rows
   static constexpr int P_OFF = LMAX * RP;                               // position rows
-  static constexpr int PROWS = (PMAX + 15) / 16 * 16;
+  static constexpr int RPI = NT / (DK / 4);                             // rows per pass of the workgroup
+  static constexpr int PROWS = (PMAX + RPI - 1) / RPI * RPI;            // (RPI is a multiple of 16)
   static constexpr int S_OFF = P_OFF + PROWS * RP;                      // scores / probabilities [NQ][LMAX]
   static constexpr int B_OFF = S_OFF + NQ * LMAX * 4;                   // band products [NQ][PROWS]
-  static constexpr int LDS = B_OFF + NQ * PROWS * 4;
-  static constexpr int RPI = NT / (DK / 4);                             // rows per pass of the workgroup
+  static constexpr int Q_OFF = B_OFF + NQ * PROWS * 4;                 // q + pos_bias_u, then q + pos_bias_v rows
+  static constexpr int LDS = Q_OFF + 2 * NQ * RP;
   static constexpr int KCH = LMAX / RPI;                                // K / V chunks per thread
   static constexpr int PCH = PROWS / RPI;                               // position chunks per thread
-  static_assert(KCH * RPI == LMAX && PCH * RPI == PROWS, "row split");
+  static_assert(KCH * RPI == LMAX && PCH * RPI == PROWS && RPI % 16 == 0, "row split");
   static_assert(LDS <= 160 * 1024, "LDS");
 };
 
 template <int DK>
-__global__ __launch_bounds__(256) void attn_chunk_f32_kernel(const AttnParams p) {
+__global__ __launch_bounds__(CfgS<DK>::NT) void attn_chunk_f32_kernel(const AttnParams p) {
   using C = CfgS<DK>;
-  constexpr int NQ = C::NQ, LMAX = C::LMAX, NS = DK / 16;
+  constexpr int NQ = C::NQ, LMAX = C::LMAX, NS = DK / 16, NW = C::NW;
   __shared__ __attribute__((aligned(16))) char smem[C::LDS];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int rl = lane & 15, g = lane >> 4;  // MFMA row / column in the tile, k group
@@ -860,44 +863,56 @@ __global__ __launch_bounds__(256) void attn_chunk_f32_kernel(const AttnParams p)
   const float* vb = reinterpret_cast<const float*>(p.v) + (int64_t)b * p.kv_bs + h * DK;
   const float* pb = reinterpret_cast<const float*>(p.p) + h * DK;
 
-  // This thread's rows (tid / (DK/4) + RPI i) and 16-byte column chunk. Rows
-  // past the last visible key repeat it (their scores are masked and their
+  // This thread's rows (tid / (DK/4) + RPI i) and 16-byte column chunk, read
+  // through buffer descriptors: rows past the last visible key and position
+  // rows past the band get an offset beyond the descriptor's range, so they
+  // read as zero without a memory access (their scores are masked and their
   // probabilities are zero); every load is issued before the first store.
+  constexpr int kRawBuffer = 0x00020000;  // descriptor dword 3: untyped 32-bit data
+  const int krows = p.ring_len ? p.ring_len : p.L;
+  const int kbytes = ((krows - 1) * (int)p.kv_rs + DK) * 4, pbytes = ((p.p_rows - 1) * (int)p.p_rs + DK) * 4;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc((void*)kb, (short)0, kbytes, kRawBuffer);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc((void*)vb, (short)0, kbytes, kRawBuffer);
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc((void*)pb, (short)0, pbytes, kRawBuffer);
   const int row0 = tid / (DK / 4), cb = (tid % (DK / 4)) * 4;
-  int64_t koff[C::KCH];
+  int koff[C::KCH];
   {
     int rr = key_row(p, jbeg + min(row0, nk - 1));
 #pragma unroll
     for (int i = 0; i < C::KCH; ++i) {
       const int row = row0 + C::RPI * i;
-      koff[i] = (int64_t)(row < nk ? rr : key_row(p, jend - 1)) * p.kv_rs + cb;
+      koff[i] = row < nk ? (rr * (int)p.kv_rs + cb) * 4 : kbytes;
       rr += C::RPI;  // the next row of this thread: key + RPI (ring: mod ring_len)
       if (p.ring_len && rr >= p.ring_len) rr -= p.ring_len;
     }
   }
   u32x4 kr[C::KCH], vr[C::KCH], pr[C::PCH];
 #pragma unroll
-  for (int i = 0; i < C::KCH; ++i) kr[i] = *reinterpret_cast<const u32x4*>(kb + koff[i]);
+  for (int i = 0; i < C::KCH; ++i) kr[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, koff[i], 0, 0);
 #pragma unroll
   for (int i = 0; i < C::PCH; ++i) {
     // rows outside the table meet only masked pairs: clamped (finite)
-    const int n = min(max(r0 + row0 + C::RPI * i, 0), p.p_rows - 1);
-    pr[i] = *reinterpret_cast<const u32x4*>(pb + (int64_t)n * p.p_rs + cb);
+    const int row = row0 + C::RPI * i;
+    const int n = min(max(r0 + row, 0), p.p_rows - 1);
+    pr[i] = __builtin_amdgcn_raw_buffer_load_b128(rp, row < np ? (n * (int)p.p_rs + cb) * 4 : pbytes, 0, 0);
   }
 #pragma unroll
-  for (int i = 0; i < C::KCH; ++i) vr[i] = *reinterpret_cast<const u32x4*>(vb + koff[i]);
-  // q_u, q_v A fragments: row rl, d_k values 16s + 4g + [0, 4); rows past T read row T - 1
-  floatx4 qu[NS], qv[NS];
+  for (int i = 0; i < C::KCH; ++i) vr[i] = __builtin_amdgcn_raw_buffer_load_b128(rv, koff[i], 0, 0);
+  // q rows with the two position biases added, staged in LDS with the same
+  // row split as the keys (one 16-byte chunk per thread; rows past T read as
+  // zero): loading the MFMA fragments straight from memory in every wave
+  // would put 16 rows under each 16 lanes, which the address unit serves at
+  // a quarter of the rate of whole 64-byte runs
+  const int qrow = tid / (DK / 4);
+  floatx4 qx, qbu, qbv;
   {
-    const float* qr = reinterpret_cast<const float*>(p.q) + (int64_t)b * p.q_bs + (int64_t)min(rl, p.T - 1) * p.q_rs +
-                      h * DK;
-#pragma unroll
-    for (int st = 0; st < NS; ++st) {
-      const int d = 16 * st + 4 * g;
-      const floatx4 x = *reinterpret_cast<const floatx4*>(qr + d);
-      qu[st] = x + *reinterpret_cast<const floatx4*>(p.bias_u + h * DK + d);
-      qv[st] = x + *reinterpret_cast<const floatx4*>(p.bias_v + h * DK + d);
-    }
+    const float* qbase = reinterpret_cast<const float*>(p.q) + (int64_t)b * p.q_bs + h * DK;
+    const int qbytes = ((p.T - 1) * (int)p.q_rs + DK) * 4;
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)qbase, (short)0, qbytes, kRawBuffer);
+    qx = __builtin_bit_cast(floatx4,
+                            __builtin_amdgcn_raw_buffer_load_b128(rq, qrow < p.T ? (qrow * (int)p.q_rs + cb) * 4 : qbytes, 0, 0));
+    qbu = *reinterpret_cast<const floatx4*>(p.bias_u + h * DK + cb);
+    qbv = *reinterpret_cast<const floatx4*>(p.bias_v + h * DK + cb);
   }
 #pragma unroll
   for (int i = 0; i < C::KCH; ++i)
@@ -905,12 +920,25 @@ __global__ __launch_bounds__(256) void attn_chunk_f32_kernel(const AttnParams p)
 #pragma unroll
   for (int i = 0; i < C::PCH; ++i)
     *reinterpret_cast<u32x4*>(smem + C::P_OFF + (row0 + C::RPI * i) * C::RP + cb * 4) = pr[i];
+  if (qrow < NQ) {
+    *reinterpret_cast<floatx4*>(smem + C::Q_OFF + qrow * C::RP + cb * 4) = qx + qbu;
+    *reinterpret_cast<floatx4*>(smem + C::Q_OFF + (NQ + qrow) * C::RP + cb * 4) = qx + qbv;
+  }
   __syncthreads();
+
+  // q_u, q_v A fragments: row rl, d_k values 16s + 4g + [0, 4)
+  floatx4 qu[NS], qv[NS];
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    const int d = 16 * st + 4 * g;
+    qu[st] = *reinterpret_cast<const floatx4*>(smem + C::Q_OFF + rl * C::RP + d * 4);
+    qv[st] = *reinterpret_cast<const floatx4*>(smem + C::Q_OFF + (NQ + rl) * C::RP + d * 4);
+  }
 
   // score tiles (keys) and band tiles (position rows), spread over the waves
   float* Sl = reinterpret_cast<float*>(smem + C::S_OFF);
   float* Bl = reinterpret_cast<float*>(smem + C::B_OFF);
-  for (int t = w; t < nkt + npt; t += 4) {
+  for (int t = w; t < nkt + npt; t += NW) {
     const bool is_s = t < nkt;
     const int tt = is_s ? t : t - nkt;
     const char* rows = smem + (is_s ? C::K_OFF : C::P_OFF) + (tt * 16 + rl) * C::RP + 16 * g;
@@ -935,43 +963,45 @@ __global__ __launch_bounds__(256) void attn_chunk_f32_kernel(const AttnParams p)
   for (int i = 0; i < C::KCH; ++i)
     *reinterpret_cast<u32x4*>(smem + C::K_OFF + (row0 + C::RPI * i) * C::RP + cb * 4) = vr[i];
 
-  // softmax per query row: wave w takes rows 4w + lane / 16, each row split
-  // over 16 lanes (keys jl = lane % 16 + 16k), so the reductions stay inside
-  // 16-lane rows (DPP, no LDS round trips)
+  // softmax per query row: wave w takes rows RW w + lane / RL, each row
+  // split over RL lanes (keys jl = lane % RL + RL k), so the reductions stay
+  // inside RL-lane groups
   {
-    const int i = 4 * w + (lane >> 4), q = lane & 15;
+    constexpr int RW = NQ / NW, RL = 64 / RW;
+    static_assert(RW * NW == NQ && LMAX % RL == 0, "softmax rows");
+    const int i = RW * w + lane / RL, q = lane % RL;
     const int2 iv = query_interval(p, bl, i);
-    float x[LMAX / 16];
+    float x[LMAX / RL];
     float m = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < LMAX / 16; ++k) {
-      const int jl = q + 16 * k;
+    for (int k = 0; k < LMAX / RL; ++k) {
+      const int jl = q + RL * k;
       x[k] = -INFINITY;
       if (jl < nk && in_interval(jbeg + jl, iv))
         x[k] = Sl[i * LMAX + jl] * p.scale + Bl[i * C::PROWS + jl + NQ - 1 - i] * p.scale_bd;
       m = fmaxf(m, x[k]);
     }
 #pragma unroll
-    for (int o = 8; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 16));
+    for (int o = RL / 2; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, RL));
     float sum = 0.f;
 #pragma unroll
-    for (int k = 0; k < LMAX / 16; ++k) {
+    for (int k = 0; k < LMAX / RL; ++k) {
       x[k] = m == -INFINITY ? 0.f : __expf(x[k] - m);
       sum += x[k];
     }
 #pragma unroll
-    for (int o = 8; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 16);
+    for (int o = RL / 2; o > 0; o >>= 1) sum += __shfl_xor(sum, o, RL);
     const float inv = sum > 0.f ? 1.f / sum : 0.f;  // a row that sees no key gives 0
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int k = 0; k < LMAX / 16; ++k) Sl[i * LMAX + q + 16 * k] = x[k] * inv;
+    for (int k = 0; k < LMAX / RL; ++k) Sl[i * LMAX + q + RL * k] = x[k] * inv;
   }
   __syncthreads();
 
-  // O = probs . V: wave w takes d_k tiles w, w + 4, ...; the B operand is
+  // O = probs . V: wave w takes d_k tiles w, w + NW, ...; the B operand is
   // V[key 16kt + 4g + s][16dt + rl], one float per MFMA
   const float* Vl = reinterpret_cast<const float*>(smem + C::K_OFF);
-  for (int dt = w; dt < DK / 16; dt += 4) {
+  for (int dt = w; dt < DK / 16; dt += NW) {
     floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
     for (int kt = 0; kt < nkt; ++kt) {
       const floatx4 a = *reinterpret_cast<const floatx4*>(Sl + rl * LMAX + kt * 16 + 4 * g);
@@ -1070,8 +1100,8 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
   if (dt == kF32) {
     if (p.T <= CfgS<128>::NQ && p.L <= CfgS<128>::LMAX && !p.dbg_bd) {
       const dim3 grid(p.H, nb);
-      if (head_dim == 64) hipLaunchKernelGGL(attn_chunk_f32_kernel<64>, grid, dim3(256), 0, s, p);
-      else if (head_dim == 128) hipLaunchKernelGGL(attn_chunk_f32_kernel<128>, grid, dim3(256), 0, s, p);
+      if (head_dim == 64) hipLaunchKernelGGL(attn_chunk_f32_kernel<64>, grid, dim3(CfgS<64>::NT), 0, s, p);
+      else if (head_dim == 128) hipLaunchKernelGGL(attn_chunk_f32_kernel<128>, grid, dim3(CfgS<128>::NT), 0, s, p);
       else return hipErrorInvalidValue;
       return hipGetLastError();
     }
