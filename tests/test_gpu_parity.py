@@ -276,6 +276,33 @@ def test_linear_bf16_bias_large(rows):
         assert np.all(d <= bound), name
 
 
+@pytest.mark.parametrize("rows,quant", [(700, False), (700, True), (125, False), (33, True)])
+def test_linear_f32_persistent_tiles(rows, quant):
+    """fp32 y = x W^T + b on row counts that take the K-parallel kernel with
+    persistent workgroups: 700 rows are 22 x 32 tiles of 32 x 32, three per
+    workgroup, so ranges cross from one row tile into the next (the A rows
+    are reloaded mid-range) and the last row tile is ragged; 125 and 33 rows
+    give one tile per workgroup. Dense and u8 weights, with biases, within
+    1e-5 of the float64 oracle."""
+    D, H = 1024, 8
+    rng = np.random.default_rng(61)
+    w = W.make_layer_weights(rng, D, H, True, quant, centred=True)
+    for name in ("linear_q", "linear_out"):
+        if quant:
+            s = rng.uniform(1e-4, 1e-3, size=w[f"{name}.scales"].shape)
+            w[f"{name}.scales"] = s.astype(np.float16)
+            b = -128.0 * w[f"{name}.scales"].astype(np.float64) + rng.normal(0, 1e-3, size=s.shape)
+            w[f"{name}.biases"] = b.astype(np.float16)
+        w[f"{name}.bias"] = rng.normal(0, 0.1, D).astype(w[f"{name}.bias"].dtype)
+    p = oracle_params(w, D, H)
+    layer = gpu_layer(w, D, H, True, O.F32)
+    x = rng.standard_normal((rows, D)).astype(np.float32)
+    for name in ("linear_q", "linear_out"):
+        got = host(layer.debug_linear(name, dev(x, O.F32)))
+        ref = getattr(p, name).forward(x.astype(np.float64), O.F32)
+        assert rel_err(got, ref) < 1e-5, name
+
+
 def test_forward_bf16_with_biases():
     """The offline bf16 layer with non-zero linear biases (the V bias enters
     through the transposed V epilogue), B=2, T=375, key padding; biases of
