@@ -160,31 +160,62 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
   const char* vbase = reinterpret_cast<const char*>(p.v) + ((int64_t)b * p.kv_bs + h * DK) * sizeof(T);
   const char* pbase = reinterpret_cast<const char*>(p.p) + (int64_t)h * DK * sizeof(T);
 
-  for (int j0 = (jbeg / NK) * NK; j0 < jend; j0 += NK) {
-    __syncthreads();  // previous tile fully consumed
-    // K rows and V^T (transposed on the way in), zero past the last key.
-    constexpr int CPR = C::RB / 16;
-    for (int c = tid; c < NK * CPR; c += NT) {
-      const int row = c / CPR, cb = (c % CPR) * 16;
-      const int j = j0 + row;
-      const bool ok = j < p.L;
-      const int64_t off = (int64_t)(ok ? key_row(p, j) : 0) * p.kv_rs * sizeof(T) + cb;
-      *reinterpret_cast<u32x4*>(Ks + row * C::KP + cb) = load16<u32x4>(kbase + off, ok);
-      const frag_t vv = load16<frag_t>(vbase + off, ok);
-      const int d0 = cb / (int)sizeof(T);
+  // A key tile's K rows, V rows and position rows pmin .. pmin + PR - 1 are
+  // loaded into registers one tile ahead (while the previous tile computes)
+  // and stored to LDS at the top of their tile: rows past the last key or
+  // outside the table read row 0 and are zeroed, so every load is issued
+  // unconditionally.
+  constexpr int CPR = C::RB / 16;                       // 16-byte chunks per row
+  constexpr int NKV = (NK * CPR + NT - 1) / NT;         // K / V chunks per thread
+  constexpr int NPC = (C::PR * CPR + NT - 1) / NT;      // position chunks per thread
+  u32x4 kr[NKV], pr[NPC];
+  frag_t vr[NKV];
+  auto fetch = [&](int j0) {
 #pragma unroll
-      for (int e = 0; e < EPL; ++e)
-        *reinterpret_cast<T*>(Vt + (d0 + e) * C::VP + row * (int)sizeof(T)) = vv[e];
+    for (int i = 0; i < NKV; ++i) {
+      const int c = tid + i * NT, row = min(c / CPR, NK - 1), cb = (c % CPR) * 16;
+      const int j = j0 + row;
+      const bool ok = c < NK * CPR && j < p.L;
+      const int64_t off = (int64_t)(ok ? key_row(p, j) : 0) * p.kv_rs * sizeof(T) + cb;
+      const u32x4 kv = *reinterpret_cast<const u32x4*>(kbase + off);
+      const frag_t vv = *reinterpret_cast<const frag_t*>(vbase + off);
+      kr[i] = ok ? kv : u32x4{0u, 0u, 0u, 0u};
+      vr[i] = ok ? vv : frag_t{};
     }
-    // Position rows pmin .. pmin + PR - 1 (zero outside the table).
     const int pmin = p.center - p.qoff - (i0 + QB - 1) + j0;
-    for (int c = tid; c < C::PR * CPR; c += NT) {
-      const int row = c / CPR, cb = (c % CPR) * 16;
+#pragma unroll
+    for (int i = 0; i < NPC; ++i) {
+      const int c = tid + i * NT, row = min(c / CPR, C::PR - 1), cb = (c % CPR) * 16;
       const int tp = pmin + row;
-      const bool ok = tp >= 0 && tp < p.p_rows;
-      *reinterpret_cast<u32x4*>(Ps + row * C::KP + cb) =
-          load16<u32x4>(pbase + (int64_t)(ok ? tp : 0) * p.p_rs * sizeof(T) + cb, ok);
+      const bool ok = c < C::PR * CPR && tp >= 0 && tp < p.p_rows;
+      const u32x4 pv = *reinterpret_cast<const u32x4*>(pbase + (int64_t)(ok ? tp : 0) * p.p_rs * sizeof(T) + cb);
+      pr[i] = ok ? pv : u32x4{0u, 0u, 0u, 0u};
     }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < NKV; ++i) {
+      const int c = tid + i * NT, row = c / CPR, cb = (c % CPR) * 16;
+      if (c >= NK * CPR) break;
+      *reinterpret_cast<u32x4*>(Ks + row * C::KP + cb) = kr[i];
+      const int d0 = cb / (int)sizeof(T);  // V^T: transposed on the way in
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) *reinterpret_cast<T*>(Vt + (d0 + e) * C::VP + row * (int)sizeof(T)) = vr[i][e];
+    }
+#pragma unroll
+    for (int i = 0; i < NPC; ++i) {
+      const int c = tid + i * NT, row = c / CPR, cb = (c % CPR) * 16;
+      if (c >= C::PR * CPR) break;
+      *reinterpret_cast<u32x4*>(Ps + row * C::KP + cb) = pr[i];
+    }
+  };
+  const int jstart = (jbeg / NK) * NK;
+  const int jlast = jend > jstart ? jstart + (jend - 1 - jstart) / NK * NK : jstart;
+  if (jstart < jend) fetch(jstart);
+  for (int j0 = jstart; j0 < jend; j0 += NK) {
+    __syncthreads();  // previous tile fully consumed
+    stash();
+    fetch(min(j0 + NK, jlast));  // (the last tile loads itself again, unused)
     __syncthreads();
 
     // S^T = K Qu^T and the wave's band B'^T = P' Qv^T.
