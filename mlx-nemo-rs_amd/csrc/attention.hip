@@ -111,22 +111,29 @@ struct Cfg {
   static constexpr int NB = NU + 1;                        // 16-row band sub-tiles
 };
 
-template <typename T, int DK, int NW, bool DEBUG>
+// KS (key split, for inputs too short to give every CU a workgroup): the NW
+// waves of a workgroup share its 16 queries and take the key tiles w,
+// w + NW, ... each with LDS tiles of its own and no workgroup barrier in the
+// loop; their softmax states (running maximum, sum, O) are merged at the end.
+template <typename T, int DK, int NW, bool DEBUG, bool KS = false>
 __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
-  using C = Cfg<T, DK, NW>;
+  using C = Cfg<T, DK, KS ? 1 : NW>;  // (split: one wave's tile geometry, 16 queries)
   using F = Frag<T>;
   using frag_t = typename F::type;
   constexpr int NT = C::NT, QB = C::QB, NK = C::NK, EPL = F::EPL;
-  __shared__ __attribute__((aligned(16))) char smem[C::LDS];
-  char* Ks = smem + C::K_OFF;
-  char* Vt = smem + C::V_OFF;
-  char* Ps = smem + C::P_OFF;
+  __shared__ __attribute__((aligned(16))) char smem[KS ? NW * C::LDS : C::LDS];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, ql = lane & 15;
+  const int tt = KS ? lane : tid;  // this thread's index among the threads that load a tile
+  char* const tb = smem + (KS ? w * C::LDS : 0);
+  char* Ks = tb + C::K_OFF;
+  char* Vt = tb + C::V_OFF;
+  char* Ps = tb + C::P_OFF;
   const int bl = blockIdx.z, b = p.b0 + bl, h = blockIdx.y;
   const int i0 = blockIdx.x * QB;
-  const int qi = i0 + 16 * w + ql;  // this lane's query column
-  float* Rm = reinterpret_cast<float*>(smem + C::R_OFF) + w * 16 * C::RMP;
+  const int wq = KS ? 0 : w;        // this wave's 16-query group in the block
+  const int qi = i0 + 16 * wq + ql;  // this lane's query column
+  float* Rm = reinterpret_cast<float*>(tb + C::R_OFF) + wq * 16 * C::RMP;
 
   // Queries with the position biases folded in, rounded like the reference's
   // bf16 adds; they are the B operand of both score products.
@@ -173,7 +180,7 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
   auto fetch = [&](int j0) {
 #pragma unroll
     for (int i = 0; i < NKV; ++i) {
-      const int c = tid + i * NT, row = min(c / CPR, NK - 1), cb = (c % CPR) * 16;
+      const int c = tt + i * NT, row = min(c / CPR, NK - 1), cb = (c % CPR) * 16;
       const int j = j0 + row;
       const bool ok = c < NK * CPR && j < p.L;
       const int64_t off = (int64_t)(ok ? key_row(p, j) : 0) * p.kv_rs * sizeof(T) + cb;
@@ -185,7 +192,7 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
     const int pmin = p.center - p.qoff - (i0 + QB - 1) + j0;
 #pragma unroll
     for (int i = 0; i < NPC; ++i) {
-      const int c = tid + i * NT, row = min(c / CPR, C::PR - 1), cb = (c % CPR) * 16;
+      const int c = tt + i * NT, row = min(c / CPR, C::PR - 1), cb = (c % CPR) * 16;
       const int tp = pmin + row;
       const bool ok = c < C::PR * CPR && tp >= 0 && tp < p.p_rows;
       const u32x4 pv = *reinterpret_cast<const u32x4*>(pbase + (int64_t)(ok ? tp : 0) * p.p_rs * sizeof(T) + cb);
@@ -195,7 +202,7 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
   auto stash = [&]() {
 #pragma unroll
     for (int i = 0; i < NKV; ++i) {
-      const int c = tid + i * NT, row = c / CPR, cb = (c % CPR) * 16;
+      const int c = tt + i * NT, row = c / CPR, cb = (c % CPR) * 16;
       if (c >= NK * CPR) break;
       *reinterpret_cast<u32x4*>(Ks + row * C::KP + cb) = kr[i];
       const int d0 = cb / (int)sizeof(T);  // V^T: transposed on the way in
@@ -204,19 +211,23 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
     }
 #pragma unroll
     for (int i = 0; i < NPC; ++i) {
-      const int c = tid + i * NT, row = c / CPR, cb = (c % CPR) * 16;
+      const int c = tt + i * NT, row = c / CPR, cb = (c % CPR) * 16;
       if (c >= C::PR * CPR) break;
       *reinterpret_cast<u32x4*>(Ps + row * C::KP + cb) = pr[i];
     }
   };
-  const int jstart = (jbeg / NK) * NK;
-  const int jlast = jend > jstart ? jstart + (jend - 1 - jstart) / NK * NK : jstart;
-  if (jstart < jend) fetch(jstart);
-  for (int j0 = jstart; j0 < jend; j0 += NK) {
-    __syncthreads();  // previous tile fully consumed
+  // tiles of this wave (split) or of the workgroup: jfirst, jfirst + step, ...
+  constexpr int step = KS ? NK * NW : NK;
+  const int jfirst = (jbeg / NK) * NK + (KS ? NK * w : 0);
+  const int jlast = jend > jfirst ? jfirst + (jend - 1 - jfirst) / step * step : jfirst;
+  if (jfirst < jend) fetch(jfirst);
+  for (int j0 = jfirst; j0 < jend; j0 += step) {
+    // previous tile fully consumed (split: the wave's own tiles, whose LDS
+    // operations run in order)
+    if constexpr (!KS) __syncthreads();
     stash();
-    fetch(min(j0 + NK, jlast));  // (the last tile loads itself again, unused)
-    __syncthreads();
+    fetch(min(j0 + step, jlast));  // (the last tile loads itself again, unused)
+    if constexpr (!KS) __syncthreads();
 
     // S^T = K Qu^T and the wave's band B'^T = P' Qv^T.
     floatx4 s[C::NU], bd[C::NB];
@@ -224,7 +235,7 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
     for (int u = 0; u < C::NU; ++u) s[u] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < C::NB; ++t) bd[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    const int band0 = QB - 16 - 16 * w;  // first band row of this wave
+    const int band0 = QB - 16 - 16 * wq;  // first band row of this wave
 #pragma unroll
     for (int kf = 0; kf < C::NKF; ++kf) {
       const int cb = kf * 64 + g * 16;
@@ -322,6 +333,57 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
     }
   }
 
+  if constexpr (KS) {
+    // Merge the waves' states through LDS (each wave writes into its own
+    // tile area): query column ql, d_k rows 16 d + 4 g + r of O; wave w then
+    // finishes d_k rows 16 d + ... for d = w, w + NW, ...
+    static_assert(C::LDS >= (DK * 16 + 32) * 4, "merge area");
+    float* mo = reinterpret_cast<float*>(tb);
+    const float l_w = col_sum(l_run);
+    if (g == 0) {
+      mo[DK * 16 + ql] = m_run;
+      mo[DK * 16 + 16 + ql] = l_w;
+    }
+#pragma unroll
+    for (int d = 0; d < DK / 16; ++d)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mo[ql * DK + 16 * d + 4 * g + r] = o[d][r];
+    __syncthreads();
+    float mw[NW], m_all = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      mw[v] = reinterpret_cast<const float*>(smem + v * C::LDS)[DK * 16 + ql];
+      m_all = fmaxf(m_all, mw[v]);
+    }
+    float l_all = 0.f, f[NW];
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      // a wave that saw nothing has m = -inf, l = 0 and O = 0
+      f[v] = mw[v] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw[v] - m_all);
+      l_all += f[v] * reinterpret_cast<const float*>(smem + v * C::LDS)[DK * 16 + 16 + ql];
+    }
+    const float inv = l_all > 0.f ? 1.f / l_all : 0.f;
+    if (qi < p.T) {
+      T* orow = reinterpret_cast<T*>(p.o) + (int64_t)b * p.o_bs + (int64_t)qi * p.o_rs + h * DK;
+      for (int d = w; d < DK / 16; d += NW) {
+        T vals[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float acc = 0.f;
+#pragma unroll
+          for (int v = 0; v < NW; ++v)
+            acc += f[v] * reinterpret_cast<const float*>(smem + v * C::LDS)[ql * DK + 16 * d + 4 * g + r];
+          vals[r] = from_float<T>(acc * inv);
+        }
+        if constexpr (sizeof(T) == 2) {
+          *reinterpret_cast<u32x2*>(orow + 16 * d + 4 * g) = *reinterpret_cast<const u32x2*>(vals);
+        } else {
+          *reinterpret_cast<u32x4*>(orow + 16 * d + 4 * g) = *reinterpret_cast<const u32x4*>(vals);
+        }
+      }
+    }
+    return;
+  }
   // Normalise; a query that saw no key outputs zeros.
   const float l_tot = col_sum(l_run);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
@@ -1057,9 +1119,23 @@ hipError_t launch(const AttnParams& p, int nb, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Key split: 16 queries per workgroup, NW waves over its key tiles.
+template <typename T, int DK, int NW>
+hipError_t launch_ks(const AttnParams& p, int nb, hipStream_t s) {
+  dim3 grid((p.T + 15) / 16, p.H, nb);
+  hipLaunchKernelGGL((attn_kernel<T, DK, NW, false, true>), grid, dim3(64 * NW), 0, s, p);
+  return hipGetLastError();
+}
+
 template <typename T, int DK>
 hipError_t dispatch_nw(const AttnParams& p, int nb, hipStream_t s) {
   const bool dbg = p.dbg_bd != nullptr;
+  // fp32 inputs too short to give the CUs a workgroup each (one utterance of
+  // 125 frames: 16 workgroups of 64 queries) split their keys over the waves
+  if constexpr (sizeof(T) == 4) {
+    if (!dbg && p.T > 16 && (int64_t)nb * p.H * ((p.T + 63) / 64) < 128)
+      return launch_ks<T, DK, DK == 64 ? 4 : 2>(p, nb, s);  // (per-wave tiles: 34 / 64 KB of LDS)
+  }
   if (p.T <= 16) return dbg ? launch<T, DK, 1, true>(p, nb, s) : launch<T, DK, 1, false>(p, nb, s);
   return dbg ? launch<T, DK, 4, true>(p, nb, s) : launch<T, DK, 4, false>(p, nb, s);
 }
