@@ -855,13 +855,16 @@ __device__ __forceinline__ floatx4 kpar_load(__amdgpu_buffer_rsrc_t r, int voff,
   return __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
 }
 
-template <bool QUANT>
+template <bool QUANT, int TR>
 __global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
-  __shared__ __attribute__((aligned(16))) float red[2][16][1024];  // [tile parity][wave][element]
-  __shared__ __attribute__((aligned(16))) char xsm[16][2048];       // two 1 KB transpose slots per wave
+  // TR x TR blocks of 16x16 per tile: 32x32 tiles (TR = 2), or 16x16 tiles
+  // (TR = 1) for problems with too few 32x32 tiles to give each CU one
+  constexpr int TS = 16 * TR, EPW = 64 * 4 * TR * TR;  // tile side; partial sums per wave
+  __shared__ __attribute__((aligned(16))) float red[2][16][EPW];  // [tile parity][wave][element]
+  __shared__ __attribute__((aligned(16))) char xsm[16][1024 * TR];  // TR 1 KB transpose slots per wave
   const int tid = threadIdx.x, lane = tid & 63, nt_threads = (int)blockDim.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), nw = nt_threads >> 6;
-  const int tilesN = p.N / 32, T = (p.M + 31) / 32 * tilesN, G = (int)gridDim.x;
+  const int tilesN = p.N / TS, T = (p.M + TS - 1) / TS * tilesN, G = (int)gridDim.x;
   const int v0 = (int)((int64_t)blockIdx.x * T / G), v1 = (int)((int64_t)(blockIdx.x + 1) * T / G);
   if (v0 >= v1) return;  // (whole workgroup)
   const int kq = w * 64 + 4 * (lane & 3);   // quad-run chunk of the wave's k-columns
@@ -871,25 +874,24 @@ __global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
   const int xr = (lane & 15) * 64 + 16 * ((lane >> 4) ^ ((lane >> 2) & 3));
   // (A rows are addressed from the row tile's first row in the range-checked
   // VGPR offset, so rows past M read as zero)
-  const int voa0 = ((lane >> 2) * (int)p.lda + kq) * 4, voa1 = voa0 + 16 * (int)p.lda * 4;
+  const int voa = ((lane >> 2) * (int)p.lda + kq) * 4;
   const int groups = p.K / 64;
 
-  floatx4 a[2][4];
+  floatx4 a[TR][4];
   auto loadA = [&](int mt) {
     const __amdgpu_buffer_rsrc_t ra =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(reinterpret_cast<const float*>(p.A) + (int64_t)mt * 32 * p.lda),
-                                          (short)0, (int)((int64_t)(p.M - mt * 32) * p.lda * 4), kRawBuffer);
+        __builtin_amdgcn_make_buffer_rsrc((void*)(reinterpret_cast<const float*>(p.A) + (int64_t)mt * TS * p.lda),
+                                          (short)0, (int)((int64_t)(p.M - mt * TS) * p.lda * 4), kRawBuffer);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      a[0][s] = kpar_load(ra, voa0 + 64 * s, 0);
-      a[1][s] = kpar_load(ra, voa1 + 64 * s, 0);
-    }
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < TR; ++t) a[t][s] = kpar_load(ra, voa + t * 16 * (int)p.lda * 4 + 64 * s, 0);
     if (p.acopy && mt * tilesN >= v0 && mt * tilesN < v1) {
       // the workgroup holding the row tile's first column tile copies its
       // rows (each element once)
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int row = mt * 32 + 16 * t + (lane >> 2);
+      for (int t = 0; t < TR; ++t) {
+        const int row = mt * TS + 16 * t + (lane >> 2);
         if (row < p.M) {
           float* dst = reinterpret_cast<float*>(p.acopy) + mapped_row(p, row) * p.acopy_ld + kq;
 #pragma unroll
@@ -898,18 +900,17 @@ __global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
       }
     }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      kpar_xpose(xs, xw, xr, a[0][s]);
-      kpar_xpose(xs + 1024, xw, xr, a[1][s]);
-    }
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < TR; ++t) kpar_xpose(xs + 1024 * t, xw, xr, a[t][s]);
   };
 
   // W chunk (u, s) of the tile being computed (dense: quad-run layout; quant:
   // the codes), replaced by the next tile's chunk as soon as step s has taken
   // it, so the next tile's loads overlap this tile's MFMAs
-  floatx4 wd[2][4];
-  uint32_t wq[2][4];
-  floatx2 wsb[2], wsb_next[2];
+  floatx4 wd[TR][4];
+  uint32_t wq[TR][4];
+  floatx2 wsb[TR], wsb_next[TR];
   __amdgpu_buffer_rsrc_t rw, rs;
   int vow = 0, vos = 0;
   if constexpr (!QUANT) {
@@ -923,22 +924,22 @@ __global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
   }
   auto loadW = [&](int nt, int u, int s) {
     if constexpr (!QUANT)
-      wd[u][s] = kpar_load(rw, vow, (nt * 32 + 16 * u) * p.K * 4 + 64 * s);
+      wd[u][s] = kpar_load(rw, vow, (nt * TS + 16 * u) * p.K * 4 + 64 * s);
     else
-      wq[u][s] = __builtin_amdgcn_raw_buffer_load_b32(rw, vow, (nt * 32 + 16 * u) * p.K + 16 * s, 0);
+      wq[u][s] = __builtin_amdgcn_raw_buffer_load_b32(rw, vow, (nt * TS + 16 * u) * p.K + 16 * s, 0);
   };
-  auto loadSB = [&](int nt, floatx2 (&d)[2]) {
+  auto loadSB = [&](int nt, floatx2 (&d)[TR]) {
     if constexpr (QUANT) {
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
-        d[u] = __builtin_bit_cast(floatx2, __builtin_amdgcn_raw_buffer_load_b64(rs, vos, (nt * 32 + 16 * u) * groups * 8, 0));
+      for (int u = 0; u < TR; ++u)
+        d[u] = __builtin_bit_cast(floatx2, __builtin_amdgcn_raw_buffer_load_b64(rs, vos, (nt * TS + 16 * u) * groups * 8, 0));
     }
   };
 
   int mt_cur = v0 / tilesN;
   loadA(mt_cur);
 #pragma unroll
-  for (int u = 0; u < 2; ++u)
+  for (int u = 0; u < TR; ++u)
 #pragma unroll
     for (int s = 0; s < 4; ++s) loadW(v0 % tilesN, u, s);
   loadSB(v0 % tilesN, wsb);
@@ -946,16 +947,16 @@ __global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
     const int mt = v / tilesN, nt = v % tilesN;
     const int nn = min(v + 1, v1 - 1) % tilesN;  // the next tile's columns (the last tile reloads its own)
     loadSB(nn, wsb_next);
-    floatx4 acc[2][2];
+    floatx4 acc[TR][TR];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < TR; ++t)
 #pragma unroll
-      for (int u = 0; u < 2; ++u) acc[t][u] = floatx4{};
+      for (int u = 0; u < TR; ++u) acc[t][u] = floatx4{};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      floatx4 bf[2];
+      floatx4 bf[TR];
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
+      for (int u = 0; u < TR; ++u) {
         if constexpr (!QUANT) {
           kpar_xpose(xs + 1024 * u, xw, xr, wd[u][s]);
           bf[u] = wd[u][s];
@@ -969,29 +970,29 @@ __global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < TR; ++t)
 #pragma unroll
-          for (int u = 0; u < 2; ++u)
+          for (int u = 0; u < TR; ++u)
             acc[t][u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][s][j], bf[u][j], acc[t][u], 0, 0, 0);
     }
     if constexpr (QUANT) {
-      wsb[0] = wsb_next[0];
-      wsb[1] = wsb_next[1];
+#pragma unroll
+      for (int u = 0; u < TR; ++u) wsb[u] = wsb_next[u];
     }
-    // element 4 (2 t + u) + e of lane l: row 16 t + 4 (l / 16) + e, column 16 u + l % 16
-    float (&rb)[16][1024] = red[v & 1];
+    // element 4 (TR t + u) + e of lane l: row 16 t + 4 (l / 16) + e, column 16 u + l % 16
+    float (&rb)[16][EPW] = red[v & 1];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < TR; ++t)
 #pragma unroll
-      for (int u = 0; u < 2; ++u) *reinterpret_cast<floatx4*>(&rb[w][lane * 16 + 4 * (2 * t + u)]) = acc[t][u];
+      for (int u = 0; u < TR; ++u) *reinterpret_cast<floatx4*>(&rb[w][lane * 4 * TR * TR + 4 * (TR * t + u)]) = acc[t][u];
     __syncthreads();
     // (this buffer is written again two tiles on, after the next tile's
     // barrier, which every thread reaches only after its sums here)
-    for (int idx = tid; idx < 1024; idx += nt_threads) {
+    for (int idx = tid; idx < EPW; idx += nt_threads) {
       float sum = 0.f;
       for (int ww = 0; ww < nw; ++ww) sum += rb[ww][idx];
-      const int l = idx >> 4, tu = (idx >> 2) & 3, e = idx & 3;
-      const int row = mt * 32 + 16 * (tu >> 1) + 4 * (l >> 4) + e, col = nt * 32 + 16 * (tu & 1) + (l & 15);
+      const int l = idx / (4 * TR * TR), tu = (idx >> 2) % (TR * TR), e = idx & 3;
+      const int row = mt * TS + 16 * (tu / TR) + 4 * (l >> 4) + e, col = nt * TS + 16 * (tu % TR) + (l & 15);
       if (row >= p.M) continue;
       const float y = epilogue_value<float>(p, row, col, sum);
       if (!p.C2)
@@ -1005,9 +1006,19 @@ __global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
   }
 }
 
+// Tile side of the K-parallel kernel: 16x16 tiles when 32x32 tiles would
+// occupy at most half the CUs (the workgroup's chain of loads, MFMAs and
+// reduction is then the whole kernel, and a quarter-size tile shortens it:
+// measured 8.9 -> 6.6 us at 125 x 512 x 512 and 9.1 -> 7.9 us at 249 rows;
+// at 224 x 1024 x 1024, 224 tiles of 32x32, 16x16 tiles were slower, 12.3
+// against 13.5 us).
+int kpar_tile_rows(const GemmParams& p) {
+  return (int64_t)((p.M + 31) / 32) * (p.N / 32) <= 128 ? 1 : 2;
+}
+
 // Workgroups of the K-parallel kernel: as many tiles each as the tiles over
 // the CUs need, spread so that no workgroup has more.
-int kpar_grid(const GemmParams& p) {
+int kpar_grid(const GemmParams& p, int tr) {
   static int cus = 0;
   if (!cus) {
     int dev = 0, n = 0;
@@ -1016,9 +1027,19 @@ int kpar_grid(const GemmParams& p) {
       n = 256;
     cus = n;
   }
-  const int T = (p.M + 31) / 32 * (p.N / 32);
+  const int ts = 16 * tr;
+  const int T = (p.M + ts - 1) / ts * (p.N / ts);
   const int per = (T + cus - 1) / cus;
   return (T + per - 1) / per;
+}
+
+template <bool QUANT>
+hipError_t launch_kpar(const GemmParams& p, hipStream_t s) {
+  if (kpar_tile_rows(p) == 1)
+    hipLaunchKernelGGL((gemm_kpar_kernel<QUANT, 1>), dim3(kpar_grid(p, 1)), dim3(p.K), 0, s, p);
+  else
+    hipLaunchKernelGGL((gemm_kpar_kernel<QUANT, 2>), dim3(kpar_grid(p, 2)), dim3(p.K), 0, s, p);
+  return hipGetLastError();
 }
 
 // The K-parallel kernel applies to fp32, K = 64 .. 1024, 16-byte operand
@@ -1123,10 +1144,7 @@ template <typename T, bool QUANT>
 hipError_t dispatch(const GemmParams& p, hipStream_t s) {
   const int bk = ROWB / (int)sizeof(T);
   if constexpr (sizeof(T) == 4) {
-    if (p.C2 || p.acopy) {  // (validated by gemm())
-      hipLaunchKernelGGL((gemm_kpar_kernel<QUANT>), dim3(kpar_grid(p)), dim3(p.K), 0, s, p);
-      return hipGetLastError();
-    }
+    if (p.C2 || p.acopy) return launch_kpar<QUANT>(p, s);  // (validated by gemm())
   }
   if constexpr (sizeof(T) == 2) {
     hipError_t err;
@@ -1145,10 +1163,7 @@ hipError_t dispatch(const GemmParams& p, hipStream_t s) {
   // against 12.6 us at 749 x 1024 x 1024, so bf16 keeps split-K); the split
   // output and row copy only exist there
   if constexpr (sizeof(T) == 4) {
-    if (kpar_ok<T>(p)) {
-      hipLaunchKernelGGL((gemm_kpar_kernel<QUANT>), dim3(kpar_grid(p)), dim3(p.K), 0, s, p);
-      return hipGetLastError();
-    }
+    if (kpar_ok<T>(p)) return launch_kpar<QUANT>(p, s);
   }
   if (const int splits = split_count<T>(p)) {
     const int64_t tiles = (int64_t)((p.M + 63) / 64) * (p.N / 64);
