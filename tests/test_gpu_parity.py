@@ -210,6 +210,27 @@ def test_forward_f32_contexts_and_padding(d_model, n_heads, ctx):
     assert rel_err(got, ref, rows) < F32_TOL
 
 
+def test_forward_f32_many_query_blocks():
+    """fp32 at a size with enough query blocks for the whole-workgroup form of
+    the generic kernel (4 x 8 heads x 5 blocks of 64 queries = 160 workgroups;
+    short inputs take the key-split form): key padding and a chunked context,
+    against the float64 oracle."""
+    rng = np.random.default_rng(12)
+    d_model, n_heads, B, T = 512, 8, 4, 300
+    w = random_weights(rng, d_model, n_heads, scale=0.05)
+    p = oracle_params(w, d_model, n_heads)
+    lengths = [300, 257, 130, 64]
+    x = rng.standard_normal((B, T, d_model)).astype(np.float32)
+    pos = O.RelPositionalEncoding(d_model, 5000, False).get_encoding(T)
+    layer = gpu_layer(w, d_model, n_heads, True, O.F32)
+    for ctx in (None, ((64, 15), "chunked_limited")):
+        octx = O.AttentionContext.new(*ctx) if ctx else None
+        ref = O.mhsa_forward(p, x, pos, octx, O.key_padding_mask(lengths, T))
+        got = host(layer.forward(dev(x, O.F32), dev(pos, O.F32), M.AttentionContext.new(*ctx) if ctx else None,
+                                 M.key_padding_mask(lengths, T)))
+        assert rel_err(got, ref, visible_rows(B, T, octx, lengths)) < F32_TOL, ctx
+
+
 def test_forward_large_f32():
     """FastConformer-large layer, fp32, B=1, T=125 (10 s of audio)."""
     cfg = W.CONFIGS["large_f32"]
