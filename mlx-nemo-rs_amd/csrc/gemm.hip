@@ -360,10 +360,12 @@ struct TileCfg {
   static constexpr int DIST = NS - 1;
   static constexpr int WM = BM / 2, WN = BN / 2;  // per-wave block
   static constexpr int TM = WM / 32, TN = WN / 32;
-  static constexpr int ABYTES = BM * 128, STAGE = (BM + BN) * 128;
+  // a stage holds 64 k-columns: A rows of 128 bytes (bf16), B rows of 128
+  // bytes (bf16) or of 64 bytes (8-bit codes)
+  static constexpr int BROW = QUANT ? 64 : 128;
+  static constexpr int ABYTES = BM * 128, STAGE = BM * 128 + BN * BROW;
   static constexpr int NA = BM / 32;               // A loads per wave per stage (1 KB each)
-  static constexpr int NB = QUANT ? 0 : BN / 32;   // dense B loads per wave per stage
-  static constexpr int QB = BN / 64;               // quantized 16-code chunks per thread per stage
+  static constexpr int NB = BN * BROW / 4096;      // B loads per wave per stage (1 KB each)
   static constexpr int OP = WN * 2 + 16;           // staged output row pitch (bytes)
   // loads spread between MFMAs whenever a tile of at least 128 x 128 has a
   // CU to itself (a 64 x 64 tile has one MFMA per wave and k-step)
@@ -413,86 +415,75 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
   const char* Bb = reinterpret_cast<const char*>(p.W) + (int64_t)n0 * p.K * (QUANT ? 1 : 2);
   const __amdgpu_buffer_rsrc_t rb =
       __builtin_amdgcn_make_buffer_rsrc((void*)Bb, (short)0, (int)((int64_t)BN * p.K * (QUANT ? 1 : 2)), kRawBuffer);
-  int boff[C::NB > 0 ? C::NB : 1];
+  // dense B as A. Codes: load g of wave w fills LDS bytes 1024 (w NB + g) +
+  // [0, 1024) of the B region, 16 rows of 64 codes: lane l stores row
+  // l / 4, 16-byte chunk l % 4, which holds code chunk (l % 4) ^ ((row / 4) % 4)
+  int boff[C::NB];
 #pragma unroll
   for (int g = 0; g < C::NB; ++g) {
-    const int pos = (w * C::NB + g) * 64 + lane, row = pos >> 3;
-    boff[g] = (int)(row * p.K * 2 + 16 * ((pos & 7) ^ ((row >> 1) & 7)));
+    if constexpr (QUANT) {
+      const int row = (w * C::NB + g) * 16 + (lane >> 2);
+      boff[g] = (int)(row * p.K + 16 * ((lane & 3) ^ ((row >> 2) & 3)));
+    } else {
+      const int pos = (w * C::NB + g) * 64 + lane, row = pos >> 3;
+      boff[g] = (int)(row * p.K * 2 + 16 * ((pos & 7) ^ ((row >> 1) & 7)));
+    }
   }
+  constexpr int KB = QUANT ? 64 : 128;  // B bytes per row and stage
   auto issue = [&](int kt, int buf) {
     char* S = smem + buf * C::STAGE;
 #pragma unroll
     for (int g = 0; g < C::NA; ++g)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(S + (w * C::NA + g) * 1024), 16, (int)aoff[g],
                                                (int)(kt * 128), 0, 0);
-    if constexpr (!QUANT) {
 #pragma unroll
-      for (int g = 0; g < C::NB; ++g)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(S + C::ABYTES + (w * C::NB + g) * 1024), 16,
-                                                 (int)boff[g], (int)(kt * 128), 0, 0);
-    }
+    for (int g = 0; g < C::NB; ++g)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(S + C::ABYTES + (w * C::NB + g) * 1024), 16,
+                                               (int)boff[g], (int)(kt * KB), 0, 0);
   };
   auto issue1 = [&](int g, int kt, int buf) {  // load g of this wave's stage stream
     char* S = smem + buf * C::STAGE;
     if (g < C::NA)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void*)(S + (w * C::NA + g) * 1024), 16, (int)aoff[g],
                                                (int)(kt * 128), 0, 0);
-    else if constexpr (!QUANT)
+    else
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void*)(S + C::ABYTES + (w * C::NB + g - C::NA) * 1024), 16,
-                                               (int)boff[g - C::NA], (int)(kt * 128), 0, 0);
+                                               (int)boff[g - C::NA], (int)(kt * KB), 0, 0);
   };
-  // quantized B: chunk q = tid + 256 i holds codes 16 (q % 4) .. + 16 of row q / 4.
-  // Codes of stage s load into register set s % 2 two stages ahead and are
-  // dequantised into LDS during stage s - 1, between its MFMAs.
-  u32x4 qr[2][C::QB];
-  floatx2 qs[2][C::QB];
+  // Quantized B is dequantised in registers, fragment by fragment, one
+  // sub-step ahead of its MFMAs. Lane (row n, half h) reads the 32 codes
+  // 32 h + [0, 32) of its row per stage as two 16-byte LDS reads (cq[0]:
+  // sub-steps 0-1, cq[1]: 2-3); sub-step s takes codes 32 h + 8 s + [0, 8),
+  // and the A fragments take the same k-columns (chunk 4 h + s). Scale and
+  // bias of (row, group) for stage kt sit in register set kt % 2, loaded two
+  // stages ahead.
+  constexpr int TNQ = QUANT ? C::TN : 1;
+  u32x4 cq[2][TNQ];
+  floatx2 qsb[2][TNQ];
   const int groups = p.K / 64;
-  auto qload = [&](int kt, int set) {
+  const int qrow = wn * C::WN + (lane & 31);  // B row of fragment 0 within the tile
+  auto sbload = [&](int kt, int set) {
 #pragma unroll
-    for (int i = 0; i < C::QB; ++i) {
-      const int q = tid + 256 * i, r = q >> 2;
-      qr[set][i] = *reinterpret_cast<const u32x4*>(Bb + (int64_t)r * p.K + kt * 64 + (q & 3) * 16);
-      qs[set][i] = *reinterpret_cast<const floatx2*>(p.sb + 2 * ((int64_t)(n0 + r) * groups + kt));
-    }
+    for (int j = 0; j < TNQ; ++j)
+      qsb[set][j] = *reinterpret_cast<const floatx2*>(p.sb + 2 * ((int64_t)(n0 + qrow + 32 * j) * groups + kt));
   };
-  auto qstore = [&](int i, int set, int buf) {
-    char* Bs = smem + buf * C::STAGE + C::ABYTES;
-    // (opaque redefinition here: keeps the compiler from hoisting the
-    // dequantisation, and the wait for the codes, up to the loads)
-    asm volatile("" : "+v"(qr[set][i]), "+v"(qs[set][i]));
-    const int q = tid + 256 * i, r = q >> 2, c2 = 2 * (q & 3);
-    bf16 v[16];
-    dequant16<bf16>(qr[set][i], qs[set][i].x, qs[set][i].y, v);
-    *reinterpret_cast<u32x4*>(Bs + r * 128 + 16 * (c2 ^ ((r >> 1) & 7))) = reinterpret_cast<const u32x4*>(v)[0];
-    *reinterpret_cast<u32x4*>(Bs + r * 128 + 16 * ((c2 + 1) ^ ((r >> 1) & 7))) = reinterpret_cast<const u32x4*>(v)[1];
-  };
-  // The same work cut into 9 pieces per chunk (8 pairs of codes, then the two
-  // stores), so that it can sit between MFMAs without starving them.
-  bf16 qv[C::QB][16];
-  auto qpiece = [&](int i, int k, int set, int buf) {
-    if (k == 0) asm volatile("" : "+v"(qr[set][i]), "+v"(qs[set][i]));
-    if (k < 8) {
+  // LDS offset of code chunk 2 (lane / 32) + u of fragment j's row
+  int cqo[2];
 #pragma unroll
-      for (int e = 2 * k; e < 2 * k + 2; ++e) {
-        const float code = (float)((qr[set][i][e >> 2] >> (8 * (e & 3))) & 0xFFu);
-        qv[i][e] = (bf16)__builtin_fmaf(qs[set][i].x, code, qs[set][i].y);
-      }
-    } else {
-      char* Bs = smem + buf * C::STAGE + C::ABYTES;
-      const int q = tid + 256 * i, r = q >> 2, c2 = 2 * (q & 3);
-      *reinterpret_cast<u32x4*>(Bs + r * 128 + 16 * (c2 ^ ((r >> 1) & 7))) = reinterpret_cast<const u32x4*>(qv[i])[0];
-      *reinterpret_cast<u32x4*>(Bs + r * 128 + 16 * ((c2 + 1) ^ ((r >> 1) & 7))) =
-          reinterpret_cast<const u32x4*>(qv[i])[1];
-    }
+  for (int u = 0; u < 2; ++u) cqo[u] = C::ABYTES + qrow * 64 + 16 * ((2 * (lane >> 5) + u) ^ ((qrow >> 2) & 3));
+  auto cread = [&](const char* S, int u) {
+#pragma unroll
+    for (int j = 0; j < TNQ; ++j) cq[u][j] = *reinterpret_cast<const u32x4*>(S + cqo[u] + j * 32 * 64);
   };
 
   // fragment (t, s): rows 32 t + lane % 32 of this wave's block, k-chunk
-  // 2 s + lane / 32 of the stage
+  // 2 s + lane / 32 of the stage (quantized B: 4 (lane / 32) + s, above)
   const int arow = (wm * C::WM + (lane & 31)) * 128;
   const int brow = C::ABYTES + (wn * C::WN + (lane & 31)) * 128;
   int so[4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) so[s] = 16 * ((2 * s + (lane >> 5)) ^ ((lane >> 1) & 7));
+  for (int s = 0; s < 4; ++s)
+    so[s] = 16 * ((QUANT ? 4 * (lane >> 5) + s : 2 * s + (lane >> 5)) ^ ((lane >> 1) & 7));
 
   floatx16 acc[C::TN][C::TM];
 #pragma unroll
@@ -500,23 +491,44 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
 #pragma unroll
     for (int i = 0; i < C::TM; ++i) acc[j][i] = floatx16{};
 
+  bf16x8 fa[2][C::TM], fb[2][C::TN];
+  u32x4 fq[2][TNQ];  // dequantised B fragments, as packed bf16 pairs
+  // half (e4) of fragment j for sub-step t: codes from cq, scale and bias
+  // from set st (the same rounding as the dequantisation kernel); each pair
+  // of values is one packed conversion
+  auto deq4 = [&](int j, int t, int e4, int st) {
+    if constexpr (QUANT) {
+      const uint32_t c = cq[t >> 1][j][2 * (t & 1) + e4];
+      float f[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) f[e] = __builtin_fmaf(qsb[st][j].x, (float)((c >> (8 * e)) & 0xFFu), qsb[st][j].y);
+      const bf16x2 lo = {(bf16)f[0], (bf16)f[1]}, hi = {(bf16)f[2], (bf16)f[3]};
+      fq[t & 1][j][2 * e4] = __builtin_bit_cast(uint32_t, lo);
+      fq[t & 1][j][2 * e4 + 1] = __builtin_bit_cast(uint32_t, hi);
+    }
+  };
+  auto bfr = [&](int b, int j) -> bf16x8 {
+    if constexpr (QUANT) return __builtin_bit_cast(bf16x8, fq[b][j]);
+    else return fb[b][j];
+  };
+
   const int nk = p.K / 64;
 #pragma unroll
   for (int st = 0; st < C::DIST; ++st) issue(min(st, nk - 1), st);
   if constexpr (QUANT) {
-    qload(0, 0);
-    qload(min(1, nk - 1), 1);
-#pragma unroll
-    for (int i = 0; i < C::QB; ++i) qstore(i, 0, 0);
+    sbload(0, 0);
+    sbload(min(1, nk - 1), 1);
+    __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) lgkmcnt(0): stage 0 landed
   }
   __syncthreads();
 
-  bf16x8 fa[2][C::TM], fb[2][C::TN];
   auto rd = [&](const char* S, int s, int b) {
 #pragma unroll
     for (int i = 0; i < C::TM; ++i) fa[b][i] = *reinterpret_cast<const bf16x8*>(S + arow + i * 4096 + so[s]);
+    if constexpr (!QUANT) {
 #pragma unroll
-    for (int j = 0; j < C::TN; ++j) fb[b][j] = *reinterpret_cast<const bf16x8*>(S + brow + j * 4096 + so[s]);
+      for (int j = 0; j < C::TN; ++j) fb[b][j] = *reinterpret_cast<const bf16x8*>(S + brow + j * 4096 + so[s]);
+    }
   };
   // Stage kt (par = kt % 2, a literal at each call so register sets stay
   // static). Loads of the next stage go to the other buffer (free since the
@@ -527,34 +539,37 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
     const char* S = smem + cur * C::STAGE;
     // stage kt + DIST streams into buffer (kt - 1) % NS, read last in stage kt - 1
     const int ktn = min(kt + C::DIST, nk - 1), nd = (kt + C::DIST) % C::NS;
-    if constexpr (QUANT) qload(min(kt + 2, nk - 1), par);  // set par held stage kt, stored during kt - 1
     if constexpr (!C::ILV) issue(ktn, nd);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       if (s < 3) {
+        if (QUANT && s == 0) cread(S, 1);
         rd(S, s + 1, (s + 1) & 1);
       } else {
-        // this wave's operand reads and its loads and stores of stage kt + 1
-        // are done (the memory operations issued after stage kt + 1's
-        // loads, those of DIST - 1 later stages, may still be in flight);
-        // after the barrier every wave's are
-        constexpr int vm = (C::DIST - 1) * (C::NA + C::NB + (QUANT ? 2 * C::QB : 0));
+        // this wave's operand reads and its loads of stage kt + 1 are done
+        // (the memory operations issued after stage kt + 1's loads, those of
+        // DIST - 1 later stages and their scale loads, may still be in
+        // flight); after the barrier every wave's are
+        constexpr int vm = (C::DIST - 1) * (C::NA + C::NB + (QUANT ? C::TN : 0));
         static_assert(vm < 64, "vmcnt range");
         __builtin_amdgcn_s_waitcnt((vm & 15) | ((vm >> 4) << 14) | (7 << 4));  // lgkmcnt(0)
         asm volatile("s_barrier" ::: "memory");
+        if constexpr (QUANT) cread(smem + nb * C::STAGE, 0);
         rd(smem + nb * C::STAGE, 0, 0);
+        if constexpr (QUANT) sbload(min(kt + 2, nk - 1), par);  // set par: last used in sub-step 2
       }
       __builtin_amdgcn_sched_barrier(0);
-      // quantized chunks of stage kt + 1 dequantised in sub-steps 0-2 (chunk
-      // i in sub-step i % 3), in pieces spread evenly between the MFMAs
+      // fragments of sub-step s + 1 (sub-step 0 of stage kt + 1 in sub-step
+      // 3) dequantised in 2 TN halves spread over this sub-step's MFMAs;
+      // sub-step 3 leaves its first third to the code reads just issued
       constexpr int NM = C::TM * C::TN;
-      const int nq = (s < 3 && QUANT) ? (C::QB - s + 2) / 3 : 0;  // chunks of this sub-step
       auto qpart = [&](int m) {
         if constexpr (QUANT) {
-          const int P = 9 * nq;
+          constexpr int P = 2 * C::TN;
+          const int m0 = s == 3 ? NM / 3 : 0, span = NM - m0;
 #pragma unroll
-          for (int pc = 0; pc < 9 * ((C::QB + 2) / 3); ++pc)
-            if (pc < P && pc * NM / P == m) qpiece(s + 3 * (pc / 9), pc % 9, par ^ 1, nb);
+          for (int pc = 0; pc < P; ++pc)
+            if (m0 + pc * span / P == m) deq4(pc >> 1, (s + 1) & 3, pc & 1, s == 3 ? par ^ 1 : par);
         }
       };
       if constexpr (C::ILV) {
@@ -565,7 +580,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
           const int j = m / C::TM, i = m % C::TM;
-          acc[j][i] = mma32(fb[s & 1][j], fa[s & 1][i], acc[j][i]);
+          acc[j][i] = mma32(bfr(s & 1, j), fa[s & 1][i], acc[j][i]);
           if (s < 3 && m % EV == EV - 1 && m / EV < DQ && s * DQ + m / EV < ND) issue1(s * DQ + m / EV, ktn, nd);
           qpart(m);
           __builtin_amdgcn_sched_barrier(0);
@@ -574,7 +589,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
           const int j = m / C::TM, i = m % C::TM;
-          acc[j][i] = mma32(fb[s & 1][j], fa[s & 1][i], acc[j][i]);
+          acc[j][i] = mma32(bfr(s & 1, j), fa[s & 1][i], acc[j][i]);
           if constexpr (QUANT) {
             qpart(m);
             __builtin_amdgcn_sched_barrier(0);
@@ -584,6 +599,11 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
       __builtin_amdgcn_sched_barrier(0);
     }
   };
+  if constexpr (QUANT) {
+    cread(smem, 0);
+#pragma unroll
+    for (int j = 0; j < C::TN; ++j) deq4(j, 0, 0, 0), deq4(j, 0, 1, 0);
+  }
   rd(smem, 0, 0);
   int kt = 0;
   for (; kt + 1 < nk; kt += 2) {
