@@ -635,6 +635,31 @@ def test_quantized_linear_full_shape(dtype):
             assert rel_err(got, ref) < 1e-5, name
 
 
+@pytest.mark.parametrize("d_model,n_heads,rows", [(384, 6, 1537), (768, 6, 3000)])
+def test_quantized_linear_bf16_tile_shapes(d_model, n_heads, rows):
+    """The bf16 dequant-GEMM on shapes that take the other tile paths: d_model
+    384 with 1537 rows gives 64x64 tiles over six k-stages and a ragged last
+    row tile; 768 with 3000 rows gives larger tiles over 12 stages. Codes, scales and biases as the stack specifies; every output
+    within one bf16 ulp of the oracle plus one fp32 rounding unit of
+    sum |x||w|, as in the full-shape test."""
+    rng = np.random.default_rng(71)
+    w = W.make_layer_weights(rng, d_model, n_heads, False, True)
+    p = oracle_params(w, d_model, n_heads)
+    layer = gpu_layer(w, d_model, n_heads, False, O.BF16)
+    x = O.bf16_round(rng.normal(size=(rows, d_model)))
+    xd = dev(x, O.BF16)
+    for name in ("linear_q", "linear_out"):
+        got = host(layer.debug_linear(name, xd))
+        lin = getattr(p, name)
+        ref = lin.forward(x, O.BF16)
+        _, e = np.frexp(ref)
+        ulp = np.ldexp(1.0, e - 8)
+        acc = np.abs(x) @ np.abs(lin.dense_weight(O.BF16)).T * 2.0 ** -24
+        d = np.abs(got - ref)
+        print(f"{name} d_model={d_model}: {int(np.sum(d > ulp))} of {d.size} beyond 1 ulp")
+        assert np.all(d <= ulp + acc), name
+
+
 def test_stack_u8_well_conditioned_against_oracle():
     """Two quantized sublayers (pre-LN, residual) at B=2, T=300 with codes
     U{0..255}, scales U(1e-4, 1e-3) and biases -128 s + N(0, 1e-3), so weights
