@@ -342,6 +342,26 @@ def test_forward_bf16_with_biases():
     assert err < BF16_TOL
 
 
+def test_forward_bf16_more_blocks_than_cus():
+    """The offline bf16 layer on a shape with more query blocks than CUs
+    (8 items of 1000-1100 valid frames, T = 1100, 4 heads: about 270 blocks
+    of 128 queries, so workgroups run in two rounds), 9 key tiles per block
+    and key padding, against the oracle within the bf16 tolerance."""
+    D, H, T, B = 512, 4, 1100, 8
+    w, rng = _biased_weights(81, D, H, 0.1)
+    x = rng.normal(size=(B, T, D))
+    lengths = [int(v) for v in rng.integers(1000, T + 1, size=B)]
+    lengths[0] = T
+    p = oracle_params(w, D, H)
+    pos = O.RelPositionalEncoding(D, 5000, True).get_encoding(T)
+    ref = O.mhsa_forward(p, O.bf16_round(x), O.bf16_round(pos), None, O.key_padding_mask(lengths, T), dtype=O.BF16)
+    layer = gpu_layer(w, D, H, True, O.BF16)
+    got = host(layer.forward(dev(x, O.BF16), dev(pos, O.BF16), None, M.key_padding_mask(lengths, T)))
+    err = abs_err(got, ref)
+    print(f"bf16 two rounds: max abs error {err:.3e} (max |ref| {np.max(np.abs(ref)):.2f})")
+    assert err < BF16_TOL
+
+
 def test_bf16_scores_growing_far_past_first_tile():
     """Scores that grow along the keys by thousands (x_t = g(t) z + noise with
     g rising to 31, so q_i . k_j scales with g(i) g(j)) exceed the first key
