@@ -422,14 +422,13 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
 //    band tile of one key tile is the first of the next, so two are computed
 //    per step. Ring row rr holds position row R0 + rr with R0 the first row
 //    any wave needs: tile k uses rr in [64k + 32, 64k + 192) and loads
-//    [64k + 192, 64k + 256) for tile k + 1, 224 live rows. The per-row
-//    position-term offsets (below) ride along in a 256-entry float ring.
+//    [64k + 192, 64k + 256) for tile k + 1, 224 live rows.
 //  * LDS rows are unpadded; 16-byte chunk j of a K, V^T or ring row r sits
 //    at chunk j ^ (r % chunks-per-row), so the 8 lanes an LDS read serves
 //    together hit 8 distinct bank groups.
-//  * Only q_u = q + pos_bias_u is held in registers. The position term uses
-//    q_v P^T = q_u P^T - (u - v) . P[n]; the per-row constant comes from
-//    pos_bias_diff and is the band MFMA's initial accumulator.
+//  * q_u = q + pos_bias_u and q_v = q + pos_bias_v are both held in
+//    registers (bf16, as the reference adds them in the activation dtype,
+//    attention.rs:501-508): q_u for the scores, q_v for the band.
 //  * bd is rounded to bf16 in the remap strip, as the reference stores
 //    matrix_bd in bf16 (attention.rs:530). The logits are
 //    s * (q_u k + bd): the reference scales bd by cast(s) (attention.rs:
@@ -451,8 +450,7 @@ struct Cfg2 {
   static constexpr int K_OFF = 0;                    // two K tiles
   static constexpr int V_OFF = 2 * KBUF;             // two V^T tiles
   static constexpr int P_OFF = V_OFF + 2 * VBUF;     // position ring
-  static constexpr int D_OFF = P_OFF + RING * RB;    // offset ring (floats)
-  static constexpr int R_OFF = D_OFF + RING * 4;     // remap strips
+  static constexpr int R_OFF = P_OFF + RING * RB;    // remap strips
   static constexpr int LDS = R_OFF + NW * 32 * RMP * 2;
   static constexpr int NS = DK / 16;                 // 16-wide d_k steps
   static constexpr int KDMA = KBUF / 1024 / NW;      // 1 KB direct-to-LDS loads per wave and tile
@@ -460,7 +458,7 @@ struct Cfg2 {
   static constexpr int RPL = 1024 / RB;              // position rows per 1 KB load
   static constexpr int PDMA = 64 / RPL / NW;         // position loads per wave for 64 rows
   static_assert(KDMA * NW * 1024 == KBUF && VDMA * NW * 1024 == VBUF && PDMA * NW * RPL == 64, "tile split");
-  static_assert(KDMA + VDMA <= NS && PDMA + 1 <= NS, "one load per band / score MFMA step");
+  static_assert(KDMA + VDMA <= NS && PDMA <= NS, "one load per band / score MFMA step");
   static_assert(LDS <= 160 * 1024, "LDS");
 };
 
@@ -497,21 +495,26 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 
   // q_u fragments (B operand): lane holds d_k values 16s + 8hh + [0, 8).
   // Rows past T read the last row (finite; their keys are all masked).
-  bf16x8 qu[NS];
+  bf16x8 qu[NS], qv[NS];
   {
     const bf16* qrow =
         reinterpret_cast<const bf16*>(p.q) + (int64_t)b * p.q_bs + (int64_t)min(qi, p.T - 1) * p.q_rs + h * DK;
     const float* bu = p.bias_u + h * DK;
+    const float* bv = p.bias_v + h * DK;
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       const int d0 = 16 * s + 8 * hh;
       const bf16x8 raw = *reinterpret_cast<const bf16x8*>(qrow + d0);
       const floatx4 b0 = *reinterpret_cast<const floatx4*>(bu + d0);
       const floatx4 b1 = *reinterpret_cast<const floatx4*>(bu + d0 + 4);
+      const floatx4 c0 = *reinterpret_cast<const floatx4*>(bv + d0);
+      const floatx4 c1 = *reinterpret_cast<const floatx4*>(bv + d0 + 4);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         qu[s][e] = (bf16)((float)raw[e] + b0[e]);
         qu[s][e + 4] = (bf16)((float)raw[e + 4] + b1[e]);
+        qv[s][e] = (bf16)((float)raw[e] + c0[e]);
+        qv[s][e + 4] = (bf16)((float)raw[e + 4] + c1[e]);
       }
     }
   }
@@ -531,7 +534,6 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   const char* kbase = reinterpret_cast<const char*>(p.k) + ((int64_t)b * p.kv_bs + h * DK) * 2;
   const char* vtbase = reinterpret_cast<const char*>(p.vt) + ((int64_t)h * DK * p.vt_ld + (int64_t)b * p.vt_bs) * 2;
   const char* pbase = reinterpret_cast<const char*>(p.p) + h * DK * 2;
-  const float* pdh = p.pdiff + (int64_t)h * p.pdiff_ld + p.p_pad;  // row n at pdh[n], |n| within the pad
 
   // Direct-to-LDS loads (buffer_load ... lds): each stream has a buffer
   // resource over its readable range, a uniform per-tile offset (soffset) and
@@ -546,8 +548,6 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   const char* pslack = pbase - (int64_t)p.p_pad * p.p_rs * 2;  // first readable position row
   const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
       (void*)pslack, (short)0, (int)((int64_t)(p.p_rows + 2 * p.p_pad) * p.p_rs * 2 - h * DK * 2), kRawBuffer);
-  const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)(pdh - p.p_pad), (short)0, (int)((int64_t)(p.p_rows + 2 * p.p_pad) * 4), kRawBuffer);
   // (passed to the builtins as (int) prvalues: an argument naming a variable
   // the lambda captured by reference makes the host compilation pass drop
   // the kernel's launch stub)
@@ -583,8 +583,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
                                                0);
   };
   // single loads of the same streams: load g of this wave's K and V^T share
-  // of key tile jn into buffer bn; load g of its ring share (g == PDMA: the
-  // offsets, wave 0)
+  // of key tile jn into buffer bn; load g of its ring share
   auto dma_kv = [&](int g, int jn, int bn) {
     if (g < C::KDMA)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(smem + C::K_OFF + bn * C::KBUF + (w * C::KDMA + g) * 1024), 16,
@@ -595,17 +594,13 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   };
   auto dma_ring = [&](int g, int rr0) {
     const int n0 = R0 + rr0 + p.p_pad;
-    if (g < C::PDMA)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rp, (lds_void*)(smem + C::P_OFF + ((rr0 + (w * C::PDMA + g) * C::RPL) % C::RING) * RB), 16, (int)roff[g],
-          n0 * (int)p.p_rs * 2, 0, 0);
-    else if (w == 0)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void*)(smem + C::D_OFF + (rr0 % C::RING) * 4), 4, lane * 4,
-                                               n0 * 4, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rp, (lds_void*)(smem + C::P_OFF + ((rr0 + (w * C::PDMA + g) * C::RPL) % C::RING) * RB), 16, (int)roff[g],
+        n0 * (int)p.p_rs * 2, 0, 0);
   };
   // Ring rows [rr0, rr0 + 64) (rr0 a multiple of 64): this wave's share of
-  // the position rows, and (wave 0) their offsets. Rows outside the table
-  // read the p_pad slack around it (finite; the offsets there are zero).
+  // the position rows. Rows outside the table read the p_pad slack around it
+  // (finite).
   // Every pair reading such a row lies outside its query's interval (past the
   // last key or query, or beyond a window the table was checked to cover), so
   // it is masked, and the values it reads cannot reach the output.
@@ -617,9 +612,6 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rp, (lds_void*)(ring + ((rr0 + (w * C::PDMA + g) * C::RPL) % C::RING) * RB), 16, (int)roff[g],
           n0 * (int)p.p_rs * 2, 0, 0);
-    if (w == 0)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void*)(smem + C::D_OFF + (rr0 % C::RING) * 4), 4, lane * 4,
-                                               n0 * 4, 0, 0);
   };
 
   // This lane's byte offset of the 16-byte chunk 2st + hh of row c in a
@@ -629,22 +621,11 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   for (int st = 0; st < NS; ++st) lo[st] = c * RB + 16 * ((2 * st + hh) ^ (c % C::KCN));
   // Band tile of 32 ring rows from rr (a multiple of 32): initial accumulator
   // (row rr + 8a + 4hh + e in register 4a + e) and MFMAs.
-  auto band_init = [&](int rr) {
-    const float* dr = reinterpret_cast<const float*>(smem + C::D_OFF) + (rr % C::RING) + 4 * hh;
-    floatx16 acc;
-#pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const floatx4 v = *reinterpret_cast<const floatx4*>(dr + 8 * a);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) acc[4 * a + e] = v[e];
-    }
-    return acc;
-  };
   auto band_tile = [&](int rr) {
-    floatx16 acc = band_init(rr);
+    floatx16 acc = floatx16{};
     const char* rb = smem + C::P_OFF + (rr % C::RING) * RB;
 #pragma unroll
-    for (int st = 0; st < NS; ++st) acc = mma32(*reinterpret_cast<const bf16x8*>(rb + lo[st]), qu[st], acc);
+    for (int st = 0; st < NS; ++st) acc = mma32(*reinterpret_cast<const bf16x8*>(rb + lo[st]), qv[st], acc);
     return acc;
   };
 
@@ -702,7 +683,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
     put(carry, 0);
     {
       // band tiles 1 and 2 as two interleaved MFMA chains
-      floatx16 b1 = band_init(rrw + 32), b2 = band_init(rrw + 64);
+      floatx16 b1 = floatx16{}, b2 = floatx16{};
       const char* r1 = smem + C::P_OFF + ((rrw + 32) % C::RING) * RB;
       const char* r2 = smem + C::P_OFF + ((rrw + 64) % C::RING) * RB;
       // operand reads run PF steps ahead of the MFMAs; the sched_barriers pin
@@ -716,8 +697,8 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
-        b1 = mma32(a1[st % PF], qu[st], b1);
-        b2 = mma32(a2[st % PF], qu[st], b2);
+        b1 = mma32(a1[st % PF], qv[st], b1);
+        b2 = mma32(a2[st % PF], qv[st], b2);
         if (st + PF < NS) {
           a1[st % PF] = *reinterpret_cast<const bf16x8*>(r1 + lo[st + PF]);
           a2[st % PF] = *reinterpret_cast<const bf16x8*>(r2 + lo[st + PF]);
@@ -749,7 +730,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 #pragma unroll
           for (int u = 0; u < 2; ++u)
             ka[st % PF][u] = *reinterpret_cast<const bf16x8*>(Ks + 32 * u * RB + lo[st + PF]);
-        if (st <= C::PDMA) dma_ring(st, rr0n);
+        if (st < C::PDMA) dma_ring(st, rr0n);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -877,26 +858,6 @@ hipError_t dispatch_bf16(const AttnParams& p, int nb, hipStream_t s) {
 }
 
 // One row per DK/8 lanes: each lane takes 8 d_k values, then a lane-group sum.
-template <int DK>
-__global__ __launch_bounds__(256) void pos_bias_diff_kernel(const AttnParams p, float* out, int64_t ld) {
-  constexpr int LPR = DK / 8, RPB = 256 / LPR;  // lanes per row, rows per block
-  const int h = blockIdx.y;
-  const int sub = threadIdx.x % LPR;
-  const int n = (int)blockIdx.x * RPB + (int)threadIdx.x / LPR - p.p_pad;
-  float acc = 0.f;
-  if (n >= 0 && n < p.p_rows) {
-    const bf16x8 v = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.p) + (int64_t)n * p.p_rs +
-                                                       h * DK + 8 * sub);
-    const float* bu = p.bias_u + h * DK + 8 * sub;
-    const float* bv = p.bias_v + h * DK + 8 * sub;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc = __builtin_fmaf((float)v[e], bu[e] - bv[e], acc);
-  }
-#pragma unroll
-  for (int m = LPR / 2; m > 0; m >>= 1) acc += __shfl_xor(acc, m, LPR);
-  if (sub == 0 && n < p.p_rows + p.p_pad) out[(int64_t)h * ld + n + p.p_pad] = -acc;
-}
-
 // ---------------------------------------------------------------------------
 // fp32 chunk kernel for short query blocks (the cache-aware streaming step:
 // T <= 16 queries against L <= 96 keys of the cache ring). One workgroup of
@@ -1197,8 +1158,7 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
   if (p.vt) {
     // V^T columns of each batch are read in whole 64-key tiles
     if (dt != kBF16 || p.ring_len || !aligned16(p.vt) || p.vt_ld % 8 || p.vt_bs % 64 || p.vt_bs < p.T ||
-        p.vt_ld < (int64_t)(p.b0 + nb) * p.vt_bs || p.L != p.T || !p.pdiff ||
-        p.pdiff_ld < p.p_rows + 2 * (int64_t)p.p_pad || p.kv_pad < 63 || p.p_pad < bf16_pos_pad(p, nb))
+        p.vt_ld < (int64_t)(p.b0 + nb) * p.vt_bs || p.L != p.T || p.kv_pad < 63 || p.p_pad < bf16_pos_pad(p, nb))
       return hipErrorInvalidValue;
     if (head_dim == 64) return dispatch_bf16<64>(p, nb, s);
     if (head_dim == 128) return dispatch_bf16<128>(p, nb, s);
@@ -1219,22 +1179,6 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
     if (head_dim == 128) return dispatch_nw<bf16, 128>(p, nb, s);
   }
   return hipErrorInvalidValue;
-}
-
-hipError_t pos_bias_diff(int head_dim, const AttnParams& p, float* out, int64_t ld, hipStream_t s) {
-  if (p.p_rows <= 0 || p.H <= 0) return hipSuccess;
-  if (!p.p || !p.bias_u || !p.bias_v || !out || p.p_pad < 0 || ld < p.p_rows + 2 * (int64_t)p.p_pad ||
-      !aligned16(p.p) || p.p_rs % 8 || p.p_rs < (int64_t)p.H * head_dim)
-    return hipErrorInvalidValue;
-  const int rpb = 256 / (head_dim / 8);
-  const dim3 grid((p.p_rows + 2 * p.p_pad + rpb - 1) / rpb, p.H);
-  if (head_dim == 64)
-    hipLaunchKernelGGL(pos_bias_diff_kernel<64>, grid, dim3(256), 0, s, p, out, ld);
-  else if (head_dim == 128)
-    hipLaunchKernelGGL(pos_bias_diff_kernel<128>, grid, dim3(256), 0, s, p, out, ld);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
 }
 
 hipError_t export_mask(const AttnParams& p, int nb, uint8_t* out, hipStream_t s) {

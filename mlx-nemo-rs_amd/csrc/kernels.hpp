@@ -88,10 +88,6 @@ struct AttnParams {
   // zeros or finite values past T); null selects the row-major V path.
   const void* vt = nullptr;
   int64_t vt_ld = 0, vt_bs = 0;
-  // bf16 path: -(bias_u - bias_v) . P[n] per head ([H][pdiff_ld] fp32, row n
-  // at column n + p_pad, zero on the pad rows), from pos_bias_diff
-  const float* pdiff = nullptr;
-  int64_t pdiff_ld = 0;
   // bf16 path: rows readable (finite) around the position table, p_pad
   // before row 0 and after row p_rows - 1 (at least bf16_pos_pad), and past
   // the last key row of the last item (at least 63)
@@ -105,9 +101,6 @@ struct AttnParams {
   int q_valid[kMaxBatch];
 };
 hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nbatch, hipStream_t s);
-// The bf16 kernel's position-term offset: out[h][n + p_pad] = -(bias_u[h] - bias_v[h]) . P[n, h]
-// for n in [0, p_rows), zero for the p_pad rows on each side (ld >= p_rows + 2 p_pad).
-hipError_t pos_bias_diff(int head_dim, const AttnParams& p, float* out, int64_t ld, hipStream_t s);
 // Position rows the bf16 kernel reads beyond the table on either side for
 // these items' key ranges (key_lo / key_hi / q_valid, context, T, center).
 int bf16_pos_pad(const AttnParams& p, int nbatch);

@@ -509,16 +509,15 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
       pad = std::max(pad, mhsa::bf16_pos_pad(a, nb));
     }
   pad = (int)align_up(pad, 8);
-  const int64_t pd_ld = nrows + 2 * (int64_t)pad;
-  const size_t qkv_b = align_up((M + kv_pad) * 3 * D * es, 256), p_b = align_up(pd_ld * D * es, 256),
-               ctx_b = align_up(M * D * es, 256), pd_b = use_vt ? align_up(L->H * pd_ld * 4, 256) : 0;
+  const int64_t prow_n = nrows + 2 * (int64_t)pad;
+  const size_t qkv_b = align_up((M + kv_pad) * 3 * D * es, 256), p_b = align_up(prow_n * D * es, 256),
+               ctx_b = align_up(M * D * es, 256);
   const size_t ws_before = L->ws.n;
-  HIPCHK(L->ws.ensure(qkv_b + p_b + ctx_b + pd_b));
+  HIPCHK(L->ws.ensure(qkv_b + p_b + ctx_b));
   if (L->ws.n != ws_before) HIPCHK(mhsa::fill_zero(L->ws.p, L->ws.n, s));  // slack rows start finite
   char* qkv = static_cast<char*>(L->ws.p);
   char* P = qkv + qkv_b + (size_t)pad * D * es;  // table rows [0, nrows) after `pad` slack rows
   char* cx = qkv + qkv_b + p_b;
-  float* pdiff = use_vt ? reinterpret_cast<float*>(cx + ctx_b) : nullptr;
   L->last_qkv = qkv;
   L->last_pos = P;
   // bf16: V also transposed per batch, [D][B * Tpad], for the MFMA PV operand;
@@ -563,10 +562,6 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
     a.vt = vt.p;
     a.vt_ld = vt.ld;
     a.vt_bs = vt.Tpad;
-    a.pdiff = pdiff;
-    a.pdiff_ld = pd_ld;
-    ProfScope ps(L, "pos_bias_diff", s);
-    HIPCHK(mhsa::pos_bias_diff(L->dk, a, pdiff, pd_ld, s));
   }
   {
     ProfScope ps(L, "attention", s);
