@@ -484,7 +484,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   if (W >= nqb * nb * p.H) return;
   const int tid = threadIdx.x, lane = tid & 63, hh = lane >> 5, c = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index (uniform)
-  const int bl = (W / nqb) % nb, b = p.b0 + bl, h = W / (nqb * nb);
+  const int bl = p.order[(W / nqb) % nb], b = p.b0 + bl, h = W / (nqb * nb);
   const int i0 = (W % nqb) * QB;
   const int iw = i0 + 32 * w;  // first query of this wave
   const int qi = iw + c;       // this lane's query column
@@ -843,10 +843,20 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 }
 
 template <int DK, bool DEBUG>
-hipError_t launch2(const AttnParams& p, int nb, hipStream_t s) {
+hipError_t launch2(AttnParams p, int nb, hipStream_t s) {
   using C = Cfg2<DK, 4>;
   const int64_t work = (int64_t)(p.T + C::QB - 1) / C::QB * p.H * nb;
   if (work > (1 << 30)) return hipErrorInvalidValue;
+  // items by descending work (query blocks x key tiles), ties in item order
+  int64_t cost[kMaxBatch];
+  for (int bl = 0; bl < nb; ++bl) {
+    int jbeg, jend;
+    key_range(p, bl, 0, p.T, jbeg, jend);
+    const int rows = imin(p.q_valid[bl], p.T);
+    cost[bl] = jend > jbeg && rows > 0 ? (int64_t)((rows + C::QB - 1) / C::QB) * ((jend - jbeg + C::NK - 1) / C::NK) : 0;
+    p.order[bl] = bl;
+  }
+  std::stable_sort(p.order, p.order + nb, [&](int a, int b) { return cost[a] > cost[b]; });
   const dim3 grid((unsigned)((work + 7) / 8 * 8));
   hipLaunchKernelGGL((attn_bf16_kernel<DK, 4, DEBUG>), grid, dim3(C::NT), 0, s, p, nb);
   return hipGetLastError();

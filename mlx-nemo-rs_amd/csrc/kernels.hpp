@@ -96,6 +96,10 @@ struct AttnParams {
   float scale = 0.f, scale_bd = 0.f;
   int has_ctx = 0, left = -1, right = -1, chunked = 0;
   int b0 = 0;
+  // bf16 (V^T) kernel: items in launch order, longest key range first, so
+  // that the work left for a second round of workgroups is the shortest
+  // (a permutation of [0, nbatch); filled by the launcher)
+  int order[kMaxBatch];
   int key_lo[kMaxBatch];
   int key_hi[kMaxBatch];
   int q_valid[kMaxBatch];
