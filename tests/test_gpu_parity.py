@@ -571,6 +571,29 @@ def test_streaming_projection_kinds_with_biases(d_model, n_heads, kind):
     assert np.array_equal(st.read_cache().cpu().numpy(), np.concatenate(caches, 0).astype(np.float32))
 
 
+@pytest.mark.parametrize("d_model,n_heads", [(128, 2), (256, 2)])
+@pytest.mark.parametrize("T,lengths", [(12, [12, 7, 1]), (16, [16, 16, 9]), (1, [1, 1, 1])])
+@pytest.mark.parametrize("ctx", [None, ((4, 1), "chunked_limited"), ((3, 2), "regular")])
+def test_forward_f32_short_utterances(d_model, n_heads, T, lengths, ctx):
+    """Offline fp32 utterances of at most 16 frames take the chunk kernel
+    (one workgroup per item and head, keys = the utterance); with key
+    padding, one-frame items and contexts, against the oracle within the
+    fp32 bound on the rows that see a key."""
+    rng = np.random.default_rng(91)
+    w = random_weights(rng, d_model, n_heads, scale=0.08)
+    p = oracle_params(w, d_model, n_heads)
+    B = len(lengths)
+    x = rng.standard_normal((B, T, d_model)).astype(np.float32)
+    pos = O.RelPositionalEncoding(d_model, 5000, False).get_encoding(T)
+    octx = O.AttentionContext.new(*ctx) if ctx else None
+    ref = O.mhsa_forward(p, x, pos, octx, O.key_padding_mask(lengths, T))
+    layer = gpu_layer(w, d_model, n_heads, True, O.F32)
+    got = host(layer.forward(dev(x, O.F32), dev(pos, O.F32), M.AttentionContext.new(*ctx) if ctx else None,
+                             M.key_padding_mask(lengths, T)))
+    rows = visible_rows(B, T, octx, lengths)
+    assert rel_err(got, ref, rows) < F32_TOL
+
+
 @pytest.mark.parametrize("d_model,n_heads,T", [(256, 2, 50), (1024, 8, 40)])
 def test_sublayer_f32_against_oracle(d_model, n_heads, T):
     """x + MHSA(LayerNorm(x)) (conformer.rs:1747-1780) in fp32 with LayerNorm
