@@ -999,19 +999,21 @@ __global__ __launch_bounds__(1024) void gemm_kpar_kernel(const GemmParams p) {
 #pragma unroll
       for (int u = 0; u < TR; ++u) wsb[u] = wsb_next[u];
     }
-    // element 4 (TR t + u) + e of lane l: row 16 t + 4 (l / 16) + e, column 16 u + l % 16
+    // element 256 (TR t + u) + 4 l + e of lane l: row 16 t + 4 (l / 16) + e,
+    // column 16 u + l % 16 (each 16-byte store of a wave covers 1 KB of
+    // consecutive words: no bank conflicts)
     float (&rb)[16][EPW] = red[v & 1];
 #pragma unroll
     for (int t = 0; t < TR; ++t)
 #pragma unroll
-      for (int u = 0; u < TR; ++u) *reinterpret_cast<floatx4*>(&rb[w][lane * 4 * TR * TR + 4 * (TR * t + u)]) = acc[t][u];
+      for (int u = 0; u < TR; ++u) *reinterpret_cast<floatx4*>(&rb[w][256 * (TR * t + u) + 4 * lane]) = acc[t][u];
     __syncthreads();
     // (this buffer is written again two tiles on, after the next tile's
     // barrier, which every thread reaches only after its sums here)
     for (int idx = tid; idx < EPW; idx += nt_threads) {
       float sum = 0.f;
       for (int ww = 0; ww < nw; ++ww) sum += rb[ww][idx];
-      const int l = idx / (4 * TR * TR), tu = (idx >> 2) % (TR * TR), e = idx & 3;
+      const int tu = idx >> 8, l = (idx >> 2) & 63, e = idx & 3;
       const int row = mt * TS + 16 * (tu / TR) + 4 * (l >> 4) + e, col = nt * TS + 16 * (tu % TR) + (l & 15);
       if (row >= p.M) continue;
       const float y = epilogue_value<float>(p, row, col, sum);
