@@ -335,7 +335,9 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
 
   if constexpr (KS) {
     // Merge the waves' states through LDS (each wave writes into its own
-    // tile area): query column ql, d_k rows 16 d + 4 g + r of O; wave w then
+    // tile area): query column ql, d_k rows 16 d + 4 g + r of O at word
+    // 64 (4 d + r) + lane (the lanes of one store on consecutive words: a
+    // query-major layout put all 16 query columns on one bank); wave w then
     // finishes d_k rows 16 d + ... for d = w, w + NW, ...
     static_assert(C::LDS >= (DK * 16 + 32) * 4, "merge area");
     float* mo = reinterpret_cast<float*>(tb);
@@ -347,7 +349,7 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
 #pragma unroll
     for (int d = 0; d < DK / 16; ++d)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) mo[ql * DK + 16 * d + 4 * g + r] = o[d][r];
+      for (int r = 0; r < 4; ++r) mo[64 * (4 * d + r) + lane] = o[d][r];
     __syncthreads();
     float mw[NW], m_all = -INFINITY;
 #pragma unroll
@@ -372,7 +374,7 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
           float acc = 0.f;
 #pragma unroll
           for (int v = 0; v < NW; ++v)
-            acc += f[v] * reinterpret_cast<const float*>(smem + v * C::LDS)[ql * DK + 16 * d + 4 * g + r];
+            acc += f[v] * reinterpret_cast<const float*>(smem + v * C::LDS)[64 * (4 * d + r) + lane];
           vals[r] = from_float<T>(acc * inv);
         }
         if constexpr (sizeof(T) == 2) {
