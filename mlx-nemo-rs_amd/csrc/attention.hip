@@ -206,8 +206,14 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
       if (c >= NK * CPR) break;
       *reinterpret_cast<u32x4*>(Ks + row * C::KP + cb) = kr[i];
       const int d0 = cb / (int)sizeof(T);  // V^T: transposed on the way in
+      // (fp32: key k of V^T row d sits at k ^ 4 ((d / 16) % 4), which puts the
+      // 4-byte stores of lanes 4 rows apart on distinct banks; reads of 4
+      // consecutive keys stay one 16-byte read)
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) *reinterpret_cast<T*>(Vt + (d0 + e) * C::VP + row * (int)sizeof(T)) = vr[i][e];
+      for (int e = 0; e < EPL; ++e) {
+        const int kx = sizeof(T) == 4 ? row ^ (4 * (((d0 + e) >> 4) & 3)) : row;
+        *reinterpret_cast<T*>(Vt + (d0 + e) * C::VP + kx * (int)sizeof(T)) = vr[i][e];
+      }
     }
 #pragma unroll
     for (int i = 0; i < NPC; ++i) {
@@ -326,7 +332,7 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
         const floatx4 pb = {sc[u][0], sc[u][1], sc[u][2], sc[u][3]};
 #pragma unroll
         for (int d = 0; d < DK / 16; ++d) {
-          const floatx4 a = *reinterpret_cast<const floatx4*>(Vt + (16 * d + ql) * C::VP + (16 * u + 4 * g) * 4);
+          const floatx4 a = *reinterpret_cast<const floatx4*>(Vt + (16 * d + ql) * C::VP + ((16 * u + 4 * g) ^ (4 * (d & 3))) * 4);
           o[d] = mma16(a, pb, o[d]);
         }
       }
