@@ -900,9 +900,13 @@ struct CfgS {
   static constexpr int P_OFF = LMAX * RP;                               // position rows
   static constexpr int RPI = NT / (DK / 4);                             // rows per pass of the workgroup
   static constexpr int PROWS = (PMAX + RPI - 1) / RPI * RPI;            // (RPI is a multiple of 16)
-  static constexpr int S_OFF = P_OFF + PROWS * RP;                      // scores / probabilities [NQ][LMAX]
-  static constexpr int B_OFF = S_OFF + NQ * LMAX * 4;                   // band products [NQ][PROWS]
-  static constexpr int Q_OFF = B_OFF + NQ * PROWS * 4;                 // q + pos_bias_u, then q + pos_bias_v rows
+  // score and band rows padded by 4 words: the MFMA result stores (rows
+  // 4g + e of one column) and the PV operand reads (16 rows) then fall on
+  // distinct banks
+  static constexpr int SLD = LMAX + 4, BLD = PROWS + 4;
+  static constexpr int S_OFF = P_OFF + PROWS * RP;                      // scores / probabilities [NQ][SLD]
+  static constexpr int B_OFF = S_OFF + NQ * SLD * 4;                    // band products [NQ][BLD]
+  static constexpr int Q_OFF = B_OFF + NQ * BLD * 4;                   // q + pos_bias_u, then q + pos_bias_v rows
   static constexpr int LDS = Q_OFF + 2 * NQ * RP;
   static constexpr int KCH = LMAX / RPI;                                // K / V chunks per thread
   static constexpr int PCH = PROWS / RPI;                               // position chunks per thread
@@ -1023,8 +1027,8 @@ __global__ __launch_bounds__(CfgS<DK>::NT) void attn_chunk_f32_kernel(const Attn
       for (int st = 0; st < NS; ++st) acc = mma16(qv[st], *reinterpret_cast<const floatx4*>(rows + 64 * st), acc);
     }
     // C layout: lane holds rows 4g + e of column rl
-    float* dst = is_s ? Sl + 4 * g * LMAX + tt * 16 + rl : Bl + 4 * g * C::PROWS + tt * 16 + rl;
-    const int ld = is_s ? LMAX : C::PROWS;
+    float* dst = is_s ? Sl + 4 * g * C::SLD + tt * 16 + rl : Bl + 4 * g * C::BLD + tt * 16 + rl;
+    const int ld = is_s ? C::SLD : C::BLD;
 #pragma unroll
     for (int e = 0; e < 4; ++e) dst[e * ld] = acc[e];
   }
@@ -1050,7 +1054,7 @@ __global__ __launch_bounds__(CfgS<DK>::NT) void attn_chunk_f32_kernel(const Attn
       const int jl = q + RL * k;
       x[k] = -INFINITY;
       if (jl < nk && in_interval(jbeg + jl, iv))
-        x[k] = Sl[i * LMAX + jl] * p.scale + Bl[i * C::PROWS + jl + NQ - 1 - i] * p.scale_bd;
+        x[k] = Sl[i * C::SLD + jl] * p.scale + Bl[i * C::BLD + jl + NQ - 1 - i] * p.scale_bd;
       m = fmaxf(m, x[k]);
     }
 #pragma unroll
@@ -1066,7 +1070,7 @@ __global__ __launch_bounds__(CfgS<DK>::NT) void attn_chunk_f32_kernel(const Attn
     const float inv = sum > 0.f ? 1.f / sum : 0.f;  // a row that sees no key gives 0
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int k = 0; k < LMAX / RL; ++k) Sl[i * LMAX + q + RL * k] = x[k] * inv;
+    for (int k = 0; k < LMAX / RL; ++k) Sl[i * C::SLD + q + RL * k] = x[k] * inv;
   }
   __syncthreads();
 
@@ -1076,7 +1080,7 @@ __global__ __launch_bounds__(CfgS<DK>::NT) void attn_chunk_f32_kernel(const Attn
   for (int dt = w; dt < DK / 16; dt += NW) {
     floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
     for (int kt = 0; kt < nkt; ++kt) {
-      const floatx4 a = *reinterpret_cast<const floatx4*>(Sl + rl * LMAX + kt * 16 + 4 * g);
+      const floatx4 a = *reinterpret_cast<const floatx4*>(Sl + rl * C::SLD + kt * 16 + 4 * g);
       floatx4 bv;
 #pragma unroll
       for (int e = 0; e < 4; ++e) bv[e] = Vl[(kt * 16 + 4 * g + e) * (C::RP / 4) + dt * 16 + rl];
