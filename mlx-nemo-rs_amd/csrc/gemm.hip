@@ -338,10 +338,11 @@ __host__ __device__ int64_t m_tiles(const GemmParams& p) {
 // One workgroup of 4 waves (2 x 2) computes a BM x BN tile; each wave holds a
 // (BM/2) x (BN/2) block of fp32 accumulators (up to 128 x 128, in AGPRs) fed
 // by 32x32x16 bf16 MFMAs, so every 16-byte operand fragment read from LDS
-// serves BM/64 or BN/64 MFMAs. Operands stream through two LDS stages of 64
-// k-columns (128 bytes per row): A (and dense B) with direct-to-LDS buffer
-// loads (no VGPR staging; rows past the matrix read as zero), quantized B as
-// u8 codes dequantised in registers on their way into LDS. A stage row's
+// serves BM/64 or BN/64 MFMAs. Operands stream through NS LDS stages of 64
+// k-columns with direct-to-LDS buffer loads (no VGPR staging; rows past the
+// matrix read as zero): A and dense B as 128-byte bf16 rows, quantized B as
+// 64-byte rows of u8 codes, which each wave dequantises in registers after
+// its fragment reads (below). A bf16 stage row's
 // eight 16-byte chunks are stored XOR-permuted by (row / 2) % 8, which puts
 // the 32 rows of one fragment read on all 64 banks. Within a stage the
 // fragment reads of k-step s + 1 are issued before the MFMAs of step s
