@@ -168,7 +168,7 @@ int32_t mhsa_forward(mhsa_layer* layer, const void* x, int32_t batch, int32_t se
 
 /* x <- x + forward(LayerNorm(x)) : the MHSA sublayer of ConformerBlock
  * (conformer.rs:1747-1780). ln_gamma / ln_beta [d_model] HOST fp32 arrays
- * (NULL = 1 / 0), eps as nn::LayerNorm (1e-5). */
+ * (NULL = 1 / 0), eps as nn::LayerNorm (1e-5); d_model <= 2048. */
 int32_t mhsa_sublayer_forward(mhsa_layer* layer, void* x_inout, int32_t batch, int32_t seq_len,
                               const float* ln_gamma_host, const float* ln_beta_host, float eps,
                               const void* pos_emb, int32_t pos_len, const mhsa_context* ctx,
@@ -259,6 +259,19 @@ int32_t mhsa_debug_rel_shift_index(int32_t rows, int32_t total_len, int32_t* out
 int32_t mhsa_debug_position_scores(mhsa_layer* layer, const void* x, int32_t batch, int32_t seq_len,
                                    const void* pos_emb, int32_t pos_len, float* out_dev, void* q_out_dev,
                                    void* p_out_dev, void* hip_stream);
+/* For a bf16 layer: the offline forward's attention logits
+ * s*(q_u k) + cast(s)*bd + mask (attention.rs:299-318) reduced per query row
+ * by the production kernel to the visible key with the largest logit (lowest
+ * index on ties, -1 when the row sees no key): top_dev [batch, n_heads,
+ * seq_len] int32 and logit_dev [batch, n_heads, seq_len] fp32 (device). The
+ * arguments are those of mhsa_forward; no output is written. q_out_dev and
+ * k_out_dev [batch, seq_len, d_model] and, for full attention, p_out_dev
+ * [pos_len, d_model] (bf16, device, each may be NULL) receive the projected
+ * queries, keys and position rows the kernel consumed. */
+int32_t mhsa_debug_top_keys(mhsa_layer* layer, const void* x, int32_t batch, int32_t seq_len, const void* pos_emb,
+                            int32_t pos_len, const mhsa_context* ctx, const int32_t* key_lengths_host,
+                            int32_t* top_dev, float* logit_dev, void* q_out_dev, void* k_out_dev, void* p_out_dev,
+                            void* hip_stream);
 
 #ifdef __cplusplus
 }

@@ -274,7 +274,7 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
         const int jl = 16 * u + 4 * g + r;
         const int j = j0 + jl;
         const float bdv = Rm[ql * C::RMP + jl + 15 - ql];
-        if (DEBUG && qi < p.T && j < p.L)
+        if (DEBUG && p.dbg_bd && qi < p.T && j < p.L)
           p.dbg_bd[(((int64_t)b * p.H + h) * p.T + qi) * p.L + j] = p.scale_bd * bdv;
         const float v = s[u][r] * sc_qk + bdv * sc_bd;
         sc[u][r] = full || in_interval(j, iv) ? v : -INFINITY;
@@ -439,9 +439,11 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
 //    attention.rs:501-508): q_u for the scores, q_v for the band.
 //  * bd is rounded to bf16 in the remap strip, as the reference stores
 //    matrix_bd in bf16 (attention.rs:530). The logits are
-//    s * (q_u k + bd): the reference scales bd by cast(s) (attention.rs:
-//    308-311), which differs from s by 1.1e-4 relative at d_k = 128, far
-//    below the bf16 resolution of bd itself.
+//    s * (q_u k) + bf16(bd * bf16(s)): the reference hands the position term
+//    to the attention as the bf16 array matrix_bd * cast(s) (attention.rs:
+//    308-311), one more bf16 rounding after the product. At the quantized
+//    stack's logits (~1e3) that rounding moves a logit by several units, so
+//    it is reproduced, not folded into one fp32 scale.
 // ---------------------------------------------------------------------------
 template <int DK, int NW>
 struct Cfg2 {
@@ -533,8 +535,13 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   int jbeg, jend;
   key_range(p, bl, i0, min(i0 + QB, p.T), jbeg, jend);
   const int2 iv = query_interval(p, bl, qi);
-  const float sc = p.scale * kLog2e;
-  const float lim = 100.f / sc;  // largest (score - reference) kept without rescaling: 2^100
+  // logits are formed already scaled (s q_u k + bf16(bd cast(s))), so the
+  // exponent base change is the only factor left
+  const float sc = kLog2e;
+  const float lim = 100.f / sc;  // largest (logit - reference) kept without rescaling: 2^100
+  // DEBUG: this lane's best visible key so far (lowest index on ties)
+  float top_v = -INFINITY;
+  int top_j = -1;
   const int jfirst = (jbeg / NK) * NK;
   // ring row rr holds position row R0 + rr
   const int R0 = p.center - p.qoff - (i0 + 31) + jfirst - 96;
@@ -757,12 +764,14 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
         const bf16x8 q8 = *reinterpret_cast<const bf16x8_a2*>(rq + 32 * u + 16 * g);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float bdv = (float)q8[e];
-          if (DEBUG) {
+          // the position term as the reference materialises it:
+          // bf16(bf16(bd) * bf16(s)) (attention.rs:308-311)
+          const float tb = (float)(bf16)((float)q8[e] * p.scale_bd);
+          if (DEBUG && p.dbg_bd) {
             const int j = j0 + 32 * u + 16 * g + 8 * hh + e;
-            if (qi < p.T && j < p.L) p.dbg_bd[(((int64_t)b * p.H + h) * p.T + qi) * p.L + j] = p.scale_bd * bdv;
+            if (qi < p.T && j < p.L) p.dbg_bd[(((int64_t)b * p.H + h) * p.T + qi) * p.L + j] = tb;
           }
-          s[u][8 * g + e] += bdv;
+          s[u][8 * g + e] = __builtin_fmaf(s[u][8 * g + e], p.scale, tb);
         }
       }
     __builtin_amdgcn_wave_barrier();
@@ -778,6 +787,17 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           if ((unsigned)(jb + 32 * u + 16 * (r >> 3) + (r & 7)) >= span) s[u][r] = -INFINITY;
+    }
+    if (DEBUG && p.dbg_top) {
+      // keys in increasing order within the lane; strict > keeps the lowest
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (s[u][r] > top_v) {
+            top_v = s[u][r];
+            top_j = j0 + 32 * u + 16 * (r >> 3) + 8 * hh + (r & 7);
+          }
     }
 #pragma unroll
     for (int u = 0; u < 2; ++u)
@@ -836,6 +856,20 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 
   const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (DEBUG && p.dbg_top) {
+    // merge with the lane holding the other 8-key halves of this query
+    const float ov = __shfl_xor(top_v, 32, 64);
+    const int oj = __shfl_xor(top_j, 32, 64);
+    if (ov > top_v || (ov == top_v && oj >= 0 && (top_j < 0 || oj < top_j))) {
+      top_v = ov;
+      top_j = oj;
+    }
+    if (hh == 0 && qi < p.T) {
+      const int64_t r = ((int64_t)b * p.H + h) * p.T + qi;
+      p.dbg_top[r] = top_j;
+      p.dbg_topv[r] = top_v;
+    }
+  }
   if (qi < p.T) {
     bf16* orow = reinterpret_cast<bf16*>(p.o) + (int64_t)b * p.o_bs + (int64_t)qi * p.o_rs + h * DK;
 #pragma unroll
@@ -872,7 +906,7 @@ hipError_t launch2(AttnParams p, int nb, hipStream_t s) {
 
 template <int DK>
 hipError_t dispatch_bf16(const AttnParams& p, int nb, hipStream_t s) {
-  return p.dbg_bd ? launch2<DK, true>(p, nb, s) : launch2<DK, false>(p, nb, s);
+  return (p.dbg_bd || p.dbg_top) ? launch2<DK, true>(p, nb, s) : launch2<DK, false>(p, nb, s);
 }
 
 // One row per DK/8 lanes: each lane takes 8 d_k values, then a lane-group sum.
@@ -1115,11 +1149,15 @@ hipError_t dispatch_nw(const AttnParams& p, int nb, hipStream_t s) {
   const bool dbg = p.dbg_bd != nullptr;
   // fp32 inputs too short to give the CUs a workgroup each (one utterance of
   // 125 frames: 16 workgroups of 64 queries) split their keys over the waves
+  // Short query blocks (the streaming chunk against more keys than the chunk
+  // kernel stages) take the key-split form too: a one-wave form of this
+  // kernel (16 queries, no split) gave wrong outputs whenever its per-key
+  // mask ran, while the key-split form of the same source is exact on those
+  // shapes, so there is no one-wave form.
   if constexpr (sizeof(T) == 4) {
-    if (!dbg && p.T > 16 && (int64_t)nb * p.H * ((p.T + 63) / 64) < 128)
+    if (!dbg && (p.T <= 16 || (int64_t)nb * p.H * ((p.T + 63) / 64) < 128))
       return launch_ks<T, DK, DK == 64 ? 4 : 2>(p, nb, s);  // (per-wave tiles: 34 / 64 KB of LDS)
   }
-  if (p.T <= 16) return dbg ? launch<T, DK, 1, true>(p, nb, s) : launch<T, DK, 1, false>(p, nb, s);
   return dbg ? launch<T, DK, 4, true>(p, nb, s) : launch<T, DK, 4, false>(p, nb, s);
 }
 
@@ -1177,6 +1215,16 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
       p.o_bs % epv)
     return hipErrorInvalidValue;
   if (p.ring_len < 0 || (p.ring_len && p.ring_head < 0)) return hipErrorInvalidValue;
+  // The bf16 and chunk kernels address one item's K/V rows, the V^T block
+  // of one head and the position table through buffer descriptors with
+  // 32-bit byte ranges and offsets: keep every such range below 2^31 bytes.
+  {
+    const int64_t es = dtype_size(dt), lim = (int64_t)1 << 31;
+    const int64_t krows = (p.ring_len ? p.ring_len : p.L) + (int64_t)p.kv_pad;
+    if (krows * p.kv_rs * es >= lim || (int64_t)(p.p_rows + 2 * (int64_t)p.p_pad) * p.p_rs * es >= lim ||
+        (int64_t)p.T * p.q_rs * es >= lim || (p.vt && (int64_t)head_dim * p.vt_ld * es >= lim))
+      return hipErrorInvalidValue;
+  }
   if (p.vt) {
     // V^T columns of each batch are read in whole 64-key tiles
     if (dt != kBF16 || p.ring_len || !aligned16(p.vt) || p.vt_ld % 8 || p.vt_bs % 64 || p.vt_bs < p.T ||

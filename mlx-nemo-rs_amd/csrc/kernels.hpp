@@ -84,6 +84,10 @@ struct AttnParams {
   void* o = nullptr;
   int64_t o_bs = 0, o_rs = 0;
   float* dbg_bd = nullptr;  // debug: scaled position scores [B, H, T, L]
+  // debug (bf16 kernel): per query row [B, H, T], the visible key with the
+  // largest logit (lowest index on ties; -1 when none is visible) and that logit
+  int* dbg_top = nullptr;
+  float* dbg_topv = nullptr;
   // bf16 path: V^T [H*dk][B*Tpad] (key j of batch b at column b*vt_bs + j,
   // zeros or finite values past T); null selects the row-major V path.
   const void* vt = nullptr;
@@ -116,6 +120,8 @@ hipError_t export_mask(const AttnParams& p, int nbatch, uint8_t* out, hipStream_
 hipError_t export_pos_index(int T, int L, int qoff, int center, int32_t* out, hipStream_t s);
 
 // y = T(LayerNorm(x) * gamma + beta), statistics in fp32; gamma/beta may be null.
+// Rows are held in registers, one wave per row: D <= kMaxLayerNormDim.
+constexpr int kMaxLayerNormDim = 2048;
 hipError_t layer_norm(DType dt, const void* x, void* y, const float* gamma, const float* beta,
                       float eps, int rows, int D, hipStream_t s);
 

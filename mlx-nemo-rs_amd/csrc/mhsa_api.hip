@@ -186,6 +186,9 @@ struct mhsa_layer {
   HostLinear lin[5];
   std::vector<float> pbu, pbv;
   bool dirty = true;
+  // bumped by every upload of the parameters: streams compare it with the
+  // version their cached K/V were projected with
+  uint64_t version = 0;
   // device parameters
   DevBuf wbuf;
   DevLinear dev[5];
@@ -227,6 +230,7 @@ struct mhsa_stream {
   mhsa_layer* layer = nullptr;
   int B = 0, C = 0, Tc = 0, R = 0;
   int head = 0;
+  uint64_t kv_version = 0;  // layer version ring_kv was projected with (0 = never)
   std::vector<int32_t> fill;
   DevBuf ring_h;   // [B, R, D] fp32
   DevBuf ring_kv;  // [B, R, 2D] fp32 (K columns then V columns)
@@ -295,6 +299,9 @@ int32_t prepare(mhsa_layer* L) {
     pb[e] = rnd(L->pbu[e]);
     pb[D + e] = rnd(L->pbv[e]);
   }
+  // kernels of an earlier call (on any stream) may still read the old
+  // parameters: let them finish before the buffer is reused or replaced
+  if (L->wbuf.p) HIPCHK(hipDeviceSynchronize());
   HIPCHK(L->wbuf.ensure(host.size()));
   HIPCHK(hipMemcpy(L->wbuf.p, host.data(), host.size(), hipMemcpyHostToDevice));
   char* base = static_cast<char*>(L->wbuf.p);
@@ -312,6 +319,7 @@ int32_t prepare(mhsa_layer* L) {
   L->d_pbv = L->d_pbu + D;
   L->dirty = false;
   L->pmemo_len = -1;
+  ++L->version;
   return MHSA_OK;
 }
 
@@ -467,11 +475,19 @@ int32_t check_layer(const mhsa_layer* L) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // Offline forward shared by mhsa_forward, the sublayer and the debug export.
+// Debug outputs of the attention kernel (all null in the product path).
+struct AttnDebug {
+  float* bd = nullptr;     // scaled position scores [B, H, T, T]
+  int* top = nullptr;      // bf16 kernel: top visible key per query row [B, H, T]
+  float* topv = nullptr;   // and its logit
+  bool any() const { return bd || top; }
+};
+
 int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos_emb, int pos_len,
-                     const mhsa_context* ctx, const int32_t* lens, void* out, const void* residual, float* dbg_bd,
-                     hipStream_t s) {
+                     const mhsa_context* ctx, const int32_t* lens, void* out, const void* residual,
+                     const AttnDebug& dbg, hipStream_t s) {
   if (B <= 0 || T <= 0) return fail(MHSA_EINVAL, "batch and seq_len must be positive (got %d, %d)", B, T);
-  if (!x || !pos_emb || (!out && !dbg_bd)) return fail(MHSA_EINVAL, "null tensor pointer");
+  if (!x || !pos_emb || (!out && !dbg.any())) return fail(MHSA_EINVAL, "null tensor pointer");
   if (!aligned16(x) || !aligned16(pos_emb) || (out && !aligned16(out)))
     return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
   int32_t rc = prepare(L);
@@ -557,7 +573,9 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   a.o = cx;
   a.o_bs = (int64_t)T * D;
   a.o_rs = D;
-  a.dbg_bd = dbg_bd;
+  a.dbg_bd = dbg.bd;
+  a.dbg_top = dbg.top;
+  a.dbg_topv = dbg.topv;
   if (use_vt) {
     a.vt = vt.p;
     a.vt_ld = vt.ld;
@@ -571,6 +589,26 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   if (!out) return MHSA_OK;
   ProfScope ps(L, "gemm_out", s);
   return run_gemm(L, L->dev[3], D, cx, D, (int)M, out, D, residual, D, s);
+}
+
+// K and V of every ring row from the cached inputs h (the reference
+// re-projects [cache; x] on every step, attention.rs:721-722): run when the
+// stream's projections are older than the layer's parameters, i.e. on the
+// first step of a new stream (h = 0 gives K = b_k, V = b_v) and after any
+// weight or dtype change.
+int32_t reproject_ring(mhsa_layer* L, mhsa_stream* S, hipStream_t s) {
+  const int D = L->D, M = S->B * S->R;
+  char* kv = static_cast<char*>(S->ring_kv.p);
+  int32_t rc;
+  if (L->qkv_fused) {
+    rc = run_gemm(L, L->dev[1], 2 * D, S->ring_h.p, D, M, kv, 2 * D, nullptr, 0, s);
+  } else {
+    rc = run_gemm(L, L->dev[1], D, S->ring_h.p, D, M, kv, 2 * D, nullptr, 0, s);
+    if (!rc) rc = run_gemm(L, L->dev[2], D, S->ring_h.p, D, M, kv + (size_t)D * 4, 2 * D, nullptr, 0, s);
+  }
+  if (rc) return rc;
+  S->kv_version = L->version;
+  return MHSA_OK;
 }
 
 }  // namespace
@@ -761,7 +799,7 @@ int32_t mhsa_forward(mhsa_layer* L, const void* x, int32_t batch, int32_t seq_le
                      int32_t pos_len, const mhsa_context* ctx, const int32_t* lens, void* out, void* hs) {
   if (int32_t rc = check_layer(L)) return rc;
   if (!out) return fail(MHSA_EINVAL, "null output pointer");
-  return forward_impl(L, x, batch, seq_len, pos_emb, pos_len, ctx, lens, out, nullptr, nullptr,
+  return forward_impl(L, x, batch, seq_len, pos_emb, pos_len, ctx, lens, out, nullptr, AttnDebug(),
                       static_cast<hipStream_t>(hs));
 }
 
@@ -771,6 +809,8 @@ int32_t mhsa_sublayer_forward(mhsa_layer* L, void* x, int32_t batch, int32_t seq
   if (int32_t rc = check_layer(L)) return rc;
   if (!x || batch <= 0 || seq_len <= 0) return fail(MHSA_EINVAL, "bad sublayer arguments");
   if (!aligned16(x)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  if (L->D > mhsa::kMaxLayerNormDim)
+    return fail(MHSA_ENOTSUP, "the sublayer's LayerNorm supports d_model <= %d (got %d)", mhsa::kMaxLayerNormDim, L->D);
   hipStream_t s = static_cast<hipStream_t>(hs);
   const int D = L->D;
   const int64_t M = (int64_t)batch * seq_len;
@@ -787,6 +827,7 @@ int32_t mhsa_sublayer_forward(mhsa_layer* L, void* x, int32_t batch, int32_t seq
       tmp[D + i] = bf ? round_bf16(bv) : bv;
     }
     if (tmp != L->ln_host) {
+      if (L->ln_dev.p) HIPCHK(hipDeviceSynchronize());  // earlier LayerNorm launches may still read them
       HIPCHK(L->ln_dev.ensure(tmp.size() * 4));
       HIPCHK(hipMemcpy(L->ln_dev.p, tmp.data(), tmp.size() * 4, hipMemcpyHostToDevice));
       L->ln_host = tmp;
@@ -799,7 +840,7 @@ int32_t mhsa_sublayer_forward(mhsa_layer* L, void* x, int32_t batch, int32_t seq
     ProfScope ps(L, "layer_norm", s);
     HIPCHK(mhsa::layer_norm(dtype_of(L), x, L->hbuf.p, gd, bd, eps, (int)M, D, s));
   }
-  return forward_impl(L, L->hbuf.p, batch, seq_len, pos_emb, pos_len, ctx, lens, x, x, nullptr, s);
+  return forward_impl(L, L->hbuf.p, batch, seq_len, pos_emb, pos_len, ctx, lens, x, x, AttnDebug(), s);
 }
 
 int32_t mhsa_stream_create(mhsa_layer* L, int32_t batch, int32_t cache_size, int32_t chunk_len, mhsa_stream** out) {
@@ -849,14 +890,8 @@ int32_t mhsa_stream_load_cache(mhsa_stream* S, const void* cache, const int32_t*
   const int D = L->D;
   S->head = 0;
   for (int b = 0; b < S->B; ++b) S->fill[b] = filled ? std::min(std::max(filled[b], 0), S->C) : 0;
-  if (S->C == 0) return MHSA_OK;
-  HIPCHK(mhsa::ring_write(mhsa::kF32, cache, S->ring_h.p, S->B, S->C, D, S->R, D, 0, s));
-  const int M = S->B * S->C;
-  char* kv = static_cast<char*>(S->ring_kv.p);
-  if (L->qkv_fused)
-    return run_gemm(L, L->dev[1], 2 * D, cache, D, M, kv, 2 * D, nullptr, 0, s, S->C, S->R, 0, S->R);
-  if ((rc = run_gemm(L, L->dev[1], D, cache, D, M, kv, 2 * D, nullptr, 0, s, S->C, S->R, 0, S->R))) return rc;
-  return run_gemm(L, L->dev[2], D, cache, D, M, kv + (size_t)D * 4, 2 * D, nullptr, 0, s, S->C, S->R, 0, S->R);
+  if (S->C > 0) HIPCHK(mhsa::ring_write(mhsa::kF32, cache, S->ring_h.p, S->B, S->C, D, S->R, D, 0, s));
+  return reproject_ring(L, S, s);
 }
 
 int32_t mhsa_stream_read_cache(const mhsa_stream* S, void* out, void* hs) {
@@ -892,6 +927,7 @@ int32_t mhsa_forward_with_cache(mhsa_layer* L, mhsa_stream* S, const void* x, co
     if ((rc = run_gemm(L, L->dev[4], D, pos_emb, D, pos_len, L->pmemo.p, D, nullptr, 0, s))) return rc;
     L->pmemo_len = pos_len;
   }
+  if (S->kv_version != L->version && (rc = reproject_ring(L, S, s))) return rc;
   const int64_t M = (int64_t)B * T;
   const size_t qb = align_up(M * D * 4, 256);
   HIPCHK(S->ws.ensure(2 * qb));
@@ -1122,7 +1158,9 @@ int32_t mhsa_debug_position_scores(mhsa_layer* L, const void* x, int32_t B, int3
   if (int32_t rc = check_layer(L)) return rc;
   if (!out) return fail(MHSA_EINVAL, "null output pointer");
   hipStream_t s = static_cast<hipStream_t>(hs);
-  int32_t rc = forward_impl(L, x, B, T, pos_emb, pos_len, nullptr, nullptr, nullptr, nullptr, out, s);
+  AttnDebug dbg;
+  dbg.bd = out;
+  int32_t rc = forward_impl(L, x, B, T, pos_emb, pos_len, nullptr, nullptr, nullptr, nullptr, dbg, s);
   if (rc) return rc;
   // the workspace still holds [q | k | v] rows and, after them, the projected
   // position table (all pos_len rows: full attention projects every row)
@@ -1133,6 +1171,32 @@ int32_t mhsa_debug_position_scores(mhsa_layer* L, const void* x, int32_t B, int3
                             (size_t)M, hipMemcpyDeviceToDevice, s));
   if (p_out)
     HIPCHK(hipMemcpyAsync(p_out, L->last_pos, (size_t)pos_len * L->D * es, hipMemcpyDeviceToDevice, s));
+  HIPCHK(hipStreamSynchronize(s));
+  return MHSA_OK;
+}
+
+int32_t mhsa_debug_top_keys(mhsa_layer* L, const void* x, int32_t B, int32_t T, const void* pos_emb, int32_t pos_len,
+                            const mhsa_context* ctx, const int32_t* lens, int32_t* top_dev, float* logit_dev,
+                            void* q_out, void* k_out, void* p_out, void* hs) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (!top_dev || !logit_dev) return fail(MHSA_EINVAL, "null output pointer");
+  if (L->dt != mhsa::kBF16) return fail(MHSA_ENOTSUP, "top-key export is a bf16-kernel debug output");
+  if (p_out && ctx && (ctx->left >= 0 || ctx->right >= 0))
+    return fail(MHSA_EINVAL, "position rows are exported for full attention only");
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  AttnDebug dbg;
+  dbg.top = top_dev;
+  dbg.topv = logit_dev;
+  int32_t rc = forward_impl(L, x, B, T, pos_emb, pos_len, ctx, lens, nullptr, nullptr, dbg, s);
+  if (rc) return rc;
+  // the workspace holds [q | k | v] rows (bf16: v went to the transposed
+  // buffer) and the projected position rows the kernel read
+  const size_t es = esz(L), row = (size_t)L->D * es;
+  const int64_t M = (int64_t)B * T;
+  if (q_out) HIPCHK(hipMemcpy2DAsync(q_out, row, L->last_qkv, 3 * row, row, (size_t)M, hipMemcpyDeviceToDevice, s));
+  if (k_out)
+    HIPCHK(hipMemcpy2DAsync(k_out, row, L->last_qkv + row, 3 * row, row, (size_t)M, hipMemcpyDeviceToDevice, s));
+  if (p_out) HIPCHK(hipMemcpyAsync(p_out, L->last_pos, (size_t)pos_len * row, hipMemcpyDeviceToDevice, s));
   HIPCHK(hipStreamSynchronize(s));
   return MHSA_OK;
 }

@@ -130,8 +130,10 @@ hipError_t ln_launch(const void* x, void* y, const float* g, const float* b, flo
   }
   if (D <= 512)
     hipLaunchKernelGGL((ln_kernel<T, 8>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
-  else
+  else if (D <= 1024)
     hipLaunchKernelGGL((ln_kernel<T, 16>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
+  else
+    hipLaunchKernelGGL((ln_kernel<T, 32>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
   return hipGetLastError();
 }
 
@@ -192,7 +194,7 @@ hipError_t fill_zero(void* ptr, size_t bytes, hipStream_t s) {
 hipError_t layer_norm(DType dt, const void* x, void* y, const float* gamma, const float* beta, float eps, int rows,
                       int D, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
-  if (!x || !y || D <= 0 || D > 1024) return hipErrorInvalidValue;
+  if (!x || !y || D <= 0 || D > kMaxLayerNormDim) return hipErrorInvalidValue;
   return dt == kF32 ? ln_launch<float>(x, y, gamma, beta, eps, rows, D, s)
                     : ln_launch<bf16>(x, y, gamma, beta, eps, rows, D, s);
 }

@@ -36,7 +36,7 @@ EXPORTS = (
     "mhsa_sublayer_forward", "mhsa_stream_create", "mhsa_stream_destroy", "mhsa_stream_load_cache",
     "mhsa_stream_read_cache", "mhsa_stream_fill", "mhsa_forward_with_cache", "mhsa_pos_encoding",
     "mhsa_debug_dequantize", "mhsa_debug_linear", "mhsa_debug_offline_mask", "mhsa_debug_stream_mask", "mhsa_debug_rel_shift_index",
-    "mhsa_debug_position_scores", "mhsa_profile_enable", "mhsa_profile_reset", "mhsa_profile_count",
+    "mhsa_debug_position_scores", "mhsa_debug_top_keys", "mhsa_profile_enable", "mhsa_profile_reset", "mhsa_profile_count",
     "mhsa_profile_entry",
 )
 
@@ -108,6 +108,7 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_debug_stream_mask": (I, [I, I, I, P(StreamMask), VP, VP]),
         "mhsa_debug_rel_shift_index": (I, [I, I, VP, VP]),
         "mhsa_debug_position_scores": (I, [VP, VP, I, I, VP, I, VP, VP, VP, VP]),
+        "mhsa_debug_top_keys": (I, [VP, VP, I, I, VP, I, P(Context), PI, VP, VP, VP, VP, VP, VP]),
         "mhsa_profile_enable": (I, [VP, I]),
         "mhsa_profile_reset": (I, [VP]),
         "mhsa_profile_count": (I, [VP]),
@@ -450,6 +451,29 @@ class RelPositionMultiHeadAttention:
                                                     _dptr(q) if q is not None else None,
                                                     _dptr(p) if p is not None else None, _stream_ptr()))
         return (out, q, p) if with_inputs else out
+
+    def debug_top_keys(self, x, pos_emb, context: Optional[AttentionContext] = None,
+                       key_mask: Optional[Sequence[int]] = None, with_inputs: bool = False):
+        """bf16 layers: per query row, the visible key with the largest
+        attention logit as the production kernel forms it, and that logit:
+        ([B, H, T] int32, [B, H, T] float32); -1 where a row sees no key.
+        With `with_inputs` (full attention), also the projected q, k [B, T, D]
+        and position rows [P, D] the kernel consumed."""
+        import torch
+        b, t, d = x.shape
+        pe = pos_emb.reshape(-1, d)
+        self._check_dev(x, pe)
+        top = torch.empty((b, self.n_heads(), t), dtype=torch.int32, device=x.device)
+        val = torch.empty((b, self.n_heads(), t), dtype=torch.float32, device=x.device)
+        q = torch.empty_like(x) if with_inputs else None
+        k = torch.empty_like(x) if with_inputs else None
+        p = torch.empty_like(pe) if with_inputs else None
+        ctx = context.c() if context is not None else None
+        opt = lambda a: _dptr(a) if a is not None else None
+        _check(self._lib.mhsa_debug_top_keys(self._h, _dptr(x), b, t, _dptr(pe), pe.shape[0],
+                                             ctypes.byref(ctx) if ctx is not None else None, _int_array(key_mask),
+                                             _dptr(top), _dptr(val), opt(q), opt(k), opt(p), _stream_ptr()))
+        return (top, val, q, k, p) if with_inputs else (top, val)
 
     def _check_dev(self, *ts):
         want = self.dtype

@@ -291,18 +291,31 @@ def _softmax(scores: np.ndarray) -> np.ndarray:
     return e / np.sum(e, axis=-1, keepdims=True)
 
 
+def position_term(matrix_bd, additive_mask, head_dim: int, dtype: str):
+    """The additive mask `attend` hands to the attention: bd * cast(s), stored
+    in the bd dtype, plus the context/padding mask, stored again
+    (attention.rs:307-314)."""
+    scale = f32_scale(head_dim)
+    mask = _rnd(matrix_bd * to_dtype(scale, dtype), dtype)
+    if additive_mask is not None:
+        mask = _rnd(mask + additive_mask, dtype)
+    return mask
+
+
+def attend_logits(q_u, k, matrix_bd, additive_mask, head_dim: int, dtype: str):
+    """The logits softmax sees inside `attend`: s * q_u k^T + position_term
+    (attention.rs:299-318; SDPA scales the content term by the f32 scale)."""
+    scale = f32_scale(head_dim)
+    return scale * np.matmul(q_u, np.swapaxes(k, -1, -2)) + position_term(matrix_bd, additive_mask, head_dim, dtype)
+
+
 def attend(q_u, k, v, matrix_bd, additive_mask, head_dim: int, dtype: str):
     """softmax(s * q_u k^T + bd * cast(s) + mask) v (attention.rs:299-318).
 
     `fast::scaled_dot_product_attention` is evaluated in float64 (MLX
     internal precision unpinned); its output is stored in `dtype`.
     """
-    scale = f32_scale(head_dim)
-    mask = _rnd(matrix_bd * to_dtype(scale, dtype), dtype)
-    if additive_mask is not None:
-        mask = _rnd(mask + additive_mask, dtype)
-    scores = scale * np.matmul(q_u, np.swapaxes(k, -1, -2)) + mask
-    probs = _softmax(scores)
+    probs = _softmax(attend_logits(q_u, k, matrix_bd, additive_mask, head_dim, dtype))
     return _rnd(np.matmul(probs, v), dtype)
 
 
@@ -340,6 +353,48 @@ def _merge_heads(t: np.ndarray) -> np.ndarray:
     return t.transpose(0, 2, 1, 3).reshape(b, n, h * dk)
 
 
+def project(p: MhsaParams, x: np.ndarray, pos_emb: np.ndarray, dtype: str = F32):
+    """The offline forward's projections (attention.rs:478-499), heads split:
+    q, k, v [B,H,T,dk] and the projected position rows pp [1,H,P,dk]."""
+    x = np.asarray(x, dtype=np.float64)
+    pos_emb = np.asarray(pos_emb, dtype=np.float64)
+    h = p.n_heads
+    q = _split_heads(p.linear_q.forward(x, dtype), h)  # 478-490
+    k = _split_heads(p.linear_k.forward(x, dtype), h)
+    v = _split_heads(p.linear_v.forward(x, dtype), h)
+    pp = _split_heads(p.linear_pos.forward(pos_emb, dtype), h)  # 493-499: [1,H,P,dk]
+    return q, k, v, pp
+
+
+def biased_queries(p: MhsaParams, q: np.ndarray, dtype: str):
+    """q_u = q + pos_bias_u, q_v = q + pos_bias_v in the activation dtype (attention.rs:501-508)."""
+    h, dk = p.n_heads, p.head_dim
+    bu = to_dtype(p.pos_bias_u, dtype).reshape(1, h, 1, dk)
+    bv = to_dtype(p.pos_bias_v, dtype).reshape(1, h, 1, dk)
+    return _rnd(q + bu, dtype), _rnd(q + bv, dtype)
+
+
+def _offline_mask(context, key_mask, start: int, end: int, seq_len: int):
+    """Context mask of query rows [start, end) plus the key padding mask (attention.rs:533-543)."""
+    cmask = context.block_mask(start, end, seq_len) if context is not None else None
+    if cmask is not None and key_mask is not None:
+        return cmask + key_mask
+    return cmask if cmask is not None else key_mask
+
+
+def attention_logits(p: MhsaParams, q: np.ndarray, k: np.ndarray, pp: np.ndarray,
+                     context: Optional[AttentionContext] = None,
+                     key_mask: Optional[np.ndarray] = None, dtype: str = F32) -> np.ndarray:
+    """Logits [B,H,T,T] the offline forward's softmax sees, from projected
+    q, k [B,H,T,dk] and position rows pp [1,H,2T-1,dk]: the whole query range
+    as one block (blocking does not change any element, attention.rs:1066-1104)."""
+    seq_len = q.shape[2]
+    q_u, q_v = biased_queries(p, q, dtype)
+    bd = _rnd(np.matmul(q_v, np.swapaxes(pp, -1, -2)), dtype)  # 530
+    bd = rel_shift(bd)[..., :seq_len]
+    return attend_logits(q_u, k, bd, _offline_mask(context, key_mask, 0, seq_len, seq_len), p.head_dim, dtype)
+
+
 def mhsa_forward(p: MhsaParams, x: np.ndarray, pos_emb: np.ndarray,
                  context: Optional[AttentionContext] = None,
                  key_mask: Optional[np.ndarray] = None, dtype: str = F32,
@@ -348,19 +403,10 @@ def mhsa_forward(p: MhsaParams, x: np.ndarray, pos_emb: np.ndarray,
 
     x [B,T,D] and pos_emb [1,2T-1,D] hold values already in `dtype`.
     """
-    x = np.asarray(x, dtype=np.float64)
-    pos_emb = np.asarray(pos_emb, dtype=np.float64)
-    bsz, seq_len, _ = x.shape
+    bsz, seq_len, _ = np.shape(x)
     h, dk = p.n_heads, p.head_dim
-    q = _split_heads(p.linear_q.forward(x, dtype), h)  # 478-490
-    k = _split_heads(p.linear_k.forward(x, dtype), h)
-    v = _split_heads(p.linear_v.forward(x, dtype), h)
-    pp = p.linear_pos.forward(pos_emb, dtype)  # 493-499
-    pp = _split_heads(pp, h)  # [1,H,P,dk]
-    bu = to_dtype(p.pos_bias_u, dtype).reshape(1, h, 1, dk)  # 503-508
-    bv = to_dtype(p.pos_bias_v, dtype).reshape(1, h, 1, dk)
-    q_u = _rnd(q + bu, dtype)
-    q_v = _rnd(q + bv, dtype)
+    q, k, v, pp = project(p, x, pos_emb, dtype)
+    q_u, q_v = biased_queries(p, q, dtype)
     p_t = np.swapaxes(pp, -1, -2)  # 510
     block = query_block_size(bsz * h, seq_len, max_score_elements)  # 517
     outs = []
@@ -371,12 +417,7 @@ def mhsa_forward(p: MhsaParams, x: np.ndarray, pos_emb: np.ndarray,
         p_slice = p_t[..., (seq_len - end):(2 * seq_len - 1 - start)]  # 529
         bd = _rnd(np.matmul(qv_b, p_slice), dtype)  # 530
         bd = rel_shift(bd)[..., :seq_len]  # 531-532
-        cmask = context.block_mask(start, end, seq_len) if context is not None else None
-        kmask = key_mask
-        if cmask is not None and kmask is not None:  # 536-543
-            mask = cmask + kmask
-        else:
-            mask = cmask if cmask is not None else kmask
+        mask = _offline_mask(context, key_mask, start, end, seq_len)  # 533-543
         outs.append(attend(qu_b, k, v, bd, mask, dk, dtype))  # 544
     ctx = np.concatenate(outs, axis=2) if len(outs) > 1 else outs[0]
     return p.linear_out.forward(_merge_heads(ctx), dtype)  # 558-565

@@ -32,6 +32,18 @@ def rel_err(got, ref, mask=None) -> float:
     return float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30))
 
 
+def row_rel_err(got, ref, mask=None) -> float:
+    """max over rows (last axis) of max |got - ref| / max |ref| within the row:
+    the relative error of each output row, read separately."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    if mask is not None:
+        got, ref = got[mask], ref[mask]
+    d = np.max(np.abs(got - ref), axis=-1)
+    r = np.max(np.abs(ref), axis=-1)
+    return float(np.max(d / np.maximum(r, 1e-30)))
+
+
 def abs_err(got, ref, mask=None) -> float:
     got = np.asarray(got, dtype=np.float64)
     ref = np.asarray(ref, dtype=np.float64)

@@ -1,7 +1,8 @@
 """GPU parity of the HIP rel-pos MHSA path against the CPU oracle.
 
 Tolerances (stated by the path's contract):
-* fp32: max |gpu - oracle| / max |oracle| <= 1e-4 ("max relative error"),
+* fp32: per output row, max |gpu - oracle| / max |oracle| <= 1e-4 ("max
+  relative error", read row by row),
 * bf16: max |gpu - oracle| <= 2e-2 (absolute),
 * dequantised int8 weights, masks and rel_shift index maps: bit-exact.
 
@@ -17,7 +18,7 @@ import torch
 import relpos_oracle as O
 import relpos_mhsa as M
 import workloads as W
-from _util import abs_err, oracle_params, random_weights, rel_err
+from _util import abs_err, oracle_params, random_weights, rel_err, row_rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -137,17 +138,20 @@ def test_position_scores_match_rel_shift(d_model, n_heads, T):
     P = p.linear_pos.forward(pos[0].astype(np.float64)).reshape(2 * T - 1, h, dk).transpose(1, 0, 2)
     bd = np.matmul(q + p.pos_bias_v.reshape(1, h, 1, dk), np.swapaxes(P, -1, -2)[None])
     ref = O.f32_scale(dk) * O.rel_shift(bd)[..., :T]
-    assert rel_err(got, ref) < 1e-5
+    assert row_rel_err(got, ref) < 1e-5
 
 
 @pytest.mark.parametrize("T", [37, 100, 300])
 def test_position_scores_bf16_match_rel_shift(T):
     """bf16 path (32x32 MFMA band with carried band tile, bf16 remap strip):
     bd is stored in bf16 as the reference stores matrix_bd (attention.rs:530),
-    from q_v = bf16(q + v) as the reference forms it (attention.rs:501-508).
-    Starting from the kernel's own bf16 q and P (the projections are pinned
-    separately), each score is within one bf16 ulp of rel_shift(q_v P^T)
-    rounded to bf16, plus fp32 accumulation noise."""
+    from q_v = bf16(q + v) as the reference forms it (attention.rs:501-508),
+    and the exported term is bf16(bd * bf16(s)) as `attend` materialises it
+    (attention.rs:308-311). Starting from the kernel's own bf16 q and P (the
+    projections are pinned separately), each term is bf16-representable and
+    equals bf16(bf16(rel_shift(q_v P^T)) * bf16(s)) exactly, except where the
+    kernel's fp32 band sum sits within accumulation noise of a bf16 rounding
+    boundary of bd; there it is the neighbouring value, within two ulps."""
     d_model, n_heads = 256, 2
     rng = np.random.default_rng(4)
     w = random_weights(rng, d_model, n_heads)
@@ -166,15 +170,20 @@ def test_position_scores_bf16_match_rel_shift(T):
     Pt = np.swapaxes(P, -1, -2)[None]
     exact = O.rel_shift(np.matmul(qv, Pt))[..., :T]
     acc = O.rel_shift(np.matmul(np.abs(qv), np.abs(Pt)))[..., :T] * 2.0 ** -20
-    ref = O.bf16_round(exact)
     sbd = float(O.bf16_round(np.float32(O.f32_scale(dk)))[()])
-    bd = got / sbd
-    # one ulp of the larger of the two values (a rounding may straddle a power of two)
-    _, e = np.frexp(np.maximum(np.abs(ref), np.abs(bd)))
+    ref = O.bf16_round(O.bf16_round(exact) * sbd)
+    assert np.array_equal(O.bf16_round(got), got), "the position term is not stored in bf16"
+    # bd within accumulation noise of a bf16 rounding boundary may round to
+    # the other neighbour: allow two ulps there, and only there
+    _, eb = np.frexp(np.abs(exact))
+    near = np.abs(np.abs(exact) - np.abs(O.bf16_round(exact))) >= np.ldexp(0.5, eb - 8) - acc
+    _, e = np.frexp(np.maximum(np.abs(ref), np.abs(got)))
     ulp = np.ldexp(1.0, e - 8)
-    bad = np.abs(bd - ref) > ulp + acc
-    assert not bad.any(), (f"{int(bad.sum())} of {bad.size} scores off by more than one ulp; worst "
-                           f"{float(np.max(np.abs(bd - ref) - ulp - acc)):.3g} at {np.argwhere(bad)[:3].tolist()}")
+    d = np.abs(got - ref)
+    bad = (d > 0) & ~(near & (d <= 2 * ulp))
+    print(f"T={T}: {int(np.sum(d > 0))} of {d.size} terms at a neighbouring bf16 value")
+    assert not bad.any(), (f"{int(bad.sum())} of {bad.size} terms differ; worst {float(np.max(d[bad])):.3g} "
+                           f"at {np.argwhere(bad)[:3].tolist()}")
 
 
 # ---------------------------------------------------------------------------
@@ -197,7 +206,7 @@ def test_forward_f32_contexts_and_padding(d_model, n_heads, ctx):
     got = host(layer.forward(dev(x, O.F32), dev(pos, O.F32), M.AttentionContext.new(*ctx) if ctx else None,
                              M.key_padding_mask(lengths, T)))
     rows = visible_rows(B, T, octx, lengths)
-    assert rel_err(got, ref, rows) < F32_TOL
+    assert row_rel_err(got, ref, rows) < F32_TOL
 
 
 def test_forward_f32_many_query_blocks():
@@ -218,7 +227,7 @@ def test_forward_f32_many_query_blocks():
         ref = O.mhsa_forward(p, x, pos, octx, O.key_padding_mask(lengths, T))
         got = host(layer.forward(dev(x, O.F32), dev(pos, O.F32), M.AttentionContext.new(*ctx) if ctx else None,
                                  M.key_padding_mask(lengths, T)))
-        assert rel_err(got, ref, visible_rows(B, T, octx, lengths)) < F32_TOL, ctx
+        assert row_rel_err(got, ref, visible_rows(B, T, octx, lengths)) < F32_TOL, ctx
 
 
 def test_forward_large_f32():
@@ -230,7 +239,7 @@ def test_forward_large_f32():
     ref = O.mhsa_forward(p, x, pos)
     layer = gpu_layer(layers[0], cfg.d_model, cfg.n_heads, cfg.use_bias, O.F32)
     got = host(layer.forward(dev(x, O.F32), dev(pos, O.F32)))
-    err = rel_err(got, ref)
+    err = row_rel_err(got, ref)
     print(f"large_f32 max relative error {err:.3e}")
     assert err < F32_TOL
 
@@ -311,7 +320,7 @@ def test_linear_f32_persistent_tiles(rows, quant):
     for name in ("linear_q", "linear_out"):
         got = host(layer.debug_linear(name, dev(x, O.F32)))
         ref = getattr(p, name).forward(x.astype(np.float64), O.F32)
-        assert rel_err(got, ref) < 1e-5, name
+        assert row_rel_err(got, ref) < 1e-5, name
 
 
 def test_forward_bf16_with_biases():
@@ -389,8 +398,8 @@ def test_padded_keys_are_ignored_gpu():
         short = host(layer.forward(dev(x[1:2, :valid], O.F32), dev(pe.get_encoding(valid), O.F32), ctx))
         # the reference's own bounds (attention.rs:1060-1061); the GEMM's K
         # split depends on the row count, so batch 1 and 2 sum in other orders
-        assert rel_err(masked[:1], full) < 1e-5
-        assert rel_err(masked[1:2, :valid], short) < 1e-5
+        assert row_rel_err(masked[:1], full) < 1e-5
+        assert row_rel_err(masked[1:2, :valid], short) < 1e-5
 
 
 def test_local_window_bf16_against_oracle():
@@ -460,7 +469,7 @@ def test_streaming_xl_50_steps():
             for b in range(B):
                 mask = O.streaming_mask((70, 13), "chunked_limited", C, fills[b], T, T)
                 ref, _ = O.mhsa_forward_with_cache(p, x[b:b + 1], pos, caches[b], mask)
-                e = rel_err(g[b:b + 1], ref)
+                e = row_rel_err(g[b:b + 1], ref)
                 worst = max(worst, e)
                 assert e < F32_TOL, (step, b, fills[b], e)
         for b in range(B):
@@ -469,6 +478,86 @@ def test_streaming_xl_50_steps():
     print(f"streaming worst relative error {worst:.3e}")
     cache_gpu = st.read_cache().cpu().numpy()
     assert np.array_equal(cache_gpu, np.concatenate(caches, 0).astype(np.float32))
+
+
+def test_streaming_new_stream_with_biases_no_mask():
+    """A stream that never saw load_cache starts from the reference's zero
+    cache (EncoderCache::new): its unfilled rows are h = 0, so their keys and
+    values are the projection biases (attention.rs:650, 721-722), visible
+    when no mask is given. Three steps with q/k/v/out biases against the
+    oracle carrying a zero-initialised cache."""
+    rng = np.random.default_rng(14)
+    w = random_weights(rng, 256, 2, use_bias=True, scale=0.05)
+    p = oracle_params(w, 256, 2)
+    B, C, T = 2, 20, 6
+    pos = O.RelPositionalEncoding(256, 5000, False).get_encoding(C + T)
+    layer = gpu_layer(w, 256, 2, True, O.F32)
+    st = layer.stream(B, C, T)
+    cache = np.zeros((B, C, 256))
+    for step in range(3):
+        x = rng.standard_normal((B, T, 256)).astype(np.float32)
+        got = host(st.step(dev(x, O.F32), dev(pos, O.F32)))
+        ref, cache = O.mhsa_forward_with_cache(p, x, pos, cache, None)
+        assert row_rel_err(got, ref) < F32_TOL, step
+    assert np.array_equal(st.read_cache().cpu().numpy(), cache.astype(np.float32))
+
+
+def test_streaming_weights_changed_mid_stream():
+    """The reference re-projects the cached h with the current weights on
+    every step; reloading weights between steps must do the same."""
+    rng = np.random.default_rng(15)
+    w1 = random_weights(rng, 256, 2, use_bias=True, scale=0.05)
+    w2 = random_weights(rng, 256, 2, use_bias=True, scale=0.05)
+    B, C, T = 2, 20, 6
+    pos = O.RelPositionalEncoding(256, 5000, False).get_encoding(C + T)
+    layer = gpu_layer(w1, 256, 2, True, O.F32)
+    st = layer.stream(B, C, T)
+    cache = rng.standard_normal((B, C, 256))
+    st.load_cache(dev(cache, O.F32), [C, C])
+    x = rng.standard_normal((B, T, 256)).astype(np.float32)
+    st.step(dev(x, O.F32), dev(pos, O.F32))
+    _, cache = O.mhsa_forward_with_cache(oracle_params(w1, 256, 2), x, pos, cache.astype(np.float32), None)
+    layer.load_weights(W.prefixed(w2, "layer"), "layer")
+    x = rng.standard_normal((B, T, 256)).astype(np.float32)
+    got = host(st.step(dev(x, O.F32), dev(pos, O.F32)))
+    ref, _ = O.mhsa_forward_with_cache(oracle_params(w2, 256, 2), x, pos, cache, None)
+    assert row_rel_err(got, ref) < F32_TOL
+
+
+@pytest.mark.parametrize("B,C,T,ctx", [(3, 140, 27, ((140, 26), "chunked_limited")),
+                                       (32, 140, 27, ((100, 8), "regular")),
+                                       (2, 100, 14, ((70, 13), "chunked_limited"))])
+def test_streaming_long_context_ring_wraps(B, C, T, ctx):
+    """Streaming shapes past the chunk kernel's limits (T > 16 or more than 96
+    keys), so the generic fp32 kernel reads the ring: key-split form (few
+    workgroups), four-wave form (B = 32) and one-wave form (T = 14, 114 keys).
+    Nine steps wrap the ring head past its end; every step is checked
+    against the oracle and the cache read back bit-equal."""
+    rng = np.random.default_rng(16)
+    d, h = 512, 4
+    w = random_weights(rng, d, h, use_bias=True, scale=0.04)
+    p = oracle_params(w, d, h)
+    pos = O.RelPositionalEncoding(d, 5000, False).get_encoding(C + T)
+    layer = gpu_layer(w, d, h, True, O.F32)
+    st = layer.stream(B, C, T)
+    cache = rng.standard_normal((B, C, d)).astype(np.float32)
+    fills = [int(v) for v in rng.integers(0, C + 1, size=B)]
+    for b in range(B):
+        cache[b, :C - fills[b]] = 0.0
+    st.load_cache(dev(cache, O.F32), fills)
+    caches = [cache[b:b + 1].astype(np.float64) for b in range(B)]
+    pos_d = dev(pos, O.F32)
+    (left, right), style = ctx
+    for step in range(9):
+        x = rng.standard_normal((B, T, d)).astype(np.float32)
+        got = host(st.step(dev(x, O.F32), pos_d, M.StreamingMask((left, right), style)))
+        for b in range(B):
+            mask = O.streaming_mask((left, right), style, C, fills[b], T, T)
+            ref, caches[b] = O.mhsa_forward_with_cache(p, x[b:b + 1], pos, caches[b], mask)
+            assert row_rel_err(got[b:b + 1], ref) < F32_TOL, (step, b)
+            fills[b] = O.next_fill(fills[b], T, 0, C)
+        assert st.fill() == fills
+    assert np.array_equal(st.read_cache().cpu().numpy(), np.concatenate(caches, 0).astype(np.float32))
 
 
 def test_streaming_rows_past_valid_give_output_bias():
@@ -487,7 +576,7 @@ def test_streaming_rows_past_valid_give_output_bias():
         mask = O.streaming_mask((4, 1), "regular", C, 4, T, 3)
         assert mask.dtype == np.bool_
         ref, _ = O.mhsa_forward_with_cache(p, x[b:b + 1], pos, cache[b:b + 1].astype(np.float64), mask)
-        assert rel_err(got[b:b + 1], ref) < F32_TOL
+        assert row_rel_err(got[b:b + 1], ref) < F32_TOL
         assert np.allclose(got[b, 3:], w["linear_out.bias"][None, :], atol=1e-6)
 
 
@@ -505,7 +594,7 @@ def test_streaming_functional_form_and_cache_drop():
     layer.cache_drop_size = 2
     out, nc = layer.forward_with_cache(dev(x, O.F32), dev(pos, O.F32), dev(cache, O.F32), C, None)
     ref, ref_nc = O.mhsa_forward_with_cache(p, x, pos, cache.astype(np.float64), None)
-    assert rel_err(host(out), ref) < F32_TOL
+    assert row_rel_err(host(out), ref) < F32_TOL
     assert np.array_equal(nc.cpu().numpy(), ref_nc.astype(np.float32))
 
 
@@ -522,7 +611,7 @@ def test_streaming_equals_offline_last_rows():
     st.load_cache(dev(seq[:, :C], O.F32), [C, C])
     got = host(st.step(dev(seq[:, C:], O.F32), dev(pos, O.F32)))
     full = host(layer.forward(dev(seq, O.F32), dev(pos, O.F32)))
-    assert rel_err(got, full[:, C:]) < 1e-5
+    assert row_rel_err(got, full[:, C:]) < 1e-5
 
 
 @pytest.mark.parametrize("d_model,n_heads,kind", [(256, 4, "u8"), (256, 4, "mixed"), (1280, 10, "u8"),
@@ -564,7 +653,7 @@ def test_streaming_projection_kinds_with_biases(d_model, n_heads, kind):
         for b in range(B):
             mask = O.streaming_mask((70, 13), "chunked_limited", C, fills[b], T, T)
             ref, _ = O.mhsa_forward_with_cache(p, x[b:b + 1], pos, caches[b], mask)
-            assert rel_err(got[b:b + 1], ref) < F32_TOL, (step, b)
+            assert row_rel_err(got[b:b + 1], ref) < F32_TOL, (step, b)
             caches[b] = O.cache_update(caches[b], x[b:b + 1].astype(np.float64), 0)
             fills[b] = O.next_fill(fills[b], T, 0, C)
         assert st.fill() == fills
@@ -591,10 +680,10 @@ def test_forward_f32_short_utterances(d_model, n_heads, T, lengths, ctx):
     got = host(layer.forward(dev(x, O.F32), dev(pos, O.F32), M.AttentionContext.new(*ctx) if ctx else None,
                              M.key_padding_mask(lengths, T)))
     rows = visible_rows(B, T, octx, lengths)
-    assert rel_err(got, ref, rows) < F32_TOL
+    assert row_rel_err(got, ref, rows) < F32_TOL
 
 
-@pytest.mark.parametrize("d_model,n_heads,T", [(256, 2, 50), (1024, 8, 40)])
+@pytest.mark.parametrize("d_model,n_heads,T", [(256, 2, 50), (1024, 8, 40), (1280, 10, 30)])
 def test_sublayer_f32_against_oracle(d_model, n_heads, T):
     """x + MHSA(LayerNorm(x)) (conformer.rs:1747-1780) in fp32 with LayerNorm
     gamma/beta and key padding: the LayerNorm kernel's statistics and affine,
@@ -613,7 +702,7 @@ def test_sublayer_f32_against_oracle(d_model, n_heads, T):
     layer.sublayer_forward_(xd, dev(pos, O.F32), None, M.key_padding_mask(lengths, T), gamma=gamma, beta=beta)
     got = host(xd)
     vis = visible_rows(2, T, None, lengths)
-    assert rel_err(got[vis], ref[vis]) < F32_TOL
+    assert row_rel_err(got[vis], ref[vis]) < F32_TOL
 
 
 # ---------------------------------------------------------------------------
@@ -665,7 +754,7 @@ def test_quantized_linear_full_shape(dtype):
                   f"{np.max((d - ulp) / acc):.3f} fp32 units of sum|x||w|")
             assert np.all(d <= ulp + acc), name
         else:
-            assert rel_err(got, ref) < 1e-5, name
+            assert row_rel_err(got, ref) < 1e-5, name
 
 
 @pytest.mark.parametrize("d_model,n_heads,rows", [(384, 6, 1537), (768, 6, 3000)])
@@ -718,24 +807,6 @@ def test_stack_u8_well_conditioned_against_oracle():
     err = rel_err(got, ref)
     print(f"well-conditioned u8 stack: max abs error {abs_err(got, ref):.3e}, / max|ref| {err:.3e}")
     assert err < 2e-2
-
-
-def test_stack_u8_specified_distribution_report():
-    """The specified distribution (E[W] ~ 1.4) drives logits to ~1e3, where
-    the softmax is argmax-like and a single bf16 ulp can change which key
-    wins; outputs are compared as a report only (printed), and must be finite."""
-    cfg = W.CONFIGS["xl_stack_u8"]
-    rng = np.random.default_rng(40)
-    layers = [W.make_layer_weights(rng, cfg.d_model, cfg.n_heads, False, True) for _ in range(2)]
-    T, lengths = 300, [300, 217]
-    x = rng.standard_normal((2, T, cfg.d_model)).astype(np.float32)
-    pos = O.RelPositionalEncoding(cfg.d_model, 5000, True).get_encoding(T)
-    ref = _stack_oracle(layers, cfg, x, lengths, pos, T)
-    got = host(_stack_gpu(layers, cfg, x, lengths, pos))
-    assert np.isfinite(got).all()
-    close = np.mean(np.abs(got - ref) <= 1e-2 * np.max(np.abs(ref)))
-    print(f"specified u8 stack: max|ref| {np.max(np.abs(ref)):.3e}, max error / max|ref| {rel_err(got, ref):.3e}, "
-          f"fraction of outputs within 1% of max|ref|: {close:.4f}")
 
 
 def test_stack_u8_full_size_deterministic():

@@ -385,6 +385,98 @@ def test_bf16_mode_rounds_only_at_op_boundaries():
     assert 0 < np.max(np.abs(f - b)) < 0.05 * np.max(np.abs(f))
 
 
+def _torch_bf16_forward(p, x, pos):
+    """The reference's offline bf16 forward with every array a torch bfloat16
+    tensor, so each op result is stored in bf16 because of its dtype, not
+    because of an explicit rounding call (torch's CPU bf16 matmul accumulates
+    in fp32 and rounds once, as MLX's does):
+
+    linear outputs and bias adds (quantization.rs:126-136), q + pos_bias_u/v
+    (attention.rs:501-508), matrix_bd (530), bd * cast(scale) (308-311), the
+    attention output (315-317). The softmax itself runs in float64 (MLX's SDPA
+    precision is unpinned). rel_shift is taken from its closed form
+    out[i][j] = bd[i][T-1-i+j] (attention.rs:1248-1282) with a gather.
+    """
+    bf = torch.bfloat16
+    t = lambda a: torch.tensor(np.asarray(a, dtype=np.float32)).to(bf)
+    B, T, D = x.shape
+    h, dk = p.n_heads, p.head_dim
+
+    def linear(lin, a):
+        y = a @ t(lin.weight).T
+        return y + t(lin.bias) if lin.bias is not None else y
+
+    split = lambda y, n: y.reshape(y.shape[0], n, h, dk).transpose(1, 2)
+    X, PE = t(x), t(pos[0])
+    q = split(linear(p.linear_q, X), T)
+    k = split(linear(p.linear_k, X), T)
+    v = split(linear(p.linear_v, X), T)
+    P = split(linear(p.linear_pos, PE)[None], 2 * T - 1)
+    q_u = q + t(p.pos_bias_u).reshape(1, h, 1, dk)
+    q_v = q + t(p.pos_bias_v).reshape(1, h, 1, dk)
+    bd = q_v @ P.transpose(-1, -2)  # [B, h, T, 2T-1], bf16
+    i = torch.arange(T).reshape(T, 1)
+    j = torch.arange(T).reshape(1, T)
+    idx = ((T - 1) - i + j).expand(B, h, T, T)
+    bd = torch.gather(bd, 3, idx)
+    scale = torch.tensor(1.0, dtype=torch.float32) / torch.sqrt(torch.tensor(float(dk), dtype=torch.float32))
+    pos_term = bd * scale.to(bf)  # bf16 * bf16 -> bf16
+    logits = scale.double() * (q_u.double() @ k.double().transpose(-1, -2)) + pos_term.double()
+    ctx = (torch.softmax(logits, dim=-1) @ v.double()).to(bf)
+    ctx = ctx.transpose(1, 2).reshape(B, T, D)
+    return linear(p.linear_out, ctx).double().numpy()
+
+
+def _bf16_case():
+    """A small case whose every bf16 rounding changes the output: bf16-exact
+    inputs and weights with full 8-bit significands, so each matmul and add
+    produces more bits than bf16 keeps, and d_k = 8, whose 1/sqrt(d_k) is not
+    a bf16 number (bf16(1/sqrt 8) = 0.353515625)."""
+    d, h, T = 16, 2, 5
+    p = random_params(d, h, seed=11, scale=0.6)
+    rng = np.random.default_rng(12)
+    x = O.bf16_round(rng.standard_normal((2, T, d)))
+    pos = O.bf16_round(O.RelPositionalEncoding(d, 64, False).get_encoding(T))
+    return p, x, pos
+
+
+def test_bf16_oracle_equals_native_bf16_restatement():
+    """Pins where the bf16 oracle rounds: it must equal, bit for bit, the
+    reference's op sequence run on native bfloat16 tensors."""
+    p, x, pos = _bf16_case()
+    got = O.mhsa_forward(p, x, pos, dtype=O.BF16)
+    ref = _torch_bf16_forward(p, x, pos)
+    assert np.array_equal(got, ref), np.max(np.abs(got - ref))
+
+
+def test_bf16_oracle_every_rounding_is_load_bearing(monkeypatch):
+    """Dropping any single one of the oracle's bf16 roundings (op results via
+    `_rnd`, weight and bias casts via `to_dtype`) changes the output of the
+    case above, so together with the bit-exact match to the native-bf16
+    restatement a dropped or an added rounding fails."""
+    p, x, pos = _bf16_case()
+    base = O.mhsa_forward(p, x, pos, dtype=O.BF16)
+    for fname in ("_rnd", "to_dtype"):
+        orig = getattr(O, fname)
+        calls = {"n": 0, "skip": -1}
+
+        def patched(a, dtype, _orig=orig):
+            calls["n"] += 1
+            if calls["n"] - 1 == calls["skip"]:
+                return np.asarray(a, dtype=np.float64)
+            return _orig(a, dtype)
+
+        monkeypatch.setattr(O, fname, patched)
+        O.mhsa_forward(p, x, pos, dtype=O.BF16)
+        n = calls["n"]
+        assert n == (13 if fname == "_rnd" else 11), (fname, n)
+        for k in range(n):
+            calls["n"], calls["skip"] = 0, k
+            out = O.mhsa_forward(p, x, pos, dtype=O.BF16)
+            assert not np.array_equal(out, base), f"dropping {fname} call {k} of {n} leaves the output unchanged"
+        monkeypatch.setattr(O, fname, orig)
+
+
 # ---------------------------------------------------------------------------
 # a11-a14: streaming (attention.rs:606-816, conformer.rs:97-323, 883-1036)
 # ---------------------------------------------------------------------------
