@@ -166,6 +166,24 @@ int32_t mhsa_forward(mhsa_layer* layer, const void* x, int32_t batch, int32_t se
                      int32_t pos_len, const mhsa_context* ctx, const int32_t* key_lengths_host, void* out,
                      void* hip_stream);
 
+/* No counterpart in the reference. mhsa_forward for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): same arguments and results, but every
+ * intermediate lives in a fixed 128 MiB device array of the library (16 MiB
+ * of split-K partials, 112 MiB of workspace), one per GPU, held until the
+ * process ends; it calls no hipMalloc or hipFree. Inputs needing more
+ * workspace fail with MHSA_EINVAL (the message gives the bytes needed: about
+ * 10 * d_model bytes per frame (batch * seq_len) plus 4 * d_model per position
+ * row in bf16, 16 and 8 in fp32; at the 0.6B shape, batch 8 x 375 frames
+ * needs 33 MB and batch 4 x 1500 needs 67 MB). The layer's parameters must
+ * already be on the device (uploading allocates): after loading weights or
+ * changing the dtype, run mhsa_forward once. All calls on one GPU share the
+ * array, so calls that overlap on one GPU (different streams or threads)
+ * race; serialise them. */
+int32_t mhsa_forward_noalloc(mhsa_layer* layer, const void* x, int32_t batch, int32_t seq_len, const void* pos_emb,
+                             int32_t pos_len, const mhsa_context* ctx, const int32_t* key_lengths_host, void* out,
+                             void* hip_stream);
+
 /* x <- x + forward(LayerNorm(x)) : the MHSA sublayer of ConformerBlock
  * (conformer.rs:1747-1780). ln_gamma / ln_beta [d_model] HOST fp32 arrays
  * (NULL = 1 / 0), eps as nn::LayerNorm (1e-5); d_model <= 2048. */

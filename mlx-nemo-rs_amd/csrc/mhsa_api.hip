@@ -16,6 +16,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -198,6 +199,7 @@ struct mhsa_layer {
   // scratch
   DevBuf ws;
   DevBuf gemm_partial;         // K-split partial sums of small GEMMs
+  float* partial_override = nullptr;  // set for the duration of an allocation-free call
   DevBuf vtbuf;                // bf16: transposed V [D][B * Tpad]
   DevBuf hbuf;                 // sublayer: LayerNorm output
   const char* last_qkv = nullptr;  // where the last offline forward put [q|k|v] rows
@@ -216,12 +218,13 @@ struct ProfScope {
   Profiler& p;
   hipStream_t s;
   int idx;
-  ProfScope(mhsa_layer* L, const char* tag, hipStream_t s_) : p(L->prof), s(s_), idx(L->prof.begin(tag, s_)) {}
+  ProfScope(mhsa_layer* L, const char* tag, hipStream_t s_, bool enabled = true)
+      : p(L->prof), s(s_), idx(enabled ? L->prof.begin(tag, s_) : -1) {}
   ~ProfScope() { p.end(idx, s); }
   // Close the current span and open the next one.
   void next(const char* tag) {
     p.end(idx, s);
-    idx = p.begin(tag, s);
+    idx = idx >= 0 || p.on ? p.begin(tag, s) : -1;
   }
 };
 }  // namespace
@@ -351,8 +354,12 @@ int32_t run_gemm(mhsa_layer* L, const DevLinear& lin, int n_rows_w, const void* 
   p.seg_stride = seg_rows > 0 ? seg_stride : 0;
   p.ring_off = ring_off;
   p.ring_len = ring_len > 0 ? ring_len : std::max(M, 1);
-  HIPCHK(L->gemm_partial.ensure((size_t)mhsa::kGemmPartialElems * sizeof(float)));
-  p.partial = static_cast<float*>(L->gemm_partial.p);
+  if (L->partial_override) {
+    p.partial = L->partial_override;
+  } else {
+    HIPCHK(L->gemm_partial.ensure((size_t)mhsa::kGemmPartialElems * sizeof(float)));
+    p.partial = static_cast<float*>(L->gemm_partial.p);
+  }
   p.partial_elems = mhsa::kGemmPartialElems;
   if (vt) {
     p.vt = vt->p;
@@ -483,15 +490,30 @@ struct AttnDebug {
   bool any() const { return bd || top; }
 };
 
+// Fixed device memory an allocation-free call works in: [workspace | V^T]
+// carved from `base`, `cap` bytes (the GEMMs' split-K partials are given
+// separately through the layer's partial_override).
+struct Arena {
+  char* base = nullptr;
+  size_t cap = 0;
+};
+
 int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos_emb, int pos_len,
                      const mhsa_context* ctx, const int32_t* lens, void* out, const void* residual,
-                     const AttnDebug& dbg, hipStream_t s) {
+                     const AttnDebug& dbg, hipStream_t s, const Arena* arena = nullptr) {
   if (B <= 0 || T <= 0) return fail(MHSA_EINVAL, "batch and seq_len must be positive (got %d, %d)", B, T);
   if (!x || !pos_emb || (!out && !dbg.any())) return fail(MHSA_EINVAL, "null tensor pointer");
   if (!aligned16(x) || !aligned16(pos_emb) || (out && !aligned16(out)))
     return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
-  int32_t rc = prepare(L);
-  if (rc) return rc;
+  int32_t rc;
+  if (arena) {
+    if (L->dirty)
+      return fail(MHSA_EINVAL, "the layer's parameters changed since their last upload, and uploading allocates: "
+                               "run mhsa_forward once after loading weights or changing the dtype");
+  } else if ((rc = prepare(L))) {
+    return rc;
+  }
+  const bool prof = !arena;  // (event pairs are created on first use)
   const int D = L->D;
   const size_t es = esz(L);
   const DistRange dr = context_distances(ctx, 0, T, T);
@@ -528,34 +550,55 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   const int64_t prow_n = nrows + 2 * (int64_t)pad;
   const size_t qkv_b = align_up((M + kv_pad) * 3 * D * es, 256), p_b = align_up(prow_n * D * es, 256),
                ctx_b = align_up(M * D * es, 256);
-  const size_t ws_before = L->ws.n;
-  HIPCHK(L->ws.ensure(qkv_b + p_b + ctx_b));
-  if (L->ws.n != ws_before) HIPCHK(mhsa::fill_zero(L->ws.p, L->ws.n, s));  // slack rows start finite
-  char* qkv = static_cast<char*>(L->ws.p);
-  char* P = qkv + qkv_b + (size_t)pad * D * es;  // table rows [0, nrows) after `pad` slack rows
-  char* cx = qkv + qkv_b + p_b;
-  L->last_qkv = qkv;
-  L->last_pos = P;
-  // bf16: V also transposed per batch, [D][B * Tpad], for the MFMA PV operand;
-  // zero-filled on allocation so padding columns are finite
+  // bf16: V also transposed per batch, [D][B * Tpad], for the MFMA PV operand.
+  // The QKV GEMM writes every column the attention kernel reads (whole tiles
+  // of tokens: projections of the next utterance's rows, or of zero rows past
+  // the last one), so it needs no clearing.
   VtOut vt;
+  size_t vt_b = 0;
   if (use_vt) {
     vt.T = T;
     vt.Tpad = (int)align_up(T, 256);  // whole GEMM tiles of tokens per utterance
     vt.ld = (int64_t)B * vt.Tpad;
-    const size_t bytes = (size_t)D * vt.ld * 2;
-    const size_t before = L->vtbuf.n;
-    HIPCHK(L->vtbuf.ensure(bytes));
-    if (L->vtbuf.n != before) HIPCHK(mhsa::fill_zero(L->vtbuf.p, L->vtbuf.n, s));
-    vt.p = L->vtbuf.p;
+    vt_b = align_up((int64_t)D * vt.ld * 2, 256);
   }
+  char* qkv;
+  if (arena) {
+    if (qkv_b + p_b + ctx_b + vt_b > arena->cap)
+      return fail(MHSA_EINVAL, "batch %d x seq_len %d needs %zu bytes of workspace; the allocation-free forward "
+                  "has %zu", B, T, qkv_b + p_b + ctx_b + vt_b, arena->cap);
+    qkv = arena->base;
+    if (use_vt) vt.p = arena->base + qkv_b + p_b + ctx_b;
+    // the slack rows the bf16 kernel may read (key rows past the last item,
+    // position rows around the table) hold the previous call's values: clear them
+    if (kv_pad) HIPCHK(mhsa::fill_zero(qkv + (size_t)M * 3 * D * es, (size_t)kv_pad * 3 * D * es, s));
+    if (pad) {
+      HIPCHK(mhsa::fill_zero(qkv + qkv_b, (size_t)pad * D * es, s));
+      HIPCHK(mhsa::fill_zero(qkv + qkv_b + (size_t)(pad + nrows) * D * es, (size_t)pad * D * es, s));
+    }
+  } else {
+    const size_t ws_before = L->ws.n;
+    HIPCHK(L->ws.ensure(qkv_b + p_b + ctx_b));
+    if (L->ws.n != ws_before) HIPCHK(mhsa::fill_zero(L->ws.p, L->ws.n, s));  // slack rows start finite
+    qkv = static_cast<char*>(L->ws.p);
+    if (use_vt) {
+      const size_t before = L->vtbuf.n;
+      HIPCHK(L->vtbuf.ensure(vt_b));
+      if (L->vtbuf.n != before) HIPCHK(mhsa::fill_zero(L->vtbuf.p, L->vtbuf.n, s));
+      vt.p = L->vtbuf.p;
+    }
+  }
+  char* P = qkv + qkv_b + (size_t)pad * D * es;  // table rows [0, nrows) after `pad` slack rows
+  char* cx = qkv + qkv_b + p_b;
+  L->last_qkv = qkv;
+  L->last_pos = P;
 
   {
-    ProfScope ps(L, "gemm_qkv", s);
+    ProfScope ps(L, "gemm_qkv", s, prof);
     if ((rc = project_qkv(L, x, (int)M, qkv, 3 * D, s, use_vt ? &vt : nullptr))) return rc;
   }
   {
-    ProfScope ps(L, "gemm_pos", s);
+    ProfScope ps(L, "gemm_pos", s, prof);
     if ((rc = run_gemm(L, L->dev[4], D, static_cast<const char*>(pos_emb) + (size_t)row0 * D * es, D, nrows, P, D,
                        nullptr, 0, s)))
       return rc;
@@ -582,13 +625,48 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
     a.vt_bs = vt.Tpad;
   }
   {
-    ProfScope ps(L, "attention", s);
+    ProfScope ps(L, "attention", s, prof);
     rc = run_attention(L, a, B, key_bounds, s);
   }
   if (rc) return rc;
   if (!out) return MHSA_OK;
-  ProfScope ps(L, "gemm_out", s);
+  ProfScope ps(L, "gemm_out", s, prof);
   return run_gemm(L, L->dev[3], D, cx, D, (int)M, out, D, residual, D, s);
+}
+
+// ---- allocation-free forward ---------------------------------------------
+// mhsa_forward_noalloc works in this array: the GEMMs' split-K partials
+// (kGemmPartialElems floats, as the allocating path uses, so both paths make
+// the same kernel choices and give the same bits) followed by the offline
+// workspace ([q|k|v] rows, position rows, attention output, bf16 V^T).
+// Each GPU the library runs on holds its own copy until the process ends.
+constexpr size_t kNoAllocScratchBytes = (size_t)128 << 20;
+constexpr size_t kNoAllocPartialBytes = (size_t)mhsa::kGemmPartialElems * sizeof(float);
+static_assert(kNoAllocPartialBytes % 256 == 0 && kNoAllocPartialBytes < kNoAllocScratchBytes, "scratch split");
+}  // namespace
+
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+// Device address of `scratch` per device: host code never uses the array's
+// name as an address (on the host it is only a stand-in for the symbol).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+char* g_scratch_dev[kMaxDevices] = {};
+
+int32_t scratch_for_current_device(char** out) {
+  int dev = -1;
+  HIPCHK(hipGetDevice(&dev));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MHSA_EINVAL, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    HIPCHK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) return fail(MHSA_EHIP, "hipGetSymbolAddress returned a null address");
+    g_scratch_dev[dev] = static_cast<char*>(p);
+  }
+  *out = g_scratch_dev[dev];
+  return MHSA_OK;
 }
 
 // K and V of every ring row from the cached inputs h (the reference
@@ -801,6 +879,22 @@ int32_t mhsa_forward(mhsa_layer* L, const void* x, int32_t batch, int32_t seq_le
   if (!out) return fail(MHSA_EINVAL, "null output pointer");
   return forward_impl(L, x, batch, seq_len, pos_emb, pos_len, ctx, lens, out, nullptr, AttnDebug(),
                       static_cast<hipStream_t>(hs));
+}
+
+int32_t mhsa_forward_noalloc(mhsa_layer* L, const void* x, int32_t batch, int32_t seq_len, const void* pos_emb,
+                             int32_t pos_len, const mhsa_context* ctx, const int32_t* lens, void* out, void* hs) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (!out) return fail(MHSA_EINVAL, "null output pointer");
+  char* base = nullptr;
+  if (int32_t rc = scratch_for_current_device(&base)) return rc;
+  Arena arena;
+  arena.base = base + kNoAllocPartialBytes;
+  arena.cap = kNoAllocScratchBytes - kNoAllocPartialBytes;
+  L->partial_override = reinterpret_cast<float*>(base);
+  const int32_t rc = forward_impl(L, x, batch, seq_len, pos_emb, pos_len, ctx, lens, out, nullptr, AttnDebug(),
+                                  static_cast<hipStream_t>(hs), &arena);
+  L->partial_override = nullptr;
+  return rc;
 }
 
 int32_t mhsa_sublayer_forward(mhsa_layer* L, void* x, int32_t batch, int32_t seq_len, const float* gamma,

@@ -32,7 +32,7 @@ LINEARS = ("linear_q", "linear_k", "linear_v", "linear_out", "linear_pos")
 EXPORTS = (
     "mhsa_last_error", "mhsa_version", "mhsa_create", "mhsa_destroy", "mhsa_set_dtype", "mhsa_get_dtype",
     "mhsa_head_dim", "mhsa_n_heads", "mhsa_d_model", "mhsa_set_cache_drop_size", "mhsa_load_linear_standard",
-    "mhsa_load_linear_quantized", "mhsa_load_pos_bias", "mhsa_load_weights", "mhsa_forward",
+    "mhsa_load_linear_quantized", "mhsa_load_pos_bias", "mhsa_load_weights", "mhsa_forward", "mhsa_forward_noalloc",
     "mhsa_sublayer_forward", "mhsa_stream_create", "mhsa_stream_destroy", "mhsa_stream_load_cache",
     "mhsa_stream_read_cache", "mhsa_stream_fill", "mhsa_forward_with_cache", "mhsa_pos_encoding",
     "mhsa_debug_dequantize", "mhsa_debug_linear", "mhsa_debug_offline_mask", "mhsa_debug_stream_mask", "mhsa_debug_rel_shift_index",
@@ -93,6 +93,7 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_load_pos_bias": (I, [VP, I, VP, VP]),
         "mhsa_load_weights": (I, [VP, P(Tensor), I, ctypes.c_char_p, I, I, I]),
         "mhsa_forward": (I, [VP, VP, I, I, VP, I, P(Context), PI, VP, VP]),
+        "mhsa_forward_noalloc": (I, [VP, VP, I, I, VP, I, P(Context), PI, VP, VP]),
         "mhsa_sublayer_forward": (I, [VP, VP, I, I, P(ctypes.c_float), P(ctypes.c_float), F, VP, I, P(Context), PI,
                                       VP]),
         "mhsa_stream_create": (I, [VP, I, I, I, P(VP)]),
@@ -368,6 +369,21 @@ class RelPositionMultiHeadAttention:
         _check(self._lib.mhsa_forward(self._h, _dptr(x), b, t, _dptr(pe), pe.shape[0],
                                       ctypes.byref(ctx) if ctx is not None else None, lens, _dptr(out),
                                       _stream_ptr()))
+        return out
+
+    def forward_noalloc(self, x, pos_emb, out, context: Optional[AttentionContext] = None,
+                        key_mask: Optional[Sequence[int]] = None):
+        """`forward` into a caller-given `out`, with every intermediate in the
+        library's fixed per-GPU scratch (no device allocation; no counterpart
+        in the reference). The parameters must already be uploaded: run
+        `forward` once after loading weights or changing the dtype."""
+        b, t, d = x.shape
+        pe = pos_emb.reshape(-1, d)
+        self._check_dev(x, pe, out)
+        ctx = context.c() if context is not None else None
+        _check(self._lib.mhsa_forward_noalloc(self._h, _dptr(x), b, t, _dptr(pe), pe.shape[0],
+                                              ctypes.byref(ctx) if ctx is not None else None, _int_array(key_mask),
+                                              _dptr(out), _stream_ptr()))
         return out
 
     def sublayer_forward_(self, x, pos_emb, context=None, key_mask=None, gamma=None, beta=None, eps=1e-5):
