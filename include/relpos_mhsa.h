@@ -198,7 +198,8 @@ int32_t mhsa_sublayer_forward(mhsa_layer* layer, void* x_inout, int32_t batch, i
  * `cache_size` frames (EncoderCache::last_channel slice, streaming/core.rs:
  * 117-166) kept as an HBM ring of C + chunk_len rows holding the cached
  * normalised inputs h and their projected K and V, plus each session's
- * fill. Zero-filled at creation, like EncoderCache::new. Only fp32 layers. */
+ * fill. Zero-filled at creation, like EncoderCache::new. The cache is fp32
+ * for both layer dtypes, as the reference keeps it (conformer.rs:422-434). */
 int32_t mhsa_stream_create(mhsa_layer* layer, int32_t batch, int32_t cache_size, int32_t chunk_len,
                            mhsa_stream** out);
 void mhsa_stream_destroy(mhsa_stream* stream);
@@ -216,14 +217,28 @@ int32_t mhsa_stream_fill(const mhsa_stream* stream, int32_t* filled_out_host);
  * followed by the encoder's cache pad/truncate and fill update
  * (conformer.rs:983-999, 1025-1036).
  *  x       [batch, chunk_len, d_model] device fp32 (the normalised input h)
- *  pos_emb [2*(cache_size+chunk_len)-1, d_model] device fp32; its projection
- *          is memoised per pos_len as the reference does (attention.rs:749-761)
+ *  pos_emb [2*(cache_size+chunk_len)-1, d_model] device, layer dtype; its
+ *          projection is memoised per pos_len as the reference does
+ *          (attention.rs:749-761)
  *  mask    NULL = no mask (att_context_size absent)
  *  out     [batch, chunk_len, d_model] device fp32
+ * Activations are fp32 for both layer dtypes: with an f32 cache the
+ * reference's [cache; x] and everything derived from it are f32 (MLX
+ * promotes the bf16 parameters), and the streamed features are never cast to
+ * the layer dtype (conformer.rs:845-849); a bf16 layer contributes its bf16
+ * parameter values and bf16 position rows.
  * Afterwards the cache holds [cache[q_keep:]; x[:q_keep]] (q_keep =
  * chunk_len - cache_drop_size) and fill = min(fill + q_keep, cache_size). */
 int32_t mhsa_forward_with_cache(mhsa_layer* layer, mhsa_stream* stream, const void* x, const void* pos_emb,
                                 int32_t pos_len, const mhsa_stream_mask* mask, void* out, void* hip_stream);
+/* forward_with_cache(x, pos_emb, None, _, att_mask): the no-cache path
+ * (attention.rs:687-700), keys and values from x alone (total_len =
+ * seq_len). Same dtypes as mhsa_forward_with_cache; pos_emb has
+ * 2*seq_len-1 rows; the mask's fill levels do not apply (there is no cache).
+ * The reference's returned cache is x[:, :seq_len - cache_drop_size], a slice
+ * of the caller's own input. */
+int32_t mhsa_forward_uncached(mhsa_layer* layer, const void* x, int32_t batch, int32_t seq_len, const void* pos_emb,
+                              int32_t pos_len, const mhsa_stream_mask* mask, void* out, void* hip_stream);
 
 /* ---- helpers ------------------------------------------------------------ */
 

@@ -132,6 +132,9 @@ hipError_t ring_write(DType dt, const void* src, void* ring, int B, int n, int D
 hipError_t ring_read(DType dt, const void* ring, void* dst, int B, int n, int D, int R, int64_t ld,
                      int off, hipStream_t s);
 
+// dst[i] = float(src[i]) for n bf16 values (16-byte aligned, n % 8 == 0).
+hipError_t widen_bf16(const void* src, float* dst, int64_t n, hipStream_t s);
+
 // Zero-fill of device memory by a kernel (no memset node under graph capture).
 hipError_t fill_zero(void* ptr, size_t bytes, hipStream_t s);
 

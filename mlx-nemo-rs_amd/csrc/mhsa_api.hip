@@ -206,9 +206,16 @@ struct mhsa_layer {
   const char* last_pos = nullptr;  // and its projected position rows (debug export)
   DevBuf ln_dev;               // sublayer: LayerNorm gamma, beta
   std::vector<float> ln_host;  // values currently in ln_dev
-  // streaming position memo (attention.rs:749-761)
+  // Parameters the fp32 streaming kernels read (see prepare_stream): an
+  // fp32 layer's own, or a bf16 layer's promoted to fp32
+  DevLinear sdev[5];
+  DevBuf wbuf32;               // bf16 layer: fp32 copies of its bf16 dense weights
+  uint64_t stream_version = 0; // layer version sdev was built for
+  // streaming position memo (attention.rs:749-761), fp32
   DevBuf pmemo;
+  DevBuf pmemo_bf16;           // bf16 layer: the projection before widening
   int pmemo_len = -1;
+  DevBuf uws;                  // workspace of the no-cache path
   Profiler prof;
 };
 
@@ -334,9 +341,9 @@ struct VtOut {
   int T = 0, Tpad = 0;
 };
 
-int32_t run_gemm(mhsa_layer* L, const DevLinear& lin, int n_rows_w, const void* A, int64_t lda, int M, void* C,
-                 int64_t ldc, const void* R, int64_t ldr, hipStream_t s, int seg_rows = 0, int seg_stride = 0,
-                 int ring_off = 0, int ring_len = 0, const VtOut* vt = nullptr) {
+int32_t run_gemm(mhsa_layer* L, DType dt, const DevLinear& lin, int n_rows_w, const void* A, int64_t lda, int M,
+                 void* C, int64_t ldc, const void* R, int64_t ldr, hipStream_t s, int seg_rows = 0,
+                 int seg_stride = 0, int ring_off = 0, int ring_len = 0, const VtOut* vt = nullptr) {
   mhsa::GemmParams p;
   p.A = A;
   p.lda = lda;
@@ -368,7 +375,7 @@ int32_t run_gemm(mhsa_layer* L, const DevLinear& lin, int n_rows_w, const void* 
     p.vt_Tpad = vt->Tpad;
     p.seg_T = vt->T;  // per-utterance M tiles
   }
-  HIPCHK(mhsa::gemm(dtype_of(L), lin.quantized, p, s));
+  HIPCHK(mhsa::gemm(dt, lin.quantized, p, s));
   return MHSA_OK;
 }
 
@@ -383,7 +390,8 @@ int32_t project_qkv(mhsa_layer* L, const void* A, int M, void* out, int64_t ldo,
       v = *vt;
       v.col0 = 2 * L->D;
     }
-    return run_gemm(L, L->dev[0], 3 * L->D, A, L->D, M, out, ldo, nullptr, 0, s, 0, 0, 0, 0, vt ? &v : nullptr);
+    return run_gemm(L, L->dt, L->dev[0], 3 * L->D, A, L->D, M, out, ldo, nullptr, 0, s, 0, 0, 0, 0,
+                    vt ? &v : nullptr);
   }
   for (int i = 0; i < 3; ++i) {
     VtOut v;
@@ -391,7 +399,7 @@ int32_t project_qkv(mhsa_layer* L, const void* A, int M, void* out, int64_t ldo,
       v = *vt;
       v.col0 = 0;
     }
-    int32_t rc = run_gemm(L, L->dev[i], L->D, A, L->D, M, static_cast<char*>(out) + (size_t)i * L->D * es, ldo,
+    int32_t rc = run_gemm(L, L->dt, L->dev[i], L->D, A, L->D, M, static_cast<char*>(out) + (size_t)i * L->D * es, ldo,
                           nullptr, 0, s, 0, 0, 0, 0, (vt && i == 2) ? &v : nullptr);
     if (rc) return rc;
   }
@@ -464,12 +472,12 @@ void set_ctx(mhsa::AttnParams& a, const mhsa_context* ctx) {
 // Launch attention in batch chunks of kMaxBatch; `per_batch` fills the
 // per-item key range / valid rows.
 template <typename Fn>
-int32_t run_attention(const mhsa_layer* L, mhsa::AttnParams a, int B, Fn per_batch, hipStream_t s) {
+int32_t run_attention(const mhsa_layer* L, DType dt, mhsa::AttnParams a, int B, Fn per_batch, hipStream_t s) {
   for (int b0 = 0; b0 < B; b0 += mhsa::kMaxBatch) {
     const int nb = std::min(mhsa::kMaxBatch, B - b0);
     a.b0 = b0;
     for (int i = 0; i < nb; ++i) per_batch(b0 + i, a.key_lo[i], a.key_hi[i], a.q_valid[i]);
-    HIPCHK(mhsa::attention(dtype_of(L), L->dk, a, nb, s));
+    HIPCHK(mhsa::attention(dt, L->dk, a, nb, s));
   }
   return MHSA_OK;
 }
@@ -599,7 +607,7 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   }
   {
     ProfScope ps(L, "gemm_pos", s, prof);
-    if ((rc = run_gemm(L, L->dev[4], D, static_cast<const char*>(pos_emb) + (size_t)row0 * D * es, D, nrows, P, D,
+    if ((rc = run_gemm(L, L->dt, L->dev[4], D, static_cast<const char*>(pos_emb) + (size_t)row0 * D * es, D, nrows, P, D,
                        nullptr, 0, s)))
       return rc;
   }
@@ -626,12 +634,12 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   }
   {
     ProfScope ps(L, "attention", s, prof);
-    rc = run_attention(L, a, B, key_bounds, s);
+    rc = run_attention(L, L->dt, a, B, key_bounds, s);
   }
   if (rc) return rc;
   if (!out) return MHSA_OK;
   ProfScope ps(L, "gemm_out", s, prof);
-  return run_gemm(L, L->dev[3], D, cx, D, (int)M, out, D, residual, D, s);
+  return run_gemm(L, L->dt, L->dev[3], D, cx, D, (int)M, out, D, residual, D, s);
 }
 
 // ---- allocation-free forward ---------------------------------------------
@@ -679,13 +687,51 @@ int32_t reproject_ring(mhsa_layer* L, mhsa_stream* S, hipStream_t s) {
   char* kv = static_cast<char*>(S->ring_kv.p);
   int32_t rc;
   if (L->qkv_fused) {
-    rc = run_gemm(L, L->dev[1], 2 * D, S->ring_h.p, D, M, kv, 2 * D, nullptr, 0, s);
+    rc = run_gemm(L, mhsa::kF32, L->sdev[1], 2 * D, S->ring_h.p, D, M, kv, 2 * D, nullptr, 0, s);
   } else {
-    rc = run_gemm(L, L->dev[1], D, S->ring_h.p, D, M, kv, 2 * D, nullptr, 0, s);
-    if (!rc) rc = run_gemm(L, L->dev[2], D, S->ring_h.p, D, M, kv + (size_t)D * 4, 2 * D, nullptr, 0, s);
+    rc = run_gemm(L, mhsa::kF32, L->sdev[1], D, S->ring_h.p, D, M, kv, 2 * D, nullptr, 0, s);
+    if (!rc)
+      rc = run_gemm(L, mhsa::kF32, L->sdev[2], D, S->ring_h.p, D, M, kv + (size_t)D * 4, 2 * D, nullptr, 0, s);
   }
   if (rc) return rc;
   S->kv_version = L->version;
+  return MHSA_OK;
+}
+
+// The streaming path computes in fp32 for both layer dtypes. The reference
+// keeps the streaming caches in f32 (conformer.rs:422-434) and never casts
+// the streamed features to the layer dtype (conformer.rs:845-849), so in a
+// bf16 model [cache; x] and every activation derived from it are f32: MLX
+// promotes the bf16 parameters to f32 in each op, and a quantized
+// projection dequantises in f32 from its bf16-cast scales and biases. Only
+// the position rows are computed in bf16 (a bf16 table through bf16 weights,
+// attention.rs:749-761). So for a bf16 layer the fp32 kernels read: dense
+// weights as fp32 copies of their bf16 values, quantized ones as uploaded
+// (codes + bf16-rounded scale/bias pairs, dequantised in fp32 by the GEMM),
+// biases and pos biases as uploaded (bf16-rounded floats).
+int32_t prepare_stream(mhsa_layer* L) {
+  int32_t rc = prepare(L);
+  if (rc) return rc;
+  if (L->stream_version == L->version) return MHSA_OK;
+  for (int i = 0; i < 5; ++i) L->sdev[i] = L->dev[i];
+  if (L->dt == mhsa::kBF16) {
+    const size_t n = (size_t)L->D * L->D;
+    std::vector<float> host(5 * n, 0.f);
+    bool any_dense = false;
+    for (int i = 0; i < 5; ++i)
+      if (!L->lin[i].quantized) {
+        any_dense = true;
+        for (size_t e = 0; e < n; ++e) host[i * n + e] = round_bf16(L->lin[i].w[e]);
+      }
+    if (any_dense) {
+      if (L->wbuf32.p) HIPCHK(hipDeviceSynchronize());  // an earlier step may still read them
+      HIPCHK(L->wbuf32.ensure(host.size() * 4));
+      HIPCHK(hipMemcpy(L->wbuf32.p, host.data(), host.size() * 4, hipMemcpyHostToDevice));
+      for (int i = 0; i < 5; ++i)
+        if (!L->lin[i].quantized) L->sdev[i].w = static_cast<const float*>(L->wbuf32.p) + i * n;
+    }
+  }
+  L->stream_version = L->version;
   return MHSA_OK;
 }
 
@@ -976,10 +1022,9 @@ int32_t mhsa_stream_fill(const mhsa_stream* S, int32_t* out) {
 int32_t mhsa_stream_load_cache(mhsa_stream* S, const void* cache, const int32_t* filled, void* hs) {
   if (!S || !cache) return fail(MHSA_EINVAL, "null argument");
   mhsa_layer* L = S->layer;
-  if (L->dt != mhsa::kF32) return fail(MHSA_ENOTSUP, "streaming supports fp32 layers only");
   if (!aligned16(cache)) return fail(MHSA_EINVAL, "cache must be 16-byte aligned");
   hipStream_t s = static_cast<hipStream_t>(hs);
-  int32_t rc = prepare(L);
+  int32_t rc = prepare_stream(L);
   if (rc) return rc;
   const int D = L->D;
   S->head = 0;
@@ -996,50 +1041,61 @@ int32_t mhsa_stream_read_cache(const mhsa_stream* S, void* out, void* hs) {
   return MHSA_OK;
 }
 
-int32_t mhsa_forward_with_cache(mhsa_layer* L, mhsa_stream* S, const void* x, const void* pos_emb, int32_t pos_len,
-                                const mhsa_stream_mask* mask, void* out, void* hs) {
-  if (int32_t rc = check_layer(L)) return rc;
-  if (!S || S->layer != L) return fail(MHSA_EINVAL, "stream does not belong to this layer");
+}  // extern "C"
+
+namespace {
+
+// One cache-aware step (S != null: the chunk against the stream's ring) or
+// the no-cache form (S == null: keys and values from x alone,
+// attention.rs:687-700), both in fp32 (prepare_stream says why).
+int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, const void* pos_emb, int pos_len,
+                    const mhsa_stream_mask* mask, void* out, hipStream_t s) {
   if (!x || !pos_emb || !out) return fail(MHSA_EINVAL, "null tensor pointer");
   if (!aligned16(x) || !aligned16(pos_emb) || !aligned16(out))
     return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
-  if (L->dt != mhsa::kF32) return fail(MHSA_ENOTSUP, "streaming supports fp32 layers only");
-  hipStream_t s = static_cast<hipStream_t>(hs);
-  int32_t rc = prepare(L);
+  if (B <= 0 || T <= 0) return fail(MHSA_EINVAL, "batch and seq_len must be positive (got %d, %d)", B, T);
+  int32_t rc = prepare_stream(L);
   if (rc) return rc;
-  const int D = L->D, B = S->B, C = S->C, T = S->Tc, R = S->R, Lk = C + T;
+  const int D = L->D, C = S ? S->C : 0, R = S ? S->R : 0, Lk = C + T;
   const bool masked = mask && mask->present;
   const mhsa_context* ctx = masked ? &mask->ctx : nullptr;
   const DistRange dr = context_distances(ctx, C, T, Lk);
   int row0, nrows, center;
   if ((rc = plan_positions(pos_len, Lk, dr, row0, nrows, center))) return rc;
 
-  // memoised position projection, keyed by pos_len (attention.rs:749-761)
+  // memoised position projection, keyed by pos_len (attention.rs:749-761);
+  // a bf16 layer projects its bf16 table in bf16 and widens the result
   if (L->pmemo_len != pos_len) {
     HIPCHK(L->pmemo.ensure(align_up((int64_t)pos_len * D * 4, 256)));
     ProfScope ps(L, "gemm_pos", s);
-    if ((rc = run_gemm(L, L->dev[4], D, pos_emb, D, pos_len, L->pmemo.p, D, nullptr, 0, s))) return rc;
+    if (L->dt == mhsa::kBF16) {
+      HIPCHK(L->pmemo_bf16.ensure(align_up((int64_t)pos_len * D * 2, 256)));
+      if ((rc = run_gemm(L, mhsa::kBF16, L->dev[4], D, pos_emb, D, pos_len, L->pmemo_bf16.p, D, nullptr, 0, s)))
+        return rc;
+      HIPCHK(mhsa::widen_bf16(L->pmemo_bf16.p, static_cast<float*>(L->pmemo.p), (int64_t)pos_len * D, s));
+    } else if ((rc = run_gemm(L, mhsa::kF32, L->sdev[4], D, pos_emb, D, pos_len, L->pmemo.p, D, nullptr, 0, s))) {
+      return rc;
+    }
     L->pmemo_len = pos_len;
   }
-  if (S->kv_version != L->version && (rc = reproject_ring(L, S, s))) return rc;
+  if (S && S->kv_version != L->version && (rc = reproject_ring(L, S, s))) return rc;
   const int64_t M = (int64_t)B * T;
   const size_t qb = align_up(M * D * 4, 256);
-  HIPCHK(S->ws.ensure(2 * qb));
-  char* q = static_cast<char*>(S->ws.p);
-  char* cx = q + qb;
-  char* kv = static_cast<char*>(S->ring_kv.p);
-  const int slot = (S->head + C) % R;  // ring rows of this chunk
+  DevBuf& ws = S ? S->ws : L->uws;
+  HIPCHK(ws.ensure((S ? 2 : 4) * qb));
+  char* q = static_cast<char*>(ws.p);  // [M, D] (cached) or [M, 3D] q|k|v rows (no cache)
+  char* cx = q + (S ? 1 : 3) * qb;
+  const int slot = S ? (S->head + C) % R : 0;  // ring rows of this chunk
+  char* kv = S ? static_cast<char*>(S->ring_kv.p) : q + (size_t)D * 4;
 
-  // One launch when the layer holds the stacked [3D, D] weight: Q to `q`, K|V
-  // to the cache ring's rows of this chunk, and the chunk's input rows copied
-  // into the input ring by the workgroups of the first column tile.
+  // (the fused chunk launch's parameters; used when the shape allows it)
   mhsa::GemmParams fp;
-  if (L->qkv_fused) {
+  if (S && L->qkv_fused) {
     fp.A = x;
     fp.lda = D;
-    fp.W = L->dev[0].w;
-    fp.sb = L->dev[0].sb;
-    fp.bias = L->dev[0].bias;
+    fp.W = L->sdev[0].w;
+    fp.sb = L->sdev[0].sb;
+    fp.bias = L->sdev[0].bias;
     fp.C = q;
     fp.ldc = D;
     fp.C2 = kv;
@@ -1055,38 +1111,55 @@ int32_t mhsa_forward_with_cache(mhsa_layer* L, mhsa_stream* S, const void* x, co
     fp.ring_off = slot;
     fp.ring_len = R;
   }
-  const bool one_launch = L->qkv_fused && mhsa::gemm_split_fused_ok(mhsa::kF32, fp);
+  const bool one_launch = !S || (L->qkv_fused && mhsa::gemm_split_fused_ok(mhsa::kF32, fp));
   ProfScope ps_kv(L, one_launch ? "gemm_qkv" : "gemm_q", s);
-  if (one_launch) {
-    HIPCHK(mhsa::gemm(mhsa::kF32, L->dev[0].quantized, fp, s));
-  } else {
-    if ((rc = run_gemm(L, L->dev[0], D, x, D, (int)M, q, D, nullptr, 0, s))) return rc;
-    ps_kv.next("gemm_kv");
+  if (!S) {
     if (L->qkv_fused) {
-      if ((rc = run_gemm(L, L->dev[1], 2 * D, x, D, (int)M, kv, 2 * D, nullptr, 0, s, T, R, slot, R))) return rc;
+      if ((rc = run_gemm(L, mhsa::kF32, L->sdev[0], 3 * D, x, D, (int)M, q, 3 * D, nullptr, 0, s))) return rc;
     } else {
-      if ((rc = run_gemm(L, L->dev[1], D, x, D, (int)M, kv, 2 * D, nullptr, 0, s, T, R, slot, R))) return rc;
-      if ((rc = run_gemm(L, L->dev[2], D, x, D, (int)M, kv + (size_t)D * 4, 2 * D, nullptr, 0, s, T, R, slot, R)))
-        return rc;
+      for (int i = 0; i < 3; ++i)
+        if ((rc = run_gemm(L, mhsa::kF32, L->sdev[i], D, x, D, (int)M, q + (size_t)i * D * 4, 3 * D, nullptr, 0, s)))
+          return rc;
     }
-    ps_kv.next("ring_write");
-    HIPCHK(mhsa::ring_write(mhsa::kF32, x, S->ring_h.p, B, T, D, R, D, slot, s));
+  } else {
+    // One launch when the layer holds the stacked [3D, D] weight: Q to `q`,
+    // K|V to the cache ring's rows of this chunk, and the chunk's input rows
+    // copied into the input ring by the workgroups of the first column tile.
+    if (one_launch) {
+      HIPCHK(mhsa::gemm(mhsa::kF32, L->sdev[0].quantized, fp, s));
+    } else {
+      if ((rc = run_gemm(L, mhsa::kF32, L->sdev[0], D, x, D, (int)M, q, D, nullptr, 0, s))) return rc;
+      ps_kv.next("gemm_kv");
+      if (L->qkv_fused) {
+        if ((rc = run_gemm(L, mhsa::kF32, L->sdev[1], 2 * D, x, D, (int)M, kv, 2 * D, nullptr, 0, s, T, R, slot, R)))
+          return rc;
+      } else {
+        if ((rc = run_gemm(L, mhsa::kF32, L->sdev[1], D, x, D, (int)M, kv, 2 * D, nullptr, 0, s, T, R, slot, R)))
+          return rc;
+        if ((rc = run_gemm(L, mhsa::kF32, L->sdev[2], D, x, D, (int)M, kv + (size_t)D * 4, 2 * D, nullptr, 0, s, T,
+                           R, slot, R)))
+          return rc;
+      }
+      ps_kv.next("ring_write");
+      HIPCHK(mhsa::ring_write(mhsa::kF32, x, S->ring_h.p, B, T, D, R, D, slot, s));
+    }
   }
   ps_kv.next("attention");
 
   std::vector<int32_t> used(B);
   for (int b = 0; b < B; ++b)
-    used[b] = std::min(std::max(masked && mask->filled_host ? mask->filled_host[b] : S->fill[b], 0), C);
+    used[b] = std::min(std::max(masked && mask->filled_host ? mask->filled_host[b] : (S ? S->fill[b] : 0), 0), C);
   mhsa::AttnParams a;
   fill_attn_common(L, a);
+  a.scale_bd = a.scale;  // bd is an f32 array on this path: cast(s) is s (attention.rs:308-311)
   a.q = q;
-  a.q_bs = (int64_t)T * D;
-  a.q_rs = D;
+  a.q_bs = (int64_t)T * (S ? D : 3 * D);
+  a.q_rs = S ? D : 3 * D;
   a.k = kv;
   a.v = kv + (size_t)D * 4;
-  a.kv_bs = (int64_t)R * 2 * D;
-  a.kv_rs = 2 * D;
-  a.ring_head = S->head;
+  a.kv_bs = S ? (int64_t)R * 2 * D : (int64_t)T * 3 * D;
+  a.kv_rs = S ? 2 * D : 3 * D;
+  a.ring_head = S ? S->head : 0;
   a.ring_len = R;
   a.p = static_cast<char*>(L->pmemo.p) + (size_t)row0 * D * 4;
   a.p_rs = D;
@@ -1100,7 +1173,7 @@ int32_t mhsa_forward_with_cache(mhsa_layer* L, mhsa_stream* S, const void* x, co
   a.qoff = C;
   set_ctx(a, ctx);
   rc = run_attention(
-      L, a, B,
+      L, mhsa::kF32, a, B,
       [&](int b, int& lo, int& hi, int& qv) {
         lo = masked ? C - used[b] : 0;  // unfilled cache rows (conformer.rs:155-181)
         hi = Lk;
@@ -1109,11 +1182,30 @@ int32_t mhsa_forward_with_cache(mhsa_layer* L, mhsa_stream* S, const void* x, co
       s);
   if (rc) return rc;
   ps_kv.next("gemm_out");
-  if ((rc = run_gemm(L, L->dev[3], D, cx, D, (int)M, out, D, nullptr, 0, s))) return rc;
-  const int keep = std::max(T - L->cache_drop, 0);  // attention.rs:665
-  S->head = (S->head + keep) % R;
-  for (int b = 0; b < B; ++b) S->fill[b] = std::min(used[b] + keep, C);  // conformer.rs:1025-1036
+  if ((rc = run_gemm(L, mhsa::kF32, L->sdev[3], D, cx, D, (int)M, out, D, nullptr, 0, s))) return rc;
+  if (S) {
+    const int keep = std::max(T - L->cache_drop, 0);  // attention.rs:665
+    S->head = (S->head + keep) % R;
+    for (int b = 0; b < B; ++b) S->fill[b] = std::min(used[b] + keep, C);  // conformer.rs:1025-1036
+  }
   return MHSA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t mhsa_forward_with_cache(mhsa_layer* L, mhsa_stream* S, const void* x, const void* pos_emb, int32_t pos_len,
+                                const mhsa_stream_mask* mask, void* out, void* hs) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (!S || S->layer != L) return fail(MHSA_EINVAL, "stream does not belong to this layer");
+  return stream_step(L, S, x, S->B, S->Tc, pos_emb, pos_len, mask, out, static_cast<hipStream_t>(hs));
+}
+
+int32_t mhsa_forward_uncached(mhsa_layer* L, const void* x, int32_t batch, int32_t seq_len, const void* pos_emb,
+                              int32_t pos_len, const mhsa_stream_mask* mask, void* out, void* hs) {
+  if (int32_t rc = check_layer(L)) return rc;
+  return stream_step(L, nullptr, x, batch, seq_len, pos_emb, pos_len, mask, out, static_cast<hipStream_t>(hs));
 }
 
 int32_t mhsa_pos_encoding(int32_t d_model, int32_t max_len, int32_t seq_len, float* out) {
@@ -1189,7 +1281,7 @@ int32_t mhsa_debug_linear(mhsa_layer* L, int32_t which, const void* x, int32_t r
   int32_t rc = prepare(L);
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(hs);
-  if ((rc = run_gemm(L, L->dev[which], L->D, x, L->D, rows, out, L->D, nullptr, 0, s))) return rc;
+  if ((rc = run_gemm(L, L->dt, L->dev[which], L->D, x, L->D, rows, out, L->D, nullptr, 0, s))) return rc;
   HIPCHK(hipStreamSynchronize(s));
   return MHSA_OK;
 }

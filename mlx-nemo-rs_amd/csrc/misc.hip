@@ -178,7 +178,24 @@ __global__ void zero_kernel(u32x4* p, int64_t n16, uint8_t* tail, int ntail) {
   if (blockIdx.x == 0 && (int)threadIdx.x < ntail) tail[threadIdx.x] = 0;
 }
 
+__global__ void widen_kernel(const bf16x8* src, floatx4* dst, int64_t n8) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n8; i += (int64_t)gridDim.x * blockDim.x) {
+    const bf16x8 v = src[i];
+    dst[2 * i] = floatx4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+    dst[2 * i + 1] = floatx4{(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
+  }
+}
+
 }  // namespace
+
+hipError_t widen_bf16(const void* src, float* dst, int64_t n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  if (!src || !dst || n % 8 || ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15))
+    return hipErrorInvalidValue;
+  hipLaunchKernelGGL(widen_kernel, dim3(grid_for(n / 8)), dim3(256), 0, s, static_cast<const bf16x8*>(src),
+                     reinterpret_cast<floatx4*>(dst), n / 8);
+  return hipGetLastError();
+}
 
 hipError_t fill_zero(void* ptr, size_t bytes, hipStream_t s) {
   if (!bytes) return hipSuccess;

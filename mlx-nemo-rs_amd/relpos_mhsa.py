@@ -34,7 +34,8 @@ EXPORTS = (
     "mhsa_head_dim", "mhsa_n_heads", "mhsa_d_model", "mhsa_set_cache_drop_size", "mhsa_load_linear_standard",
     "mhsa_load_linear_quantized", "mhsa_load_pos_bias", "mhsa_load_weights", "mhsa_forward", "mhsa_forward_noalloc",
     "mhsa_sublayer_forward", "mhsa_stream_create", "mhsa_stream_destroy", "mhsa_stream_load_cache",
-    "mhsa_stream_read_cache", "mhsa_stream_fill", "mhsa_forward_with_cache", "mhsa_pos_encoding",
+    "mhsa_stream_read_cache", "mhsa_stream_fill", "mhsa_forward_with_cache", "mhsa_forward_uncached",
+    "mhsa_pos_encoding",
     "mhsa_debug_dequantize", "mhsa_debug_linear", "mhsa_debug_offline_mask", "mhsa_debug_stream_mask", "mhsa_debug_rel_shift_index",
     "mhsa_debug_position_scores", "mhsa_debug_top_keys", "mhsa_profile_enable", "mhsa_profile_reset", "mhsa_profile_count",
     "mhsa_profile_entry",
@@ -102,6 +103,7 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_stream_read_cache": (I, [VP, VP, VP]),
         "mhsa_stream_fill": (I, [VP, PI]),
         "mhsa_forward_with_cache": (I, [VP, VP, VP, VP, I, P(StreamMask), VP, VP]),
+        "mhsa_forward_uncached": (I, [VP, VP, I, I, VP, I, P(StreamMask), VP, VP]),
         "mhsa_pos_encoding": (I, [I, I, I, P(ctypes.c_float)]),
         "mhsa_debug_dequantize": (I, [VP, I, VP, VP]),
         "mhsa_debug_linear": (I, [VP, I, VP, I, VP, VP]),
@@ -403,11 +405,22 @@ class RelPositionMultiHeadAttention:
 
     # attention.rs:606-816, functional form: cache in, cache out
     def forward_with_cache(self, x, pos_emb, cache, cache_filled_len=0, att_mask: Optional[StreamingMask] = None):
-        """Returns (output, new_cache) like the reference; the cache is [B, C, D].
+        """Returns (output, new_cache) like the reference; the cache is [B, C, D]
+        or None (the no-cache path, attention.rs:687-700). x, the cache and the
+        output are fp32 for both layer dtypes; pos_emb is in the layer dtype.
         `att_mask` describes the mask (None = no mask); its `filled` defaults
         to `cache_filled_len` for every session."""
         import torch
         b, t, d = x.shape
+        if cache is None:
+            pe = pos_emb.reshape(-1, d)
+            self._check_stream_dev(x, pe)
+            out = torch.empty_like(x)
+            m, keep = (att_mask.c() if att_mask is not None else (None, []))
+            _check(self._lib.mhsa_forward_uncached(self._h, _dptr(x), b, t, _dptr(pe), pe.shape[0],
+                                                   ctypes.byref(m) if m is not None else None, _dptr(out),
+                                                   _stream_ptr()))
+            return out, x[:, :max(t - self._cache_drop_size, 0)].clone()
         c = cache.shape[1]
         st = self.stream(b, c, t)
         if att_mask is not None and att_mask.att_context_size is not None and att_mask.filled is None:
@@ -491,6 +504,15 @@ class RelPositionMultiHeadAttention:
                                              _dptr(top), _dptr(val), opt(q), opt(k), opt(p), _stream_ptr()))
         return (top, val, q, k, p) if with_inputs else (top, val)
 
+    def _check_stream_dev(self, x, pe, *more):
+        """Streaming tensors: x, caches and outputs fp32, pos_emb in the layer dtype."""
+        import torch
+        for t in (x,) + more:
+            if not t.is_cuda or t.dtype != torch.float32 or not t.is_contiguous():
+                raise MhsaError(MHSA_EINVAL, f"streaming activations are contiguous float32 GPU tensors, got "
+                                             f"{t.dtype} on {t.device}")
+        self._check_dev(pe)
+
     def _check_dev(self, *ts):
         want = self.dtype
         for t in ts:
@@ -517,7 +539,9 @@ class StreamState:
             self._h = None
 
     def load_cache(self, cache, filled: Optional[Sequence[int]] = None) -> None:
-        self.layer._check_dev(cache)
+        import torch
+        if not cache.is_cuda or cache.dtype != torch.float32 or not cache.is_contiguous():
+            raise MhsaError(MHSA_EINVAL, "the cache is a contiguous float32 GPU tensor")
         _check(self.layer._lib.mhsa_stream_load_cache(self._h, _dptr(cache), _int_array(filled), _stream_ptr()))
 
     def read_cache(self):
@@ -535,9 +559,9 @@ class StreamState:
         import torch
         b, t, d = x.shape
         pe = pos_emb.reshape(-1, d)
-        self.layer._check_dev(x, pe)
         if out is None:
             out = torch.empty_like(x)
+        self.layer._check_stream_dev(x, pe, out)
         m, keep = (mask.c() if mask is not None else (None, []))
         _check(self.layer._lib.mhsa_forward_with_cache(self.layer._h, self._h, _dptr(x), _dptr(pe), pe.shape[0],
                                                        ctypes.byref(m) if m is not None else None, _dptr(out),

@@ -219,14 +219,15 @@ def unpack_codes(w_u32: np.ndarray, bits: int = 8) -> np.ndarray:
 
 
 def dequantize(w_u32, scales, biases, bits: int = 8, group_size: int = 64,
-               dtype: str = F32) -> np.ndarray:
+               dtype: str = F32, store: Optional[str] = None) -> np.ndarray:
     """Affine dequantisation W[n,k] = s[n,k/g] * q[n,k] + b[n,k/g].
 
     quantization.rs:1-8 (layout), 100-111 (`cast`: in bf16 mode the f16
     scales and biases are cast to bf16 first), 147-155 (`quantized_matmul`).
     Evaluated in f32: the f32 product of an f16/bf16 scale and an 8-bit code is
     exact, so the f32 sum has a single rounding and is unique with or without
-    an fma. In bf16 mode the weight is then stored as bf16 (RNE).
+    an fma. In bf16 mode the weight is then stored as bf16 (RNE), unless
+    `store` is F32 (an f32 input promotes the op to f32, below).
     """
     codes = unpack_codes(np.asarray(w_u32, dtype=np.uint32), bits).astype(np.float32)
     s = np.asarray(scales, dtype=np.float32)
@@ -238,7 +239,7 @@ def dequantize(w_u32, scales, biases, bits: int = 8, group_size: int = 64,
     b_full = np.repeat(b, group_size, axis=1)
     w = (s_full * codes).astype(np.float32) + b_full  # f32 product (exact), f32 sum
     w = w.astype(np.float32)
-    if dtype == BF16:
+    if (store or dtype) == BF16:
         return bf16_round(w)
     return w.astype(np.float64)
 
@@ -272,6 +273,24 @@ class LinearLayer:
         y = _rnd(np.matmul(x, w.T), dtype)
         if self.bias is not None:
             y = _rnd(y + to_dtype(self.bias, dtype), dtype)
+        return y
+
+    def promoted_weight(self, dtype: str) -> np.ndarray:
+        """The weight an f32 input meets after `cast(dtype)`: MLX promotes the
+        op to f32, so a dense weight is its `dtype` value and a quantized one
+        s*q + b evaluated in f32 from the cast scales and biases, not rounded
+        to bf16 afterwards (quantization.rs:92-114, 147-155)."""
+        if self.is_quantized:
+            return dequantize(self.weight, self.scales, self.biases, self.bits, self.group_size, dtype, store=F32)
+        return to_dtype(self.weight, dtype)
+
+    def forward_promoted(self, x: np.ndarray, dtype: str = F32) -> np.ndarray:
+        """quantization.rs:126-162 on an f32 input with the parameters cast to
+        `dtype`: matmul and bias add promote to f32, so nothing is rounded to
+        bf16. Equal to `forward` when dtype is F32."""
+        y = np.matmul(x, self.promoted_weight(dtype).T)
+        if self.bias is not None:
+            y = y + to_dtype(self.bias, dtype)
         return y
 
 
@@ -443,12 +462,22 @@ def cache_update(cache: np.ndarray, x: np.ndarray, cache_drop_size: int) -> np.n
 
 def mhsa_forward_with_cache(p: MhsaParams, x: np.ndarray, pos_emb: np.ndarray,
                             cache: Optional[np.ndarray], att_mask=None,
-                            dtype: str = F32):
+                            dtype: str = F32, pos_rows: Optional[np.ndarray] = None):
     """Cache-aware streaming forward (attention.rs:606-816).
 
     `att_mask` is None, a bool array [B|1, T, L] (True = visible, the
     unfused path of 777-790 where a fully hidden row yields 0), or an additive
     float array (fused SDPA path, 791-792). Returns (out, new_cache).
+
+    x and the cache are f32 arrays, as the encoder streams them: its caches
+    stay f32 after `set_dtype` (conformer.rs:422-434) and the streamed
+    features are never cast (conformer.rs:845-849). With `dtype` = bf16 the
+    parameters are the bf16-cast ones, but every op that meets an f32
+    activation promotes to f32 (MLX type promotion), so only the position
+    rows -- a bf16 table through bf16 weights -- are rounded to bf16.
+
+    `pos_rows` [P, D], when given, replaces linear_pos(pos_emb): a checker
+    can then feed a kernel's own projected rows, pinned separately.
     """
     x = np.asarray(x, dtype=np.float64)
     pos_emb = np.asarray(pos_emb, dtype=np.float64)
@@ -463,16 +492,17 @@ def mhsa_forward_with_cache(p: MhsaParams, x: np.ndarray, pos_emb: np.ndarray,
         total = seq_len
         q_keep = max(seq_len - p.cache_drop_size, 0)
         new_cache = x[:, :q_keep, :]
-    q = _split_heads(p.linear_q.forward(x, dtype), h)  # 718
-    k = _split_heads(p.linear_k.forward(kv_in, dtype), h)  # 721
-    v = _split_heads(p.linear_v.forward(kv_in, dtype), h)  # 722
-    pp = _split_heads(p.linear_pos.forward(pos_emb, dtype), h)  # 749-761
+    q = _split_heads(p.linear_q.forward_promoted(x, dtype), h)  # 718
+    k = _split_heads(p.linear_k.forward_promoted(kv_in, dtype), h)  # 721
+    v = _split_heads(p.linear_v.forward_promoted(kv_in, dtype), h)  # 722
+    pe = p.linear_pos.forward(pos_emb, dtype) if pos_rows is None else np.asarray(pos_rows, np.float64)[None]
+    pp = _split_heads(pe, h)  # 749-761: the table is in `dtype`
     p_t = np.swapaxes(pp, -1, -2)
     bu = to_dtype(p.pos_bias_u, dtype).reshape(1, h, 1, dk)
     bv = to_dtype(p.pos_bias_v, dtype).reshape(1, h, 1, dk)
-    q_u = _rnd(q + bu, dtype)
-    q_v = _rnd(q + bv, dtype)
-    bd = _rnd(np.matmul(q_v, p_t), dtype)  # 770
+    q_u = q + bu  # f32
+    q_v = q + bv
+    bd = np.matmul(q_v, p_t)  # 770, f32
     bd = rel_shift(bd)[..., :total]  # 771-772
     if att_mask is not None:
         att_mask = np.asarray(att_mask)
@@ -483,12 +513,12 @@ def mhsa_forward_with_cache(p: MhsaParams, x: np.ndarray, pos_emb: np.ndarray,
         scores = np.where(m4, scores, NEG_INF)
         w = _softmax(scores)
         w = np.where(m4, w, 0.0)
-        ctx = _rnd(np.matmul(w, v), dtype)
+        ctx = np.matmul(w, v)
     elif att_mask is not None:
-        ctx = attend(q_u, k, v, bd, m4, dk, dtype)
+        ctx = attend(q_u, k, v, bd, m4, dk, F32)  # cast(s) to bd's dtype, f32
     else:
-        ctx = attend(q_u, k, v, bd, None, dk, dtype)
-    out = p.linear_out.forward(_merge_heads(ctx), dtype)  # 795-807
+        ctx = attend(q_u, k, v, bd, None, dk, F32)
+    out = p.linear_out.forward_promoted(_merge_heads(ctx), dtype)  # 795-807
     return out, new_cache
 
 

@@ -560,6 +560,98 @@ def test_streaming_long_context_ring_wraps(B, C, T, ctx):
     assert np.array_equal(st.read_cache().cpu().numpy(), np.concatenate(caches, 0).astype(np.float32))
 
 
+def test_streaming_bf16_layer_xl_shape():
+    """A bf16 layer streamed as the encoder streams it: f32 cache and chunk,
+    so the arithmetic is f32 on the bf16-cast parameters, with bf16 position
+    rows (conformer.rs:422-434, 845-849). 16 sessions, 14-frame chunks
+    against the 70-frame cache, [70,13] chunked_limited, per-session fills,
+    12 steps against the oracle's bf16 streaming (fp32 bound) and the cache
+    read back bit-equal.
+
+    The position rows are a bf16 matmul: the GPU rounds its fp32 sum, the
+    oracle the exact one, so an element whose exact value lies within fp32
+    accumulation noise of a bf16 rounding boundary may land on the other
+    neighbour. They are checked for exactly that, and the oracle then runs on
+    the GPU's rows, which keeps the comparison at the fp32 bound."""
+    cfg = W.CONFIGS["xl_stream_f32"]
+    layers, _, ex = W.instantiate(cfg)
+    B, C, T, D = cfg.batch, cfg.cache_size, cfg.seq_len, cfg.d_model
+    w = dict(layers[0])
+    rng = np.random.default_rng(17)
+    for name in ("linear_q", "linear_k", "linear_v", "linear_out"):
+        w[f"{name}.bias"] = rng.normal(0, 0.1, D).astype(np.float32)
+    p = oracle_params(w, D, cfg.n_heads)
+    pos = O.bf16_round(O.RelPositionalEncoding(D, 5000, True).get_encoding(C + T))
+    layer = gpu_layer(w, D, cfg.n_heads, True, O.BF16)
+    st = layer.stream(B, C, T)
+    st.load_cache(dev(ex["cache"], O.F32), ex["fills"])
+    pos_d = dev(pos, O.BF16)
+    P_gpu = host(layer.debug_linear("linear_pos", pos_d))[0]
+    exact = pos[0] @ p.linear_pos.dense_weight(O.BF16).T
+    acc = np.abs(pos[0]) @ np.abs(p.linear_pos.dense_weight(O.BF16)).T * 2.0 ** -20
+    _, e = np.frexp(np.abs(exact))
+    near = np.abs(np.abs(exact) - np.abs(O.bf16_round(exact))) >= np.ldexp(0.5, e - 8) - acc
+    d = P_gpu != O.bf16_round(exact)
+    assert not (d & ~near).any()
+    _, eg = np.frexp(np.maximum(np.abs(P_gpu), np.abs(exact)))
+    assert np.all(np.abs(P_gpu - exact) <= np.ldexp(1.0, eg - 8) + acc)  # one ulp + fp32 accumulation
+    caches = [ex["cache"][b:b + 1].astype(np.float64) for b in range(B)]
+    fills = list(ex["fills"])
+    worst = 0.0
+    for step in range(12):
+        x = ex["chunks"][step]
+        got = host(st.step(dev(x, O.F32), pos_d, M.StreamingMask((70, 13), "chunked_limited")))
+        for b in range(B):
+            mask = O.streaming_mask((70, 13), "chunked_limited", C, fills[b], T, T)
+            ref, caches[b] = O.mhsa_forward_with_cache(p, x[b:b + 1], pos, caches[b], mask, dtype=O.BF16,
+                                                       pos_rows=P_gpu)
+            e = row_rel_err(got[b:b + 1], ref)
+            worst = max(worst, e)
+            assert e < F32_TOL, (step, b, e)
+            fills[b] = O.next_fill(fills[b], T, 0, C)
+    print(f"bf16 streaming worst per-row relative error {worst:.3e}")
+    assert np.array_equal(st.read_cache().cpu().numpy(), np.concatenate(caches, 0).astype(np.float32))
+
+
+@pytest.mark.parametrize("dtype", [O.F32, O.BF16])
+@pytest.mark.parametrize("quant", [False, True])
+def test_forward_without_cache(dtype, quant):
+    """forward_with_cache with no cache (attention.rs:687-700): keys and
+    values from the chunk alone, under a chunked_limited mask whose rows past
+    the valid length are blank (the bool path: they give the output bias),
+    in both layer dtypes and both projection kinds. The functional form also
+    returns the reference's new cache x[:, :T - cache_drop_size]."""
+    rng = np.random.default_rng(18)
+    d, h, B, T = 256, 2, 3, 37
+    if quant:
+        w = W.make_layer_weights(rng, d, h, True, True, centred=True)
+        for name in ("linear_q", "linear_k", "linear_v", "linear_out", "linear_pos"):
+            sc = rng.uniform(1e-4, 1e-3, size=w[f"{name}.scales"].shape)
+            w[f"{name}.scales"] = sc.astype(np.float16)
+            w[f"{name}.biases"] = (-128.0 * w[f"{name}.scales"].astype(np.float64)).astype(np.float16)
+            if name != "linear_pos":
+                w[f"{name}.bias"] = rng.normal(0, 0.1, d).astype(np.float16)
+    else:
+        w = random_weights(rng, d, h, use_bias=True, scale=0.05)
+    p = oracle_params(w, d, h, cache_drop_size=2)
+    layer = gpu_layer(w, d, h, True, dtype)
+    layer.cache_drop_size = 2
+    x = rng.standard_normal((B, T, d)).astype(np.float32)
+    pos = O.RelPositionalEncoding(d, 5000, False).get_encoding(T)
+    pos = pos if dtype == O.F32 else O.bf16_round(pos)
+    valid = 30
+    out, nc = layer.forward_with_cache(dev(x, O.F32), dev(pos, dtype), None, 0,
+                                       M.StreamingMask((12, 5), "chunked_limited", [0] * B, [valid] * B))
+    mask = O.streaming_mask((12, 5), "chunked_limited", 0, 0, T, valid)
+    assert mask.dtype == np.bool_
+    ref, ref_nc = O.mhsa_forward_with_cache(p, x, pos, None, mask, dtype=dtype)
+    got = host(out)
+    assert row_rel_err(got, ref) < F32_TOL
+    bias = O.to_dtype(np.asarray(w["linear_out.bias"], dtype=np.float64), dtype)
+    assert np.allclose(got[:, valid:], bias[None, None, :], atol=1e-6)
+    assert np.array_equal(host(nc), ref_nc)
+
+
 def test_streaming_rows_past_valid_give_output_bias():
     rng = np.random.default_rng(8)
     w = random_weights(rng, 128, 2, use_bias=True, scale=0.08)
@@ -614,9 +706,10 @@ def test_streaming_equals_offline_last_rows():
     assert row_rel_err(got, full[:, C:]) < 1e-5
 
 
+@pytest.mark.parametrize("dtype", [O.F32, O.BF16])
 @pytest.mark.parametrize("d_model,n_heads,kind", [(256, 4, "u8"), (256, 4, "mixed"), (1280, 10, "u8"),
                                                   (512, 8, "dense")])
-def test_streaming_projection_kinds_with_biases(d_model, n_heads, kind):
+def test_streaming_projection_kinds_with_biases(d_model, n_heads, kind, dtype):
     """Cache-aware steps with q/k/v/out biases and u8, dense or mixed q/k/v.
     Same-kind q/k/v with D <= 1024 take one launch for the chunk's Q, its K|V
     rows of the cache ring and its copy into the input ring; mixed kinds and
@@ -641,18 +734,19 @@ def test_streaming_projection_kinds_with_biases(d_model, n_heads, kind):
     B, C, T = 3, 70, 14
     cache = rng.standard_normal((B, C, d_model)).astype(np.float32)
     pos = O.RelPositionalEncoding(d_model, 5000, False).get_encoding(C + T)
-    layer = gpu_layer(w, d_model, n_heads, True, O.F32)
+    pos = pos if dtype == O.F32 else O.bf16_round(pos)
+    layer = gpu_layer(w, d_model, n_heads, True, dtype)
     st = layer.stream(B, C, T)
     fills = [70, 23, 0]
     st.load_cache(dev(cache, O.F32), fills)
-    pos_d = dev(pos, O.F32)
+    pos_d = dev(pos, dtype)
     caches = [cache[b:b + 1].astype(np.float64) for b in range(B)]
     for step in range(4):
         x = rng.standard_normal((B, T, d_model)).astype(np.float32)
         got = host(st.step(dev(x, O.F32), pos_d, M.StreamingMask((70, 13), "chunked_limited")))
         for b in range(B):
             mask = O.streaming_mask((70, 13), "chunked_limited", C, fills[b], T, T)
-            ref, _ = O.mhsa_forward_with_cache(p, x[b:b + 1], pos, caches[b], mask)
+            ref, _ = O.mhsa_forward_with_cache(p, x[b:b + 1], pos, caches[b], mask, dtype=dtype)
             assert row_rel_err(got[b:b + 1], ref) < F32_TOL, (step, b)
             caches[b] = O.cache_update(caches[b], x[b:b + 1].astype(np.float64), 0)
             fills[b] = O.next_fill(fills[b], T, 0, C)

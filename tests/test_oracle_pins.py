@@ -48,7 +48,7 @@ def random_params(d_model, n_heads, seed, use_bias=True, scale=0.3):
     )
 
 
-def direct_attention(p, x_q, kv_in, pos_emb, cache_len, visible, scale=None, scale_bd=None):
+def direct_attention(p, x_q, kv_in, pos_emb, cache_len, visible, scale=None, scale_bd=None, P=None):
     """Rel-pos attention from its definition, one (query, key) pair at a time.
 
     Query row i sits at absolute frame cache_len + i; key j at frame j. The
@@ -61,7 +61,7 @@ def direct_attention(p, x_q, kv_in, pos_emb, cache_len, visible, scale=None, sca
     q = p.linear_q.forward(x_q)
     k = p.linear_k.forward(kv_in)
     v = p.linear_v.forward(kv_in)
-    P = p.linear_pos.forward(pos_emb[0])
+    P = p.linear_pos.forward(pos_emb[0]) if P is None else P
     s = O.f32_scale(dk) if scale is None else scale
     sb = s if scale_bd is None else scale_bd
     B, T, _ = x_q.shape
@@ -565,6 +565,51 @@ def test_streaming_forward_matches_definition(kind):
     ref = direct_attention(p, x, np.concatenate([cache, x], 1), pos, C, vis, scale=scale)
     assert np.max(np.abs(out - ref)) < 1e-10
     assert (nc == np.concatenate([cache[:, T:], x], 1)).all()
+
+
+@pytest.mark.parametrize("quantized", [False, True])
+def test_streaming_bf16_is_f32_math_on_bf16_parameters(quantized):
+    """bf16 streaming (f32 cache and chunk, attention.rs:606-816 under MLX
+    promotion): equals the definition evaluated in float64 on the cast
+    parameters -- dense weights, biases and pos biases rounded to bf16,
+    quantized weights dequantised in f32 from bf16-rounded scales and biases
+    (the already pinned f32 dequantisation of pre-rounded inputs) -- with the
+    position rows the bf16 projection of the bf16 table (pinned by the
+    native-bf16 restatement), and the position term scaled by the f32 scale."""
+    d, h, C, T = 128, 2, 6, 3
+    rng = np.random.default_rng(21)
+    if quantized:
+        import workloads as W
+        from _util import oracle_params
+        w = W.make_layer_weights(rng, d, h, True, True)
+        for name in ("linear_q", "linear_k", "linear_v", "linear_out"):
+            w[f"{name}.bias"] = rng.normal(0, 0.1, d).astype(np.float16)
+        p = oracle_params(w, d, h)
+    else:
+        p = random_params(d, h, seed=22, scale=0.1)
+    x = rng.standard_normal((2, T, d)).astype(np.float32).astype(np.float64)
+    cache = rng.standard_normal((2, C, d)).astype(np.float32).astype(np.float64)
+    pos = O.bf16_round(O.RelPositionalEncoding(d, 64, False).get_encoding(C + T))
+    out, _ = O.mhsa_forward_with_cache(p, x, pos, cache, None, dtype=O.BF16)
+
+    def cast(lin):
+        if lin.is_quantized:
+            s16 = O.bf16_round(np.asarray(lin.scales, dtype=np.float32))
+            b16 = O.bf16_round(np.asarray(lin.biases, dtype=np.float32))
+            wt = O.dequantize(lin.weight, s16, b16, lin.bits, lin.group_size, O.F32)
+        else:
+            wt = O.bf16_round(lin.weight)
+        return O.LinearLayer(wt, None if lin.bias is None else O.bf16_round(lin.bias))
+
+    pc = O.MhsaParams(d, h, cast(p.linear_q), cast(p.linear_k), cast(p.linear_v), cast(p.linear_out),
+                      cast(p.linear_pos), O.bf16_round(p.pos_bias_u), O.bf16_round(p.pos_bias_v))
+    P = p.linear_pos.forward(pos[0], O.BF16)
+    vis = np.ones((2, T, C + T), dtype=bool)
+    ref = direct_attention(pc, x, np.concatenate([cache, x], 1), pos, C, vis, P=P)
+    assert np.max(np.abs(out - ref)) < 1e-9 * np.max(np.abs(ref))
+    # and it is not the all-bf16 arithmetic of the offline bf16 forward
+    rounded = O.bf16_round(ref)
+    assert np.max(np.abs(out - rounded)) > 0
 
 
 def test_streaming_chunk_equals_offline_rows():
