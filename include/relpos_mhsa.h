@@ -255,6 +255,11 @@ int32_t mhsa_pos_encoding(int32_t d_model, int32_t max_len, int32_t seq_len, flo
  * per kernel tag (gemm_qkv, gemm_pos, attention, gemm_out, layer_norm,
  * gemm_q, gemm_kv, ring_write). Reading waits for the recorded events. */
 int32_t mhsa_profile_enable(mhsa_layer* layer, int32_t enable);
+/* While profiling is enabled, issue every launch tagged `tag` n times inside
+ * its event pair (it then counts as n launches), so the event overhead is
+ * spread over n back-to-back launches. For timing only: an in-place output
+ * (the sublayer's residual add) is applied n times. n = 1 turns it off. */
+int32_t mhsa_profile_repeat(mhsa_layer* layer, const char* tag, int32_t n);
 int32_t mhsa_profile_reset(mhsa_layer* layer);
 /* Number of distinct tags recorded so far (flushes pending events). */
 int32_t mhsa_profile_count(mhsa_layer* layer);

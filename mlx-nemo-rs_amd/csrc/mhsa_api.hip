@@ -126,9 +126,14 @@ int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 // Per-kernel HIP-event timing on the launch stream (off unless enabled).
 struct Profiler {
   bool on = false;
+  // while on: launches tagged repeat_tag are issued repeat_n times inside
+  // one event pair, which spreads the event overhead over repeat_n launches
+  std::string repeat_tag;
+  int repeat_n = 1;
   struct Pair {
     hipEvent_t a = nullptr, b = nullptr;
     std::string tag;
+    int n = 1;
   };
   std::vector<Pair> pool;
   size_t used = 0;
@@ -151,9 +156,12 @@ struct Profiler {
     }
     Pair& p = pool[used];
     p.tag = tag;
+    p.n = reps(tag);
     if (hipEventRecord(p.a, s) != hipSuccess) return -1;
     return (int)used++;
   }
+  // How many times the launches tagged `tag` are issued.
+  int reps(const char* tag) const { return on && repeat_n > 1 && repeat_tag == tag ? repeat_n : 1; }
   void end(int idx, hipStream_t s) {
     if (idx >= 0) (void)hipEventRecord(pool[idx].b, s);
   }
@@ -171,7 +179,7 @@ struct Profiler {
         count.push_back(0);
       }
       ms[k] += t;
-      count[k] += 1;
+      count[k] += pool[i].n;
     }
     used = 0;
   }
@@ -603,13 +611,15 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
 
   {
     ProfScope ps(L, "gemm_qkv", s, prof);
-    if ((rc = project_qkv(L, x, (int)M, qkv, 3 * D, s, use_vt ? &vt : nullptr))) return rc;
+    for (int r = prof ? L->prof.reps("gemm_qkv") : 1; r > 0; --r)
+      if ((rc = project_qkv(L, x, (int)M, qkv, 3 * D, s, use_vt ? &vt : nullptr))) return rc;
   }
   {
     ProfScope ps(L, "gemm_pos", s, prof);
-    if ((rc = run_gemm(L, L->dt, L->dev[4], D, static_cast<const char*>(pos_emb) + (size_t)row0 * D * es, D, nrows, P, D,
-                       nullptr, 0, s)))
-      return rc;
+    for (int r = prof ? L->prof.reps("gemm_pos") : 1; r > 0; --r)
+      if ((rc = run_gemm(L, L->dt, L->dev[4], D, static_cast<const char*>(pos_emb) + (size_t)row0 * D * es, D, nrows,
+                         P, D, nullptr, 0, s)))
+        return rc;
   }
 
   a.q = qkv;
@@ -634,12 +644,15 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   }
   {
     ProfScope ps(L, "attention", s, prof);
-    rc = run_attention(L, L->dt, a, B, key_bounds, s);
+    for (int r = prof ? L->prof.reps("attention") : 1; r > 0 && !rc; --r)
+      rc = run_attention(L, L->dt, a, B, key_bounds, s);
   }
   if (rc) return rc;
   if (!out) return MHSA_OK;
   ProfScope ps(L, "gemm_out", s, prof);
-  return run_gemm(L, L->dt, L->dev[3], D, cx, D, (int)M, out, D, residual, D, s);
+  for (int r = prof ? L->prof.reps("gemm_out") : 1; r > 0 && !rc; --r)
+    rc = run_gemm(L, L->dt, L->dev[3], D, cx, D, (int)M, out, D, residual, D, s);
+  return rc;
 }
 
 // ---- allocation-free forward ---------------------------------------------
@@ -978,7 +991,8 @@ int32_t mhsa_sublayer_forward(mhsa_layer* L, void* x, int32_t batch, int32_t seq
   HIPCHK(L->hbuf.ensure(align_up(M * D * esz(L), 256)));
   {
     ProfScope ps(L, "layer_norm", s);
-    HIPCHK(mhsa::layer_norm(dtype_of(L), x, L->hbuf.p, gd, bd, eps, (int)M, D, s));
+    for (int r = L->prof.reps("layer_norm"); r > 0; --r)
+      HIPCHK(mhsa::layer_norm(dtype_of(L), x, L->hbuf.p, gd, bd, eps, (int)M, D, s));
   }
   return forward_impl(L, L->hbuf.p, batch, seq_len, pos_emb, pos_len, ctx, lens, x, x, AttnDebug(), s);
 }
@@ -1126,7 +1140,7 @@ int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, 
     // K|V to the cache ring's rows of this chunk, and the chunk's input rows
     // copied into the input ring by the workgroups of the first column tile.
     if (one_launch) {
-      HIPCHK(mhsa::gemm(mhsa::kF32, L->sdev[0].quantized, fp, s));
+      for (int r = L->prof.reps("gemm_qkv"); r > 0; --r) HIPCHK(mhsa::gemm(mhsa::kF32, L->sdev[0].quantized, fp, s));
     } else {
       if ((rc = run_gemm(L, mhsa::kF32, L->sdev[0], D, x, D, (int)M, q, D, nullptr, 0, s))) return rc;
       ps_kv.next("gemm_kv");
@@ -1172,17 +1186,20 @@ int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, 
   a.L = Lk;
   a.qoff = C;
   set_ctx(a, ctx);
-  rc = run_attention(
-      L, mhsa::kF32, a, B,
-      [&](int b, int& lo, int& hi, int& qv) {
-        lo = masked ? C - used[b] : 0;  // unfilled cache rows (conformer.rs:155-181)
-        hi = Lk;
-        qv = masked && mask->valid_host ? std::min(std::max(mask->valid_host[b], 0), T) : T;
-      },
-      s);
+  for (int r = L->prof.reps("attention"); r > 0 && !rc; --r)
+    rc = run_attention(
+        L, mhsa::kF32, a, B,
+        [&](int b, int& lo, int& hi, int& qv) {
+          lo = masked ? C - used[b] : 0;  // unfilled cache rows (conformer.rs:155-181)
+          hi = Lk;
+          qv = masked && mask->valid_host ? std::min(std::max(mask->valid_host[b], 0), T) : T;
+        },
+        s);
   if (rc) return rc;
   ps_kv.next("gemm_out");
-  if ((rc = run_gemm(L, mhsa::kF32, L->sdev[3], D, cx, D, (int)M, out, D, nullptr, 0, s))) return rc;
+  for (int r = L->prof.reps("gemm_out"); r > 0 && !rc; --r)
+    rc = run_gemm(L, mhsa::kF32, L->sdev[3], D, cx, D, (int)M, out, D, nullptr, 0, s);
+  if (rc) return rc;
   if (S) {
     const int keep = std::max(T - L->cache_drop, 0);  // attention.rs:665
     S->head = (S->head + keep) % R;
@@ -1233,6 +1250,14 @@ int32_t mhsa_profile_enable(mhsa_layer* L, int32_t enable) {
   if (int32_t rc = check_layer(L)) return rc;
   L->prof.flush();
   L->prof.on = enable != 0;
+  return MHSA_OK;
+}
+
+int32_t mhsa_profile_repeat(mhsa_layer* L, const char* tag, int32_t n) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (n < 1 || (n > 1 && !tag)) return fail(MHSA_EINVAL, "repeat count must be >= 1 (with a tag)");
+  L->prof.repeat_tag = tag ? tag : "";
+  L->prof.repeat_n = n;
   return MHSA_OK;
 }
 

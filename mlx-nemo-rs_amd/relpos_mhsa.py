@@ -37,7 +37,8 @@ EXPORTS = (
     "mhsa_stream_read_cache", "mhsa_stream_fill", "mhsa_forward_with_cache", "mhsa_forward_uncached",
     "mhsa_pos_encoding",
     "mhsa_debug_dequantize", "mhsa_debug_linear", "mhsa_debug_offline_mask", "mhsa_debug_stream_mask", "mhsa_debug_rel_shift_index",
-    "mhsa_debug_position_scores", "mhsa_debug_top_keys", "mhsa_profile_enable", "mhsa_profile_reset", "mhsa_profile_count",
+    "mhsa_debug_position_scores", "mhsa_debug_top_keys", "mhsa_profile_enable", "mhsa_profile_repeat",
+    "mhsa_profile_reset", "mhsa_profile_count",
     "mhsa_profile_entry",
 )
 
@@ -113,6 +114,7 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_debug_position_scores": (I, [VP, VP, I, I, VP, I, VP, VP, VP, VP]),
         "mhsa_debug_top_keys": (I, [VP, VP, I, I, VP, I, P(Context), PI, VP, VP, VP, VP, VP, VP]),
         "mhsa_profile_enable": (I, [VP, I]),
+        "mhsa_profile_repeat": (I, [VP, ctypes.c_char_p, I]),
         "mhsa_profile_reset": (I, [VP]),
         "mhsa_profile_count": (I, [VP]),
         "mhsa_profile_entry": (I, [VP, I, P(ctypes.c_char_p), P(ctypes.c_double), PI]),
@@ -442,6 +444,10 @@ class RelPositionMultiHeadAttention:
     # per-kernel HIP-event timing (no counterpart in the reference)
     def profile(self, enable: bool = True) -> None:
         _check(self._lib.mhsa_profile_enable(self._h, 1 if enable else 0))
+
+    def profile_repeat(self, tag: Optional[str], n: int = 1) -> None:
+        """Issue launches tagged `tag` n times per event pair while profiling."""
+        _check(self._lib.mhsa_profile_repeat(self._h, tag.encode() if tag else None, int(n)))
 
     def profile_reset(self) -> None:
         _check(self._lib.mhsa_profile_reset(self._h))

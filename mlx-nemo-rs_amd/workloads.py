@@ -1,6 +1,6 @@
 """Synthetic workloads for the rel-pos MHSA path (host-side numpy generators).
 
-Five configurations of the FastConformer attention sublayer:
+Six configurations of the FastConformer attention sublayer:
 
 * ``large_f32``       D=512, H=8, B=1, T=125, fp32, no padding, full context
                       (FastConformer-large, 10 s of audio), seed 0
@@ -11,6 +11,9 @@ Five configurations of the FastConformer attention sublayer:
                       U{0..70}, 50 steps, fp32, seed 2
 * ``xl_local_bf16``   D=1024, H=8, B=2, T=7500, bf16, regular (128, 128)
                       window with a 257-row banded position table, seed 3
+* ``xl_stream_f32_24l`` the same streaming step through 24 distinct layers
+                      (own weights and cache each, ~680 MB, beyond the 256 MB
+                      Infinity Cache), seed 2
 * ``xl_stack_u8``     24 sublayers x <- x + MHSA(LN(x)) with affine u8
                       projections (group 64, f16 scales U(0.002, 0.02), f16
                       biases N(0, 0.01), codes U{0..255}), B=4, T=1500, bf16,
@@ -98,6 +101,8 @@ CONFIGS: Dict[str, Workload] = {
     "xl_offline_bf16": Workload("xl_offline_bf16", 1024, 8, 8, 375, "bfloat16", seed=1),
     "xl_stream_f32": Workload("xl_stream_f32", 1024, 8, 16, 14, "float32", seed=2,
                               context=(70, 13, "chunked_limited"), cache_size=70, steps=50),
+    "xl_stream_f32_24l": Workload("xl_stream_f32_24l", 1024, 8, 16, 14, "float32", seed=2,
+                                  context=(70, 13, "chunked_limited"), cache_size=70, steps=50, layers=24),
     "xl_local_bf16": Workload("xl_local_bf16", 1024, 8, 2, 7500, "bfloat16", seed=3,
                               context=(128, 128, "regular"), pos_band=257),
     "xl_stack_u8": Workload("xl_stack_u8", 1024, 8, 4, 1500, "bfloat16", seed=4, quantized=True, layers=24),
@@ -131,11 +136,13 @@ def instantiate(cfg: Workload, centred: bool = False):
 def algorithmic_flops(cfg: Workload, lengths=None, fills=None) -> float:
     """Useful MFMA work of one pass: the projections plus 2*D FLOPs per
     (query, visible key) pair for each of QK^T, the surviving part of QP^T
-    and PV. Padded queries count, padded keys and masked pairs do not."""
+    and PV. Padded queries count, padded keys and masked pairs do not.
+    Streaming: one step with projected K/V cached, `fills` the per-session
+    cache fill levels that step reads."""
     D, T, B = cfg.d_model, cfg.seq_len, cfg.batch
-    if cfg.cache_size:  # one streaming step with projected K/V cached
+    if cfg.cache_size:
         pairs = sum(T * (T + f) for f in (fills or [cfg.cache_size] * B))
-        return 2.0 * D * D * (3 * B * T) + 6.0 * D * pairs
+        return cfg.layers * (2.0 * D * D * (4 * B * T) + 6.0 * D * pairs)
     lens = lengths or [T] * B
     if cfg.context is not None and cfg.context[2] == "regular":
         left, right = cfg.context[0], cfg.context[1]
@@ -150,6 +157,16 @@ def algorithmic_flops(cfg: Workload, lengths=None, fills=None) -> float:
         pairs = sum(T * ln for ln in lens)
         pos_rows = 2 * T - 1
     return cfg.layers * (2.0 * D * D * (4 * B * T + pos_rows) + 6.0 * D * pairs)
+
+
+def chunk_attention_bytes(cfg: Workload, fills) -> float:
+    """Algorithmic HBM bytes of one streaming chunk-attention launch (fp32):
+    the chunk's q, the visible cached and new K/V rows, the position rows the
+    step reaches and the output."""
+    D, T, B, C = cfg.d_model, cfg.seq_len, cfg.batch, cfg.cache_size
+    band = 2 * (C + T) - 1
+    vis = sum(T + f for f in fills)
+    return 4.0 * (2 * B * T * D + 2 * vis * D + band * D)
 
 
 def algorithmic_bytes(cfg: Workload) -> float:
