@@ -149,6 +149,37 @@ int32_t mhsa_load_pos_bias(mhsa_layer* layer, int32_t data_dtype, const void* po
 int32_t mhsa_load_weights(mhsa_layer* layer, const mhsa_tensor* tensors, int32_t n_tensors, const char* prefix,
                           int32_t strict, int32_t quant_bits, int32_t quant_group);
 
+/* ---- checkpoints ---------------------------------------------------------- */
+
+/* CheckpointLoader (checkpoint.rs:480-760) over an MLX safetensors file:
+ * `path` is the .safetensors file or a directory holding model.safetensors,
+ * weights.safetensors, model_weights.safetensors or weights/model.safetensors
+ * (checkpoint.rs:694-731). The quantization comes from the directory's
+ * config.yaml / model_config.yaml / config.json / model_config.json, else
+ * config.json ("quantization": {"bits", "group_size"}, defaults 8 and 64,
+ * checkpoint.rs:535-572, 613-621); for a file path, from config.json beside
+ * it. The file is memory-mapped; tensors of dtype F32, F16, BF16 and U32 are
+ * listed (the dtypes the path reads), others are skipped. */
+typedef struct mhsa_checkpoint mhsa_checkpoint;
+int32_t mhsa_checkpoint_open(const char* path, mhsa_checkpoint** out);
+void mhsa_checkpoint_close(mhsa_checkpoint* ckpt);
+/* quantization() (checkpoint.rs:682-690): bits and group size, 0 and 0 when
+ * the checkpoint is not quantized. */
+int32_t mhsa_checkpoint_quantization(const mhsa_checkpoint* ckpt, int32_t* bits, int32_t* group_size);
+/* The tensor map (Array::load_safetensors, weights.rs:207-237): count, and
+ * entry idx with its name, dtype, shape and a host pointer into the mapping
+ * (valid until mhsa_checkpoint_close). */
+int32_t mhsa_checkpoint_count(const mhsa_checkpoint* ckpt);
+int32_t mhsa_checkpoint_tensor(const mhsa_checkpoint* ckpt, int32_t idx, mhsa_tensor* out);
+/* __metadata__ value for `key` (NULL when absent), e.g. "format" = "mlx"
+ * (WeightFormat::from_safetensors_metadata, weights.rs:27-35). */
+int32_t mhsa_checkpoint_metadata(const mhsa_checkpoint* ckpt, const char* key, const char** value);
+/* load_weights(&weights, prefix, quant) (attention.rs:863-893) from the
+ * checkpoint's tensors with its quantization: mhsa_load_weights over the
+ * mapped tensors. */
+int32_t mhsa_load_weights_from_checkpoint(mhsa_layer* layer, const mhsa_checkpoint* ckpt, const char* prefix,
+                                          int32_t strict);
+
 /* ---- offline forward ---------------------------------------------------- */
 
 /* forward(x, pos_emb, context, key_mask) (attention.rs:446-573).

@@ -21,6 +21,7 @@
 #include <vector>
 
 #include "../../include/relpos_mhsa.h"
+#include "host_error.hpp"
 #include "kernels.hpp"
 
 using mhsa::DType;
@@ -186,6 +187,11 @@ struct Profiler {
 };
 
 }  // namespace
+
+int32_t mhsa::set_error(int32_t code, const char* msg) {
+  g_err = msg ? msg : "";
+  return code;
+}
 
 struct mhsa_layer {
   int D = 0, H = 0, dk = 0;
@@ -883,6 +889,9 @@ int32_t mhsa_load_weights(mhsa_layer* L, const mhsa_tensor* tensors, int32_t n, 
     const mhsa_tensor* qb = find(p + ".biases");
     const mhsa_tensor* b = find(p + ".bias");
     if (w && sc && qb) {  // quantization.rs:299-304
+      if (bits != 8 || group != 64)
+        return fail(MHSA_ENOTSUP, "`%s`: quantization bits=%d group_size=%d not supported (8, 64)", p.c_str(), bits,
+                    group);
       if (w->dtype != MHSA_U32 || sc->dtype != MHSA_F16 || qb->dtype != MHSA_F16)
         return fail(MHSA_EINVAL, "`%s`: quantized tensors must be u32 weight and f16 scales/biases", p.c_str());
       if (numel(w) != (int64_t)D * D * bits / 32 || numel(sc) != (int64_t)D * D / group || numel(qb) != numel(sc))

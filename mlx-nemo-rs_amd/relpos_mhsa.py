@@ -32,7 +32,9 @@ LINEARS = ("linear_q", "linear_k", "linear_v", "linear_out", "linear_pos")
 EXPORTS = (
     "mhsa_last_error", "mhsa_version", "mhsa_create", "mhsa_destroy", "mhsa_set_dtype", "mhsa_get_dtype",
     "mhsa_head_dim", "mhsa_n_heads", "mhsa_d_model", "mhsa_set_cache_drop_size", "mhsa_load_linear_standard",
-    "mhsa_load_linear_quantized", "mhsa_load_pos_bias", "mhsa_load_weights", "mhsa_forward", "mhsa_forward_noalloc",
+    "mhsa_load_linear_quantized", "mhsa_load_pos_bias", "mhsa_load_weights", "mhsa_checkpoint_open",
+    "mhsa_checkpoint_close", "mhsa_checkpoint_quantization", "mhsa_checkpoint_count", "mhsa_checkpoint_tensor",
+    "mhsa_checkpoint_metadata", "mhsa_load_weights_from_checkpoint", "mhsa_forward", "mhsa_forward_noalloc",
     "mhsa_sublayer_forward", "mhsa_stream_create", "mhsa_stream_destroy", "mhsa_stream_load_cache",
     "mhsa_stream_read_cache", "mhsa_stream_fill", "mhsa_forward_with_cache", "mhsa_forward_uncached",
     "mhsa_pos_encoding",
@@ -94,6 +96,13 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_load_linear_quantized": (I, [VP, I, VP, VP, VP, VP, I, I]),
         "mhsa_load_pos_bias": (I, [VP, I, VP, VP]),
         "mhsa_load_weights": (I, [VP, P(Tensor), I, ctypes.c_char_p, I, I, I]),
+        "mhsa_checkpoint_open": (I, [ctypes.c_char_p, P(VP)]),
+        "mhsa_checkpoint_close": (None, [VP]),
+        "mhsa_checkpoint_quantization": (I, [VP, PI, PI]),
+        "mhsa_checkpoint_count": (I, [VP]),
+        "mhsa_checkpoint_tensor": (I, [VP, I, P(Tensor)]),
+        "mhsa_checkpoint_metadata": (I, [VP, ctypes.c_char_p, P(ctypes.c_char_p)]),
+        "mhsa_load_weights_from_checkpoint": (I, [VP, VP, ctypes.c_char_p, I]),
         "mhsa_forward": (I, [VP, VP, I, I, VP, I, P(Context), PI, VP, VP]),
         "mhsa_forward_noalloc": (I, [VP, VP, I, I, VP, I, P(Context), PI, VP, VP]),
         "mhsa_sublayer_forward": (I, [VP, VP, I, I, P(ctypes.c_float), P(ctypes.c_float), F, VP, I, P(Context), PI,
@@ -277,6 +286,49 @@ class StreamingMask:
         return m, keep
 
 
+class Checkpoint:
+    """CheckpointLoader (checkpoint.rs:480-760) over an MLX safetensors file or
+    model directory: the memory-mapped tensor map and the quantization
+    settings from the model's config."""
+
+    _NP = {F32: np.float32, F16: np.float16, U32: np.uint32}
+
+    def __init__(self, path: str):
+        lib = library()
+        h = ctypes.c_void_p()
+        _check(lib.mhsa_checkpoint_open(os.fsencode(path), ctypes.byref(h)))
+        self._h, self._lib = h, lib
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            self._lib.mhsa_checkpoint_close(h)
+            self._h = None
+
+    def quantization(self) -> Optional[QuantizationConfig]:
+        bits, group = ctypes.c_int32(), ctypes.c_int32()
+        _check(self._lib.mhsa_checkpoint_quantization(self._h, ctypes.byref(bits), ctypes.byref(group)))
+        return QuantizationConfig(bits.value, group.value) if bits.value else None
+
+    def metadata(self, key: str) -> Optional[str]:
+        v = ctypes.c_char_p()
+        _check(self._lib.mhsa_checkpoint_metadata(self._h, key.encode(), ctypes.byref(v)))
+        return None if v.value is None else v.value.decode()
+
+    def tensors(self) -> Dict[str, np.ndarray]:
+        """name -> host array (a copy; bf16 entries as their uint16 bit patterns)."""
+        out = {}
+        for i in range(self._lib.mhsa_checkpoint_count(self._h)):
+            t = Tensor()
+            _check(self._lib.mhsa_checkpoint_tensor(self._h, i, ctypes.byref(t)))
+            shape = tuple(t.shape[k] for k in range(t.ndim))
+            dt = self._NP.get(t.dtype, np.uint16)
+            n = int(np.prod(shape)) if shape else 1
+            buf = (ctypes.c_char * (n * np.dtype(dt).itemsize)).from_address(t.data)
+            out[t.name.decode()] = np.frombuffer(bytes(buf), dtype=dt).reshape(shape)
+        return out
+
+
 # ---------------------------------------------------------------------------
 # the attention module
 # ---------------------------------------------------------------------------
@@ -359,6 +411,10 @@ class RelPositionMultiHeadAttention:
         bits, group = (quant.bits, quant.group_size) if quant else (0, 0)
         _check(self._lib.mhsa_load_weights(self._h, arr_t, len(tensors), prefix.encode(), 1 if strict else 0,
                                            bits, group))
+
+    def load_checkpoint(self, ckpt: "Checkpoint", prefix: str, strict: bool = True) -> None:
+        """load_weights from an on-disk checkpoint with its quantization."""
+        _check(self._lib.mhsa_load_weights_from_checkpoint(self._h, ckpt._h, prefix.encode(), 1 if strict else 0))
 
     # attention.rs:446-573
     def forward(self, x, pos_emb, context: Optional[AttentionContext] = None,

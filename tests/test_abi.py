@@ -81,7 +81,7 @@ def test_load_weights_detects_quantization():
     layer.load_weights(W.prefixed(w, "p"), "p")
     with pytest.raises(M.MhsaError) as e:
         layer.load_weights(W.prefixed(w, "p"), "p", quant=M.QuantizationConfig(4, 64))
-    assert e.value.code == M.MHSA_EINVAL  # shapes do not match 4-bit packing
+    assert e.value.code == M.MHSA_ENOTSUP  # only 8-bit, group-64 layers have kernels
     q = {k: v for k, v in W.prefixed(w, "p").items()}
     ql = M.LinearLayer.quantized(q["p.linear_q.weight"], q["p.linear_q.scales"], q["p.linear_q.biases"], bits=4)
     with pytest.raises(M.MhsaError) as e:

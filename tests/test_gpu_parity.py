@@ -911,3 +911,31 @@ def test_stack_u8_full_size_deterministic():
     b = _stack_gpu(layers, cfg, x, ex["lengths"], pos)
     assert torch.isfinite(a.float()).all()
     assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# on-disk checkpoints
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("quantized", [True, False])
+def test_layer_from_safetensors_checkpoint(tmp_path, quantized):
+    """A layer loaded from an MLX safetensors checkpoint (written by the
+    safetensors package, quantization in config.json) computes exactly what
+    the same weights loaded from memory compute, in bf16."""
+    import json
+    from safetensors.numpy import save_file
+    rng = np.random.default_rng(72)
+    d, h, T = 256, 2, 90
+    w = W.make_layer_weights(rng, d, h, True, quantized, centred=True)
+    prefix = "encoder.layers.3.self_attn"
+    save_file({f"{prefix}.{k}": np.ascontiguousarray(v) for k, v in w.items()}, str(tmp_path / "model.safetensors"),
+              metadata={"format": "mlx"})
+    if quantized:
+        (tmp_path / "config.json").write_text(json.dumps({"quantization": {"bits": 8, "group_size": 64}}))
+    a = M.RelPositionMultiHeadAttention(d, h, True)
+    a.load_checkpoint(M.Checkpoint(str(tmp_path)), prefix)
+    a.set_dtype(O.BF16)
+    b = gpu_layer(w, d, h, True, O.BF16)
+    x = dev(rng.standard_normal((2, T, d)), O.BF16)
+    pos = dev(O.RelPositionalEncoding(d, 5000, True).get_encoding(T), O.BF16)
+    assert torch.equal(a.forward(x, pos, None, [T, 51]), b.forward(x, pos, None, [T, 51]))
