@@ -271,6 +271,39 @@ int32_t mhsa_forward_with_cache(mhsa_layer* layer, mhsa_stream* stream, const vo
 int32_t mhsa_forward_uncached(mhsa_layer* layer, const void* x, int32_t batch, int32_t seq_len, const void* pos_emb,
                               int32_t pos_len, const mhsa_stream_mask* mask, void* out, void* hip_stream);
 
+/* ---- encoder-level streaming ---------------------------------------------- */
+
+/* The per-chunk layer loop of ConformerEncoder::forward_streaming
+ * (conformer.rs:840-1047) over the attention sublayers of n_layers layers
+ * (same d_model), with the EncoderCache (streaming/core.rs:117-166) kept as
+ * one HBM ring per layer instead of the reference's slice, pad/truncate and
+ * restack of [layers, batch, C, D] (conformer.rs:958-1023), and one fill per
+ * session (the reference uses session 0's for every session,
+ * conformer.rs:883-887). The layers must not be used by another stack or
+ * stream at the same time. */
+typedef struct mhsa_stack mhsa_stack;
+int32_t mhsa_stack_create(mhsa_layer* const* layers, int32_t n_layers, int32_t batch, int32_t cache_size,
+                          int32_t chunk_len, mhsa_stack** out);
+void mhsa_stack_destroy(mhsa_stack* stack);
+/* cache [n_layers, batch, cache_size, d_model] device fp32 (last_channel);
+ * filled_host [batch] (last_channel_len; NULL = 0). */
+int32_t mhsa_stack_load_cache(mhsa_stack* stack, const void* cache, const int32_t* filled_host, void* hip_stream);
+int32_t mhsa_stack_read_cache(const mhsa_stack* stack, void* cache_out, void* hip_stream);
+int32_t mhsa_stack_fill(const mhsa_stack* stack, int32_t* filled_out_host);
+/* One chunk through every layer: x <- x + MHSA_l(LayerNorm_l(x)) with each
+ * layer's cache (the attention part of ConformerBlock::forward_with_cache,
+ * conformer.rs:1924-1934), then the fill update min(fill + q_keep, C)
+ * (conformer.rs:1025-1036) with q_keep from each layer's cache_drop_size.
+ *  x_inout  [batch, chunk_len, d_model] device fp32, updated in place
+ *  ln_gamma_host / ln_beta_host  [n_layers, d_model] host fp32 (NULL = 1 / 0),
+ *           held at each layer's parameter precision; eps as nn::LayerNorm
+ *  pos_emb  [2*(cache_size+chunk_len)-1, d_model] device, layer dtype
+ *  mask     as for mhsa_forward_with_cache; a NULL filled_host means every
+ *           layer reads the fills the stack had at the start of the step. */
+int32_t mhsa_stack_step(mhsa_stack* stack, void* x_inout, const float* ln_gamma_host, const float* ln_beta_host,
+                        float eps, const void* pos_emb, int32_t pos_len, const mhsa_stream_mask* mask,
+                        void* hip_stream);
+
 /* ---- helpers ------------------------------------------------------------ */
 
 /* RelPositionalEncoding::new(d_model, max_len).get_encoding(seq_len)

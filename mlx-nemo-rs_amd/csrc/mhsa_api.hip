@@ -16,6 +16,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -1072,7 +1073,7 @@ namespace {
 // the no-cache form (S == null: keys and values from x alone,
 // attention.rs:687-700), both in fp32 (prepare_stream says why).
 int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, const void* pos_emb, int pos_len,
-                    const mhsa_stream_mask* mask, void* out, hipStream_t s) {
+                    const mhsa_stream_mask* mask, void* out, hipStream_t s, const void* residual = nullptr) {
   if (!x || !pos_emb || !out) return fail(MHSA_EINVAL, "null tensor pointer");
   if (!aligned16(x) || !aligned16(pos_emb) || !aligned16(out))
     return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
@@ -1207,7 +1208,7 @@ int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, 
   if (rc) return rc;
   ps_kv.next("gemm_out");
   for (int r = L->prof.reps("gemm_out"); r > 0 && !rc; --r)
-    rc = run_gemm(L, mhsa::kF32, L->sdev[3], D, cx, D, (int)M, out, D, nullptr, 0, s);
+    rc = run_gemm(L, mhsa::kF32, L->sdev[3], D, cx, D, (int)M, out, D, residual, D, s);
   if (rc) return rc;
   if (S) {
     const int keep = std::max(T - L->cache_drop, 0);  // attention.rs:665
@@ -1232,6 +1233,124 @@ int32_t mhsa_forward_uncached(mhsa_layer* L, const void* x, int32_t batch, int32
                               int32_t pos_len, const mhsa_stream_mask* mask, void* out, void* hs) {
   if (int32_t rc = check_layer(L)) return rc;
   return stream_step(L, nullptr, x, batch, seq_len, pos_emb, pos_len, mask, out, static_cast<hipStream_t>(hs));
+}
+
+}  // extern "C"
+
+struct mhsa_stack {
+  std::vector<mhsa_layer*> layers;
+  std::vector<mhsa_stream*> streams;
+  int B = 0, C = 0, T = 0, D = 0;
+  DevBuf h;       // [B, T, D] fp32: LayerNorm output of the current layer
+  DevBuf ln;      // [layers, 2, D] fp32 gamma | beta as uploaded
+  std::vector<float> ln_host;
+  ~mhsa_stack() {
+    for (mhsa_stream* st : streams) mhsa_stream_destroy(st);
+  }
+};
+
+extern "C" {
+
+int32_t mhsa_stack_create(mhsa_layer* const* layers, int32_t n_layers, int32_t batch, int32_t cache_size,
+                          int32_t chunk_len, mhsa_stack** out) {
+  if (!out || !layers || n_layers <= 0) return fail(MHSA_EINVAL, "null or empty layer list");
+  *out = nullptr;
+  std::unique_ptr<mhsa_stack> K(new (std::nothrow) mhsa_stack());
+  if (!K) return fail(MHSA_ENOMEM, "out of host memory");
+  for (int i = 0; i < n_layers; ++i) {
+    if (!layers[i]) return fail(MHSA_EINVAL, "layer %d is null", i);
+    if (layers[i]->D != layers[0]->D) return fail(MHSA_EINVAL, "layer %d has d_model %d, layer 0 %d", i, layers[i]->D,
+                                                  layers[0]->D);
+    if (layers[i]->D > mhsa::kMaxLayerNormDim)
+      return fail(MHSA_ENOTSUP, "the sublayer's LayerNorm supports d_model <= %d", mhsa::kMaxLayerNormDim);
+    for (int j = 0; j < i; ++j)
+      if (layers[j] == layers[i]) return fail(MHSA_EINVAL, "layer %d appears twice", i);
+    mhsa_stream* st = nullptr;
+    if (int32_t rc = mhsa_stream_create(layers[i], batch, cache_size, chunk_len, &st)) return rc;
+    K->layers.push_back(layers[i]);
+    K->streams.push_back(st);
+  }
+  K->B = batch;
+  K->C = cache_size;
+  K->T = chunk_len;
+  K->D = layers[0]->D;
+  HIPCHK(K->h.ensure(align_up((int64_t)batch * chunk_len * K->D * 4, 256)));
+  *out = K.release();
+  return MHSA_OK;
+}
+
+void mhsa_stack_destroy(mhsa_stack* K) { delete K; }
+
+int32_t mhsa_stack_load_cache(mhsa_stack* K, const void* cache, const int32_t* filled, void* hs) {
+  if (!K || !cache) return fail(MHSA_EINVAL, "null argument");
+  const size_t per = (size_t)K->B * K->C * K->D * 4;
+  for (size_t l = 0; l < K->streams.size(); ++l)
+    if (int32_t rc = mhsa_stream_load_cache(K->streams[l], static_cast<const char*>(cache) + l * per, filled, hs))
+      return rc;
+  return MHSA_OK;
+}
+
+int32_t mhsa_stack_read_cache(const mhsa_stack* K, void* out, void* hs) {
+  if (!K || !out) return fail(MHSA_EINVAL, "null argument");
+  const size_t per = (size_t)K->B * K->C * K->D * 4;
+  for (size_t l = 0; l < K->streams.size(); ++l)
+    if (int32_t rc = mhsa_stream_read_cache(K->streams[l], static_cast<char*>(out) + l * per, hs)) return rc;
+  return MHSA_OK;
+}
+
+int32_t mhsa_stack_fill(const mhsa_stack* K, int32_t* out) {
+  if (!K) return fail(MHSA_EINVAL, "null argument");
+  return mhsa_stream_fill(K->streams[0], out);
+}
+
+int32_t mhsa_stack_step(mhsa_stack* K, void* x, const float* gamma, const float* beta, float eps, const void* pos_emb,
+                        int32_t pos_len, const mhsa_stream_mask* mask, void* hs) {
+  if (!K || !x) return fail(MHSA_EINVAL, "null argument");
+  if (!aligned16(x)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  const int D = K->D, n = (int)K->layers.size();
+  const int64_t M = (int64_t)K->B * K->T;
+  // per-layer LayerNorm gamma/beta ([layers, D] host arrays), held at each
+  // layer's parameter precision (conformer.rs:422-434 casts the norms too)
+  const float* g = nullptr;
+  if (gamma || beta) {
+    std::vector<float> tmp((size_t)2 * n * D);
+    for (int l = 0; l < n; ++l) {
+      const bool bf = K->layers[l]->dt == mhsa::kBF16;
+      for (int i = 0; i < D; ++i) {
+        const float gv = gamma ? gamma[(size_t)l * D + i] : 1.f, bv = beta ? beta[(size_t)l * D + i] : 0.f;
+        tmp[(size_t)2 * l * D + i] = bf ? round_bf16(gv) : gv;
+        tmp[(size_t)(2 * l + 1) * D + i] = bf ? round_bf16(bv) : bv;
+      }
+    }
+    if (tmp != K->ln_host) {
+      if (K->ln.p) HIPCHK(hipDeviceSynchronize());  // an earlier step may still read them
+      HIPCHK(K->ln.ensure(tmp.size() * 4));
+      HIPCHK(hipMemcpy(K->ln.p, tmp.data(), tmp.size() * 4, hipMemcpyHostToDevice));
+      K->ln_host = tmp;
+    }
+    g = static_cast<const float*>(K->ln.p);
+  }
+  // every layer reads the fills of the step's start; each stream then moves
+  // its own copy the same way (conformer.rs:1025-1036)
+  std::vector<int32_t> fills(K->B);
+  if (int32_t rc = mhsa_stream_fill(K->streams[0], fills.data())) return rc;
+  mhsa_stream_mask m;
+  if (mask && mask->present) {
+    m = *mask;
+    if (!m.filled_host) m.filled_host = fills.data();
+    mask = &m;
+  }
+  for (int l = 0; l < n; ++l) {
+    mhsa_layer* L = K->layers[l];
+    {
+      ProfScope ps(L, "layer_norm", s);
+      HIPCHK(mhsa::layer_norm(mhsa::kF32, x, K->h.p, g ? g + (size_t)2 * l * D : nullptr,
+                              g ? g + (size_t)(2 * l + 1) * D : nullptr, eps, (int)M, D, s));
+    }
+    if (int32_t rc = stream_step(L, K->streams[l], K->h.p, K->B, K->T, pos_emb, pos_len, mask, x, s, x)) return rc;
+  }
+  return MHSA_OK;
 }
 
 int32_t mhsa_pos_encoding(int32_t d_model, int32_t max_len, int32_t seq_len, float* out) {

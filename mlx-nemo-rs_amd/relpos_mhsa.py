@@ -37,6 +37,8 @@ EXPORTS = (
     "mhsa_checkpoint_metadata", "mhsa_load_weights_from_checkpoint", "mhsa_forward", "mhsa_forward_noalloc",
     "mhsa_sublayer_forward", "mhsa_stream_create", "mhsa_stream_destroy", "mhsa_stream_load_cache",
     "mhsa_stream_read_cache", "mhsa_stream_fill", "mhsa_forward_with_cache", "mhsa_forward_uncached",
+    "mhsa_stack_create", "mhsa_stack_destroy", "mhsa_stack_load_cache", "mhsa_stack_read_cache", "mhsa_stack_fill",
+    "mhsa_stack_step",
     "mhsa_pos_encoding",
     "mhsa_debug_dequantize", "mhsa_debug_linear", "mhsa_debug_offline_mask", "mhsa_debug_stream_mask", "mhsa_debug_rel_shift_index",
     "mhsa_debug_position_scores", "mhsa_debug_top_keys", "mhsa_profile_enable", "mhsa_profile_repeat",
@@ -114,6 +116,12 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_stream_fill": (I, [VP, PI]),
         "mhsa_forward_with_cache": (I, [VP, VP, VP, VP, I, P(StreamMask), VP, VP]),
         "mhsa_forward_uncached": (I, [VP, VP, I, I, VP, I, P(StreamMask), VP, VP]),
+        "mhsa_stack_create": (I, [P(VP), I, I, I, I, P(VP)]),
+        "mhsa_stack_destroy": (None, [VP]),
+        "mhsa_stack_load_cache": (I, [VP, VP, PI, VP]),
+        "mhsa_stack_read_cache": (I, [VP, VP, VP]),
+        "mhsa_stack_fill": (I, [VP, PI]),
+        "mhsa_stack_step": (I, [VP, VP, P(ctypes.c_float), P(ctypes.c_float), F, VP, I, P(StreamMask), VP]),
         "mhsa_pos_encoding": (I, [I, I, I, P(ctypes.c_float)]),
         "mhsa_debug_dequantize": (I, [VP, I, VP, VP]),
         "mhsa_debug_linear": (I, [VP, I, VP, I, VP, VP]),
@@ -629,6 +637,60 @@ class StreamState:
                                                        ctypes.byref(m) if m is not None else None, _dptr(out),
                                                        _stream_ptr()))
         return out
+
+
+class StreamingStack:
+    """The encoder's streaming layer loop over the attention sublayers
+    (ConformerEncoder::forward_streaming, conformer.rs:840-1047): one cache
+    ring per layer, one fill per session."""
+
+    def __init__(self, layers: Sequence[RelPositionMultiHeadAttention], batch: int, cache_size: int,
+                 chunk_len: int):
+        self.layers = list(layers)
+        self.batch, self.cache_size, self.chunk_len = batch, cache_size, chunk_len
+        self._lib = library()
+        arr = (ctypes.c_void_p * len(self.layers))(*[l._h.value for l in self.layers])
+        h = ctypes.c_void_p()
+        _check(self._lib.mhsa_stack_create(arr, len(self.layers), batch, cache_size, chunk_len, ctypes.byref(h)))
+        self._h = h
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            self._lib.mhsa_stack_destroy(h)
+            self._h = None
+
+    def load_cache(self, cache, filled: Optional[Sequence[int]] = None) -> None:
+        """cache: [layers, batch, cache_size, d_model] float32 GPU tensor."""
+        _check(self._lib.mhsa_stack_load_cache(self._h, _dptr(cache.contiguous()), _int_array(filled), _stream_ptr()))
+
+    def read_cache(self):
+        import torch
+        out = torch.empty((len(self.layers), self.batch, self.cache_size, self.layers[0].d_model),
+                          dtype=torch.float32, device="cuda")
+        _check(self._lib.mhsa_stack_read_cache(self._h, _dptr(out), _stream_ptr()))
+        return out
+
+    def fill(self):
+        arr = (ctypes.c_int32 * self.batch)()
+        _check(self._lib.mhsa_stack_fill(self._h, arr))
+        return list(arr)
+
+    def step_(self, x, pos_emb, mask: Optional[StreamingMask] = None, gamma=None, beta=None, eps=1e-5):
+        """In place x <- x + MHSA_l(LN_l(x)) for every layer; gamma/beta [layers, d_model]."""
+        import torch
+        if not x.is_cuda or x.dtype != torch.float32 or not x.is_contiguous():
+            raise MhsaError(MHSA_EINVAL, "the stack streams contiguous float32 GPU activations")
+        pe = pos_emb.reshape(-1, x.shape[-1])
+        self.layers[0]._check_dev(pe)
+        g = None if gamma is None else _host_f32(gamma)
+        b = None if beta is None else _host_f32(beta)
+        fp = ctypes.POINTER(ctypes.c_float)
+        m, keep = (mask.c() if mask is not None else (None, []))
+        _check(self._lib.mhsa_stack_step(self._h, _dptr(x), None if g is None else g.ctypes.data_as(fp),
+                                         None if b is None else b.ctypes.data_as(fp), float(eps), _dptr(pe),
+                                         pe.shape[0], ctypes.byref(m) if m is not None else None, _stream_ptr()))
+        return x
 
 
 # ---------------------------------------------------------------------------

@@ -939,3 +939,79 @@ def test_layer_from_safetensors_checkpoint(tmp_path, quantized):
     x = dev(rng.standard_normal((2, T, d)), O.BF16)
     pos = dev(O.RelPositionalEncoding(d, 5000, True).get_encoding(T), O.BF16)
     assert torch.equal(a.forward(x, pos, None, [T, 51]), b.forward(x, pos, None, [T, 51]))
+
+
+# ---------------------------------------------------------------------------
+# encoder-level streaming: the stack of attention sublayers
+# ---------------------------------------------------------------------------
+
+def _stack_oracle_step(params, gammas, betas, xb, caches_b, pos, fill, T, C, dtype):
+    """One chunk of one session through the layers, as the reference's
+    ConformerBlock::forward_with_cache attention part (conformer.rs:1924-1934)
+    with the session's own fill."""
+    mask = O.streaming_mask((70, 13), "chunked_limited", C, fill, T, T)
+    for l, p in enumerate(params):
+        h = O.layer_norm(xb, O.to_dtype(gammas[l], dtype), O.to_dtype(betas[l], dtype), 1e-5, O.F32)
+        y, caches_b[l] = O.mhsa_forward_with_cache(p, h, pos, caches_b[l], mask, dtype=dtype)
+        xb = xb + y
+    return xb
+
+
+@pytest.mark.parametrize("dtype,quant,n_layers,B,steps", [(O.F32, False, 24, 4, 50), (O.BF16, True, 4, 3, 8)])
+def test_streaming_stack_against_per_session_oracle(dtype, quant, n_layers, B, steps):
+    """n_layers attention sublayers streamed together for `steps` chunks:
+    14-frame chunks, a 70-frame cache per layer, [70,13] chunked_limited,
+    per-session fills and LayerNorm parameters per layer. The oracle runs
+    every session as its own B=1 reference stream through every layer; each
+    step's output is checked (fp32 bound), and so are the caches of all
+    layers read back at the end (they hold each layer's LayerNorm output,
+    computed in fp32 here and in float64 by the oracle, so not bit-equal)."""
+    rng = np.random.default_rng(81)
+    d, h, C, T = 256, 4, 70, 14
+    ws = []
+    for _ in range(n_layers):
+        if quant:
+            w = W.make_layer_weights(rng, d, h, True, True, centred=True)
+            for name in ("linear_q", "linear_k", "linear_v", "linear_out", "linear_pos"):
+                sc = rng.uniform(1e-4, 1e-3, size=w[f"{name}.scales"].shape)
+                w[f"{name}.scales"] = sc.astype(np.float16)
+                w[f"{name}.biases"] = (-128.0 * w[f"{name}.scales"].astype(np.float64)).astype(np.float16)
+                if name != "linear_pos":
+                    w[f"{name}.bias"] = rng.normal(0, 0.1, d).astype(np.float16)
+        else:
+            w = random_weights(rng, d, h, use_bias=True, scale=0.05)
+        ws.append(w)
+    params = [oracle_params(w, d, h) for w in ws]
+    gammas = rng.uniform(0.5, 1.5, (n_layers, d)).astype(np.float32)
+    betas = rng.normal(0, 0.1, (n_layers, d)).astype(np.float32)
+    layers = [gpu_layer(w, d, h, True, dtype, prefix=f"l{i}") for i, w in enumerate(ws)]
+    stack = M.StreamingStack(layers, B, C, T)
+    cache = rng.standard_normal((n_layers, B, C, d)).astype(np.float32)
+    fills = [int(v) for v in rng.integers(0, C + 1, size=B)]
+    for b in range(B):
+        cache[:, b, :C - fills[b]] = 0.0
+    stack.load_cache(dev(cache, O.F32), fills)
+    caches = [[cache[l, b:b + 1].astype(np.float64) for l in range(n_layers)] for b in range(B)]
+    pos = O.RelPositionalEncoding(d, 5000, True).get_encoding(C + T)
+    pos = pos if dtype == O.F32 else O.bf16_round(pos)
+    pos_d = dev(pos, dtype)
+    worst = 0.0
+    for step in range(steps):
+        x = rng.standard_normal((B, T, d)).astype(np.float32)
+        xd = dev(x, O.F32)
+        stack.step_(xd, pos_d, M.StreamingMask((70, 13), "chunked_limited"), gammas, betas)
+        got = host(xd)
+        for b in range(B):
+            ref = _stack_oracle_step(params, gammas, betas, x[b:b + 1].astype(np.float64), caches[b], pos, fills[b],
+                                     T, C, dtype)
+            e = row_rel_err(got[b:b + 1], ref)
+            worst = max(worst, e)
+            assert e < F32_TOL, (step, b, e)
+            fills[b] = O.next_fill(fills[b], T, 0, C)
+        assert stack.fill() == fills
+    print(f"stack of {n_layers} layers, {steps} steps: worst per-row relative error {worst:.3e}")
+    got_cache = stack.read_cache().cpu().numpy()
+    ref_cache = np.stack([np.concatenate([caches[b][l] for b in range(B)], 0) for l in range(n_layers)])
+    live = np.abs(ref_cache).max(axis=-1) > 0  # unfilled rows are zeros on both sides
+    assert np.array_equal(got_cache[~live], ref_cache[~live].astype(np.float32))
+    assert row_rel_err(got_cache[live], ref_cache[live]) < 1e-5
