@@ -271,6 +271,32 @@ int32_t mhsa_forward_with_cache(mhsa_layer* layer, mhsa_stream* stream, const vo
 int32_t mhsa_forward_uncached(mhsa_layer* layer, const void* x, int32_t batch, int32_t seq_len, const void* pos_emb,
                               int32_t pos_len, const mhsa_stream_mask* mask, void* out, void* hip_stream);
 
+/* ---- FeedForward (the rest of the Conformer block's GEMM work) ------------- */
+
+/* FeedForward (conformer.rs:2031-2088): out = linear2(silu(linear1(x))),
+ * linear1 [ff_dim, d_model], linear2 [d_model, ff_dim], each standard or MLX
+ * affine 8-bit (group 64), with biases when use_bias. The projections run
+ * on the same GEMM kernels as the attention projections (fused in-register
+ * dequantisation), linear1 with a SiLU epilogue that stores sigmoid and the
+ * product in the dtype as nn::silu does. d_model, ff_dim multiples of 64. */
+typedef struct mhsa_ffn mhsa_ffn;
+int32_t mhsa_ffn_create(int32_t d_model, int32_t ff_dim, int32_t use_bias, mhsa_ffn** out);
+void mhsa_ffn_destroy(mhsa_ffn* ffn);
+/* set_dtype (conformer.rs:2040-2043): MHSA_F32 or MHSA_BF16. */
+int32_t mhsa_ffn_set_dtype(mhsa_ffn* ffn, int32_t dtype);
+/* load_weights (conformer.rs:2074-2087): {prefix}.linear1 / .linear2 with
+ * .weight, .bias, .scales, .biases as mhsa_load_weights resolves them
+ * (prefix e.g. "encoder.layers.0.feed_forward1"). */
+int32_t mhsa_ffn_load_weights(mhsa_ffn* ffn, const mhsa_tensor* tensors, int32_t n_tensors, const char* prefix,
+                              int32_t strict, int32_t quant_bits, int32_t quant_group);
+/* forward (conformer.rs:2066-2072): x, out [rows, d_model] device, dtype. */
+int32_t mhsa_ffn_forward(mhsa_ffn* ffn, const void* x, int32_t rows, void* out, void* hip_stream);
+/* The block's half-step sublayer x <- x + 0.5 * forward(LayerNorm(x))
+ * (conformer.rs:1703-1729, 1827-1851); gamma/beta [d_model] host fp32 or
+ * NULL, eps as nn::LayerNorm; the residual is fused into linear2's epilogue. */
+int32_t mhsa_ffn_sublayer_forward(mhsa_ffn* ffn, void* x_inout, int32_t rows, const float* ln_gamma_host,
+                                  const float* ln_beta_host, float eps, void* hip_stream);
+
 /* ---- encoder-level streaming ---------------------------------------------- */
 
 /* The per-chunk layer loop of ConformerEncoder::forward_streaming

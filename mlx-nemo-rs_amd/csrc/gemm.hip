@@ -113,13 +113,21 @@ __device__ __forceinline__ int64_t mapped_row(const GemmParams& p, int row) {
 // C offset of one output row (computed once per row).
 __device__ __forceinline__ int64_t row_offset(const GemmParams& p, int row) { return mapped_row(p, row) * p.ldc; }
 
-// The reference's op order: round the product, add the bias, round, add the
-// residual, round.
+// nn::silu as the reference evaluates it: sigmoid stored in the dtype, then
+// the product stored (conformer.rs:2069).
+template <typename T>
+__device__ __forceinline__ float silu_value(float v) {
+  return round_to<T>(v * round_to<T>(1.f / (1.f + expf(-v))));
+}
+
+// The reference's op order: round the product, add the bias, round, (SiLU,)
+// add the (scaled) residual, round.
 template <typename T>
 __device__ __forceinline__ float epilogue_value(const GemmParams& p, int row, int col, float acc) {
   float v = round_to<T>(acc);
   if (p.bias) v = round_to<T>(v + p.bias[col]);
-  if (p.R) v = round_to<T>((float)reinterpret_cast<const T*>(p.R)[(int64_t)row * p.ldr + col] + v);
+  if (p.act == kActSilu) v = silu_value<T>(v);
+  if (p.R) v = round_to<T>((float)reinterpret_cast<const T*>(p.R)[(int64_t)row * p.ldr + col] + p.res_scale * v);
   return v;
 }
 
@@ -657,7 +665,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
   // 8 columns [col, col + 8) of block row r to C, with the bias and residual
   auto store_c = [&](int r, int col, bf16x8 v) {
     const int row = row0 + r;
-    if (p.bias || p.R) {
+    if (p.bias || p.R || p.act) {
       float f[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) f[e] = (float)v[e];
@@ -670,10 +678,14 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
           f[e + 4] = round_to<bf16>(f[e + 4] + b1[e]);
         }
       }
+      if (p.act == kActSilu) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = silu_value<bf16>(f[e]);
+      }
       if (p.R) {
         const bf16x8 rv = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.R) + (int64_t)row * p.ldr + col);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] = round_to<bf16>((float)rv[e] + f[e]);
+        for (int e = 0; e < 8; ++e) f[e] = round_to<bf16>((float)rv[e] + p.res_scale * f[e]);
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = (bf16)f[e];

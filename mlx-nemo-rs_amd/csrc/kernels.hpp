@@ -53,7 +53,14 @@ struct GemmParams {
   int c2_col0 = 0;
   void* acopy = nullptr;
   int64_t acopy_ld = 0;
+  // FeedForward epilogues (conformer.rs:1727-1729, 2066-2072): act = kActSilu
+  // applies SiLU after the bias as the reference materialises nn::silu,
+  // T(y * T(sigmoid(y))); res_scale multiplies y before the residual add (the
+  // half-step residual R + 0.5 y; exact in either dtype)
+  int act = 0;
+  float res_scale = 1.f;
 };
+constexpr int kActSilu = 1;
 // Scratch the K-split path can use: 64x64 tiles x splits stays <= ~512
 // workgroups, so M*N*splits <= kGemmPartialElems.
 constexpr int64_t kGemmPartialElems = (int64_t)1 << 22;

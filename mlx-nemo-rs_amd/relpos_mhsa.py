@@ -38,7 +38,8 @@ EXPORTS = (
     "mhsa_sublayer_forward", "mhsa_stream_create", "mhsa_stream_destroy", "mhsa_stream_load_cache",
     "mhsa_stream_read_cache", "mhsa_stream_fill", "mhsa_forward_with_cache", "mhsa_forward_uncached",
     "mhsa_stack_create", "mhsa_stack_destroy", "mhsa_stack_load_cache", "mhsa_stack_read_cache", "mhsa_stack_fill",
-    "mhsa_stack_step",
+    "mhsa_stack_step", "mhsa_ffn_create", "mhsa_ffn_destroy", "mhsa_ffn_set_dtype", "mhsa_ffn_load_weights",
+    "mhsa_ffn_forward", "mhsa_ffn_sublayer_forward",
     "mhsa_pos_encoding",
     "mhsa_debug_dequantize", "mhsa_debug_linear", "mhsa_debug_offline_mask", "mhsa_debug_stream_mask", "mhsa_debug_rel_shift_index",
     "mhsa_debug_position_scores", "mhsa_debug_top_keys", "mhsa_profile_enable", "mhsa_profile_repeat",
@@ -122,6 +123,12 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_stack_read_cache": (I, [VP, VP, VP]),
         "mhsa_stack_fill": (I, [VP, PI]),
         "mhsa_stack_step": (I, [VP, VP, P(ctypes.c_float), P(ctypes.c_float), F, VP, I, P(StreamMask), VP]),
+        "mhsa_ffn_create": (I, [I, I, I, P(VP)]),
+        "mhsa_ffn_destroy": (None, [VP]),
+        "mhsa_ffn_set_dtype": (I, [VP, I]),
+        "mhsa_ffn_load_weights": (I, [VP, P(Tensor), I, ctypes.c_char_p, I, I, I]),
+        "mhsa_ffn_forward": (I, [VP, VP, I, VP, VP]),
+        "mhsa_ffn_sublayer_forward": (I, [VP, VP, I, P(ctypes.c_float), P(ctypes.c_float), F, VP]),
         "mhsa_pos_encoding": (I, [I, I, I, P(ctypes.c_float)]),
         "mhsa_debug_dequantize": (I, [VP, I, VP, VP]),
         "mhsa_debug_linear": (I, [VP, I, VP, I, VP, VP]),
@@ -294,6 +301,74 @@ class StreamingMask:
         return m, keep
 
 
+def _tensor_list(weights: Dict[str, np.ndarray]):
+    """A Weights map as the C ABI's tensor list (arrays kept alive by the caller)."""
+    arrays, tensors = [], []
+    for name, arr in weights.items():
+        a = np.ascontiguousarray(arr)
+        code = {np.dtype(np.float32): F32, np.dtype(np.float16): F16, np.dtype(np.uint32): U32}.get(a.dtype)
+        if code is None:
+            a = np.ascontiguousarray(a, dtype=np.float32)
+            code = F32
+        arrays.append(a)
+        shape = (ctypes.c_int64 * 4)(*(list(a.shape) + [0] * (4 - a.ndim)))
+        tensors.append(Tensor(name.encode(), code, a.ndim, shape, a.ctypes.data))
+    return (Tensor * max(len(tensors), 1))(*tensors), len(tensors), arrays
+
+
+class FeedForward:
+    """FeedForward (conformer.rs:2031-2088) backed by the HIP library."""
+
+    def __init__(self, d_model: int, ff_dim: int, use_bias: bool):
+        lib = library()
+        h = ctypes.c_void_p()
+        _check(lib.mhsa_ffn_create(d_model, ff_dim, 1 if use_bias else 0, ctypes.byref(h)))
+        self._h, self._lib = h, lib
+        self.d_model, self.ff_dim = d_model, ff_dim
+        self._dtype = F32
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            self._lib.mhsa_ffn_destroy(h)
+            self._h = None
+
+    def set_dtype(self, dtype) -> None:
+        self._dtype = _dtype_code(dtype)
+        _check(self._lib.mhsa_ffn_set_dtype(self._h, self._dtype))
+
+    def load_weights(self, weights: Dict[str, np.ndarray], prefix: str,
+                     quant: Optional[QuantizationConfig] = None, strict: bool = True) -> None:
+        arr_t, n, keep = _tensor_list(weights)
+        bits, group = (quant.bits, quant.group_size) if quant else (0, 0)
+        _check(self._lib.mhsa_ffn_load_weights(self._h, arr_t, n, prefix.encode(), 1 if strict else 0, bits, group))
+
+    def _check(self, x):
+        import torch
+        want = _torch_dtype(self._dtype)
+        if not x.is_cuda or x.dtype != want or not x.is_contiguous() or x.shape[-1] != self.d_model:
+            raise MhsaError(MHSA_EINVAL, f"expected a contiguous {want} GPU tensor [..., {self.d_model}]")
+
+    def forward(self, x):
+        import torch
+        self._check(x)
+        out = torch.empty_like(x)
+        _check(self._lib.mhsa_ffn_forward(self._h, _dptr(x), x.numel() // self.d_model, _dptr(out), _stream_ptr()))
+        return out
+
+    def sublayer_forward_(self, x, gamma=None, beta=None, eps=1e-5):
+        """In place x <- x + 0.5 * forward(LayerNorm(x)) (conformer.rs:1703-1729)."""
+        self._check(x)
+        g = None if gamma is None else _host_f32(gamma)
+        b = None if beta is None else _host_f32(beta)
+        fp = ctypes.POINTER(ctypes.c_float)
+        _check(self._lib.mhsa_ffn_sublayer_forward(self._h, _dptr(x), x.numel() // self.d_model,
+                                                   None if g is None else g.ctypes.data_as(fp),
+                                                   None if b is None else b.ctypes.data_as(fp), float(eps),
+                                                   _stream_ptr()))
+        return x
+
+
 class Checkpoint:
     """CheckpointLoader (checkpoint.rs:480-760) over an MLX safetensors file or
     model directory: the memory-mapped tensor map and the quantization
@@ -405,20 +480,9 @@ class RelPositionMultiHeadAttention:
 
     def load_weights(self, weights: Dict[str, np.ndarray], prefix: str,
                      quant: Optional[QuantizationConfig] = None, strict: bool = True) -> None:
-        arrays, tensors = [], []
-        for name, arr in weights.items():
-            a = np.ascontiguousarray(arr)
-            code = {np.dtype(np.float32): F32, np.dtype(np.float16): F16, np.dtype(np.uint32): U32}.get(a.dtype)
-            if code is None:
-                a = np.ascontiguousarray(a, dtype=np.float32)
-                code = F32
-            arrays.append(a)
-            shape = (ctypes.c_int64 * 4)(*(list(a.shape) + [0] * (4 - a.ndim)))
-            tensors.append(Tensor(name.encode(), code, a.ndim, shape, a.ctypes.data))
-        arr_t = (Tensor * max(len(tensors), 1))(*tensors)
+        arr_t, n, keep = _tensor_list(weights)
         bits, group = (quant.bits, quant.group_size) if quant else (0, 0)
-        _check(self._lib.mhsa_load_weights(self._h, arr_t, len(tensors), prefix.encode(), 1 if strict else 0,
-                                           bits, group))
+        _check(self._lib.mhsa_load_weights(self._h, arr_t, n, prefix.encode(), 1 if strict else 0, bits, group))
 
     def load_checkpoint(self, ckpt: "Checkpoint", prefix: str, strict: bool = True) -> None:
         """load_weights from an on-disk checkpoint with its quantization."""

@@ -626,6 +626,38 @@ def mhsa_sublayer(p: MhsaParams, x, pos_emb, context=None, key_mask=None,
 
 
 # ---------------------------------------------------------------------------
+# FeedForward (conformer.rs:2031-2088) and its half-step sublayer
+# ---------------------------------------------------------------------------
+
+def silu(x: np.ndarray, dtype: str = F32) -> np.ndarray:
+    """mlx nn::silu = x * sigmoid(x) as two ops, each result stored in `dtype`
+    (conformer.rs:2069); evaluated in float64."""
+    x = np.asarray(x, dtype=np.float64)
+    sig = _rnd(1.0 / (1.0 + np.exp(-x)), dtype)
+    return _rnd(x * sig, dtype)
+
+
+@dataclass
+class FeedForwardParams:
+    """linear1 [ff_dim, d_model], linear2 [d_model, ff_dim] (conformer.rs:2031-2064)."""
+
+    linear1: LinearLayer
+    linear2: LinearLayer
+
+
+def feed_forward(p: FeedForwardParams, x: np.ndarray, dtype: str = F32) -> np.ndarray:
+    """FeedForward::forward (conformer.rs:2066-2072): linear2(silu(linear1(x)))."""
+    return p.linear2.forward(silu(p.linear1.forward(np.asarray(x, dtype=np.float64), dtype), dtype), dtype)
+
+
+def feed_forward_sublayer(p: FeedForwardParams, x, gamma=None, beta=None, dtype: str = F32, eps: float = 1e-5):
+    """x + 0.5 * FeedForward(LayerNorm(x)) (conformer.rs:1703-1729): the half
+    is cast to the output dtype, the scaled output and the sum stored."""
+    y = feed_forward(p, layer_norm(x, gamma, beta, eps, dtype), dtype)
+    return _rnd(np.asarray(x, dtype=np.float64) + _rnd(to_dtype(0.5, dtype) * y, dtype), dtype)
+
+
+# ---------------------------------------------------------------------------
 # Index maps exported for bit-exact checks
 # ---------------------------------------------------------------------------
 

@@ -1015,3 +1015,70 @@ def test_streaming_stack_against_per_session_oracle(dtype, quant, n_layers, B, s
     live = np.abs(ref_cache).max(axis=-1) > 0  # unfilled rows are zeros on both sides
     assert np.array_equal(got_cache[~live], ref_cache[~live].astype(np.float32))
     assert row_rel_err(got_cache[live], ref_cache[live]) < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# FeedForward (conformer.rs:2031-2088)
+# ---------------------------------------------------------------------------
+
+def _ffn_weights(rng, d, f, quant, prefix="ff"):
+    """linear1 [f, d], linear2 [d, f] with biases: dense Xavier, or affine u8
+    with zero-mean weights (scales U(1e-4, 1e-3)) so activations stay O(1)."""
+    w = {}
+    for name, (o, i) in (("linear1", (f, d)), ("linear2", (d, f))):
+        if quant:
+            codes = rng.integers(0, 256, size=(o, i))
+            sc = rng.uniform(1e-4, 1e-3, size=(o, i // 64)).astype(np.float16)
+            w[f"{prefix}.{name}.weight"] = W.pack_u8(codes)
+            w[f"{prefix}.{name}.scales"] = sc
+            w[f"{prefix}.{name}.biases"] = (-128.0 * sc.astype(np.float64) + rng.normal(0, 1e-3, sc.shape)).astype(np.float16)
+            w[f"{prefix}.{name}.bias"] = rng.normal(0, 0.1, o).astype(np.float16)
+        else:
+            w[f"{prefix}.{name}.weight"] = W.xavier(rng, o, i)
+            w[f"{prefix}.{name}.bias"] = rng.normal(0, 0.1, o).astype(np.float32)
+    return w
+
+
+def _ffn_oracle(w, prefix="ff"):
+    lin = []
+    for name in ("linear1", "linear2"):
+        k = f"{prefix}.{name}"
+        if f"{k}.scales" in w:
+            lin.append(O.LinearLayer(w[f"{k}.weight"], w[f"{k}.bias"], w[f"{k}.scales"], w[f"{k}.biases"]))
+        else:
+            lin.append(O.LinearLayer(np.asarray(w[f"{k}.weight"], np.float64), w[f"{k}.bias"]))
+    return O.FeedForwardParams(*lin)
+
+
+@pytest.mark.parametrize("dtype,quant,rows", [(O.BF16, True, 6000), (O.BF16, False, 6000), (O.F32, True, 500),
+                                              (O.F32, False, 37)])
+def test_feed_forward_against_oracle(dtype, quant, rows):
+    """FeedForward at the 0.6B shape (d_model 1024, ff_dim 4096; 6000 rows is
+    the stack's B=4 x T=1500): linear1 with the SiLU epilogue, linear2, on the
+    same dequant-GEMMs as the attention projections; then the half-step
+    sublayer x + 0.5 FF(LN(x)) with the residual in linear2's epilogue.
+    Outputs reach ~15, where one bf16 ulp is 0.0625, so bf16 is bounded per
+    row (2e-2 of the row's max), fp32 within 1e-4 per row."""
+    rng = np.random.default_rng(91)
+    d, f = 1024, 4096
+    w = _ffn_weights(rng, d, f, quant)
+    p = _ffn_oracle(w)
+    ff = M.FeedForward(d, f, True)
+    ff.load_weights(w, "ff")
+    ff.set_dtype(dtype)
+    x = rng.standard_normal((rows, d))
+    x = O.bf16_round(x) if dtype == O.BF16 else x.astype(np.float32).astype(np.float64)
+    got = host(ff.forward(dev(x, dtype)))
+    ref = O.feed_forward(p, x, dtype)
+    err = row_rel_err(got, ref)
+    print(f"feed_forward {dtype} quant={quant} rows={rows}: per-row error {err:.3e}, max abs "
+          f"{abs_err(got, ref):.3e} (max |ref| {np.max(np.abs(ref)):.2f})")
+    assert err < (BF16_TOL if dtype == O.BF16 else F32_TOL)
+    gamma = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    beta = rng.normal(0, 0.1, d).astype(np.float32)
+    xd = dev(x, dtype)
+    ff.sublayer_forward_(xd, gamma, beta)
+    ref = O.feed_forward_sublayer(p, x, gamma, beta, dtype)
+    err = row_rel_err(host(xd), ref)
+    print(f"  sublayer: per-row error / row max {err:.3e}")
+    assert err < (BF16_TOL if dtype == O.BF16 else F32_TOL)

@@ -624,3 +624,45 @@ def test_streaming_chunk_equals_offline_rows():
     # offline over all C+T frames, keeping only the last T query rows
     full = O.mhsa_forward(p, seq, pos)
     assert np.max(np.abs(out - full[:, C:])) < 1e-10
+
+
+# ---------------------------------------------------------------------------
+# FeedForward (conformer.rs:2031-2088) and the half-step sublayer
+# ---------------------------------------------------------------------------
+
+def _ffn_params(d, f, seed, scale=0.5):
+    rng = np.random.default_rng(seed)
+    return O.FeedForwardParams(O.LinearLayer(rng.standard_normal((f, d)) * scale, rng.standard_normal(f) * scale),
+                               O.LinearLayer(rng.standard_normal((d, f)) * scale, rng.standard_normal(d) * scale))
+
+
+def test_feed_forward_f32_matches_torch():
+    p = _ffn_params(16, 64, 31, scale=0.3)
+    x = np.random.default_rng(32).standard_normal((5, 16))
+    xt = torch.tensor(x, dtype=torch.float64)
+    h = torch.nn.functional.silu(torch.nn.functional.linear(xt, torch.tensor(p.linear1.weight),
+                                                              torch.tensor(p.linear1.bias)))
+    ref = torch.nn.functional.linear(h, torch.tensor(p.linear2.weight), torch.tensor(p.linear2.bias)).numpy()
+    assert np.max(np.abs(O.feed_forward(p, x) - ref)) < 1e-12
+
+
+def test_feed_forward_bf16_equals_native_bf16_restatement():
+    """bf16 tensors round every op result: linear (matmul, bias add),
+    sigmoid, the product (nn::silu as two ops), linear2; then the half-step
+    residual 0.5 * y + x."""
+    p = _ffn_params(16, 64, 33)
+    x = O.bf16_round(np.random.default_rng(34).standard_normal((7, 16)))
+    bf = torch.bfloat16
+    t = lambda a: torch.tensor(np.asarray(a, dtype=np.float32)).to(bf)
+    X = t(x)
+    h = X @ t(p.linear1.weight).T + t(p.linear1.bias)
+    h = h * torch.sigmoid(h)
+    y = h @ t(p.linear2.weight).T + t(p.linear2.bias)
+    assert np.array_equal(O.feed_forward(p, x, O.BF16), y.double().numpy())
+    half = torch.tensor(0.5, dtype=bf)
+    s = (X + half * y).double().numpy()
+    yo = O.feed_forward(p, x, O.BF16)
+    assert np.array_equal(O.bf16_round(x + O.bf16_round(0.5 * yo)), s)
+    # the sublayer on an input whose LayerNorm is the identity-free case
+    sub = O.feed_forward_sublayer(p, x, dtype=O.BF16)
+    assert np.array_equal(sub, O.bf16_round(x + 0.5 * O.feed_forward(p, O.layer_norm(x, dtype=O.BF16), O.BF16)))
