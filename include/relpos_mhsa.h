@@ -297,6 +297,69 @@ int32_t mhsa_ffn_forward(mhsa_ffn* ffn, const void* x, int32_t rows, void* out, 
 int32_t mhsa_ffn_sublayer_forward(mhsa_ffn* ffn, void* x_inout, int32_t rows, const float* ln_gamma_host,
                                   const float* ln_beta_host, float eps, void* hip_stream);
 
+/* ---- ConvolutionModule (the Conformer block's convolution sublayer) ------- */
+
+/* ConvolutionModule (conformer.rs:2105-2437): pointwise_conv1 [2D, D] ->
+ * GLU (x1 * sigmoid(x2)) -> padding frames zeroed -> depthwise Conv1d
+ * (kernel_size K, groups = D; causal: K - 1 frames of left context, else
+ * (K - 1) / 2 zeros each side) -> BatchNorm (inference, running statistics)
+ * or LayerNorm -> SiLU -> pointwise_conv2 [D, D]. The pointwise convs are
+ * standard or MLX affine 8-bit linears (group 64) on the projection GEMMs;
+ * GLU, depthwise conv, BatchNorm and SiLU are one fused kernel.
+ * d_model a multiple of 64, K <= 129 (odd when not causal); LayerNorm needs
+ * d_model <= 2048. Dtypes follow MLX promotion as the reference writes it:
+ * a causal module pads with f32 zeros (conformer.rs:2250-2256) and the
+ * streaming cache is f32, so everything after the GLU is f32 unless the
+ * module is symmetric and runs offline (mhsa_conv_output_dtype). */
+#define MHSA_CONV_BATCH_NORM 0 /* ConvNormType::BatchNorm (asr/config.rs:119-128) */
+#define MHSA_CONV_LAYER_NORM 1 /* ConvNormType::LayerNorm */
+typedef struct mhsa_conv mhsa_conv;
+/* ConvolutionModule::new (conformer.rs:2138-2193): zero pointwise layers
+ * with zero biases, a zero depthwise kernel (bias when use_bias), the norm
+ * at its identity (weight 1, bias 0, running mean 0, variance 1). */
+int32_t mhsa_conv_create(int32_t d_model, int32_t kernel_size, int32_t norm_type, int32_t causal, int32_t use_bias,
+                         mhsa_conv** out);
+void mhsa_conv_destroy(mhsa_conv* conv);
+/* set_dtype (conformer.rs:2122-2136): MHSA_F32 or MHSA_BF16; BatchNorm's
+ * eps (1e-5) is cast with the parameters. */
+int32_t mhsa_conv_set_dtype(mhsa_conv* conv, int32_t dtype);
+/* load_weights (conformer.rs:2389-2427): {prefix}.pointwise_conv1 /
+ * .pointwise_conv2 as linears (.weight [O, I] or [O, 1, I], .bias, or
+ * .weight/.scales/.biases), {prefix}.depthwise_conv.weight [D, K, 1] (MLX
+ * layout) and .bias when use_bias, {prefix}.batch_norm.weight / .bias and,
+ * for BatchNorm, .running_mean / .running_var (prefix e.g.
+ * "encoder.layers.0.conv"). Strict: any missing tensor is MHSA_ENOENT. */
+int32_t mhsa_conv_load_weights(mhsa_conv* conv, const mhsa_tensor* tensors, int32_t n_tensors, const char* prefix,
+                               int32_t strict, int32_t quant_bits, int32_t quant_group);
+/* cache_size (conformer.rs:2384-2386): K - 1. */
+int32_t mhsa_conv_cache_size(const mhsa_conv* conv);
+/* The dtype mhsa_conv_forward writes: the module dtype for a symmetric
+ * module, MHSA_F32 for a causal one. */
+int32_t mhsa_conv_output_dtype(const mhsa_conv* conv);
+/* forward (conformer.rs:2197-2291): x [batch, seq_len, d_model] device, in
+ * the module dtype; lengths [batch] host (frames >= lengths[b] are padding,
+ * zeroed after the GLU; NULL = none); out [batch, seq_len, d_model] device
+ * in mhsa_conv_output_dtype. */
+int32_t mhsa_conv_forward(mhsa_conv* conv, const void* x, int32_t batch, int32_t seq_len, const int32_t* lengths,
+                          void* out, void* hip_stream);
+/* forward_with_cache (conformer.rs:2305-2378) on the streaming path's f32
+ * activations: x, out [batch, seq_len, d_model] f32 device; cache [batch,
+ * d_model, K - 1] f32 device (channel-major, as the reference's
+ * cache_last_time slice), the left context of the causal conv, replaced in
+ * place by the last K - 1 frames of [cache; GLU(x)]; NULL runs the no-cache
+ * path (zero left padding). lengths as in mhsa_conv_forward (the
+ * reference's pad_mask). A cache needs a causal module (MHSA_EINVAL). */
+int32_t mhsa_conv_forward_with_cache(mhsa_conv* conv, const float* x, int32_t batch, int32_t seq_len, float* cache,
+                                     const int32_t* lengths, float* out, void* hip_stream);
+/* The block's convolution sublayer x <- x + conv(LayerNorm(x))
+ * (conformer.rs:1790-1814; with cache 1936-1941), the residual fused into
+ * pointwise_conv2's epilogue. cache NULL: offline, x in the module dtype
+ * (MHSA_ENOTSUP for a causal bf16 module, whose f32 result x cannot hold);
+ * cache set: streaming, x f32. gamma/beta [d_model] host fp32 or NULL. */
+int32_t mhsa_conv_sublayer_forward(mhsa_conv* conv, void* x_inout, int32_t batch, int32_t seq_len, float* cache,
+                                   const int32_t* lengths, const float* ln_gamma_host, const float* ln_beta_host,
+                                   float eps, void* hip_stream);
+
 /* ---- encoder-level streaming ---------------------------------------------- */
 
 /* The per-chunk layer loop of ConformerEncoder::forward_streaming

@@ -69,6 +69,17 @@ template <> __device__ __forceinline__ float round_to<bf16>(float v) { return (f
 
 template <typename T> __device__ __forceinline__ T from_float(float v) { return (T)v; }
 
+// sigmoid(v) = 1 / (1 + e^-v) stored in T, and nn::silu as the reference
+// evaluates it: the sigmoid stored, then the product stored (conformer.rs:2069).
+template <typename T>
+__device__ __forceinline__ float sigmoid_value(float v) {
+  return round_to<T>(1.f / (1.f + expf(-v)));
+}
+template <typename T>
+__device__ __forceinline__ float silu_value(float v) {
+  return round_to<T>(v * sigmoid_value<T>(v));
+}
+
 template <typename T> __device__ __forceinline__ typename Frag<T>::type zero_frag();
 template <> __device__ __forceinline__ floatx4 zero_frag<float>() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
 template <> __device__ __forceinline__ bf16x8 zero_frag<bf16>() {

@@ -113,13 +113,6 @@ __device__ __forceinline__ int64_t mapped_row(const GemmParams& p, int row) {
 // C offset of one output row (computed once per row).
 __device__ __forceinline__ int64_t row_offset(const GemmParams& p, int row) { return mapped_row(p, row) * p.ldc; }
 
-// nn::silu as the reference evaluates it: sigmoid stored in the dtype, then
-// the product stored (conformer.rs:2069).
-template <typename T>
-__device__ __forceinline__ float silu_value(float v) {
-  return round_to<T>(v * round_to<T>(1.f / (1.f + expf(-v))));
-}
-
 // The reference's op order: round the product, add the bias, round, (SiLU,)
 // add the (scaled) residual, round.
 template <typename T>

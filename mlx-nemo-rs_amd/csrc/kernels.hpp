@@ -127,10 +127,37 @@ hipError_t export_mask(const AttnParams& p, int nbatch, uint8_t* out, hipStream_
 hipError_t export_pos_index(int T, int L, int qoff, int center, int32_t* out, hipStream_t s);
 
 // y = T(LayerNorm(x) * gamma + beta), statistics in fp32; gamma/beta may be null.
-// Rows are held in registers, one wave per row: D <= kMaxLayerNormDim.
+// act = kActSilu then applies nn::silu to the stored result (the conv
+// module's norm -> SiLU). Rows are held in registers, one wave per row:
+// D <= kMaxLayerNormDim; y may alias x.
 constexpr int kMaxLayerNormDim = 2048;
 hipError_t layer_norm(DType dt, const void* x, void* y, const float* gamma, const float* beta,
-                      float eps, int rows, int D, hipStream_t s);
+                      float eps, int rows, int D, hipStream_t s, int act = 0);
+
+// ConvolutionModule middle (conformer.rs:2197-2291, 2305-2378) for a batch
+// chunk: y[b, t, c] = post(sum_k w[k, c] * u[b, t - left + k, c] (+ bias[c]))
+// where u = GLU(g) = g[.., :D] * sigmoid(g[.., D:]) in the GLU dtype, zero
+// at frames >= len[b] and past T; frames before 0 come from cache_in
+// [b, c, K-1+s] (f32, channel-major) or are zero. post = BatchNorm (bn =
+// [4, D]: mean, rsqrt(var + eps), weight, bias) then SiLU when bn is set,
+// else nothing (LayerNorm runs afterwards). cache_out (may equal cache_in
+// only when one frame tile covers T) receives the last K - 1 frames of
+// [cache; u]. g [B, T, 2D], y [B, T, D]; D % 64 == 0, K <= kMaxConvKernel.
+constexpr int kMaxConvKernel = 129;
+struct ConvParams {
+  const void* g = nullptr;
+  void* y = nullptr;
+  const float* cache_in = nullptr;
+  float* cache_out = nullptr;
+  const float* w = nullptr;     // [K, D]
+  const float* bias = nullptr;  // [D] or null
+  const float* bn = nullptr;    // [4, D] or null
+  int T = 0, D = 0, K = 0, left = 0;
+  int len[kMaxBatch] = {};
+};
+hipError_t conv_glu_depthwise(DType glu_dt, DType conv_dt, const ConvParams& p, int nbatch, hipStream_t s);
+// Output frames one workgroup covers (a cache updated in place needs T <= this).
+int conv_frame_tile();
 
 // Ring copies between a contiguous [B, n, D] block and a ring [B, R, ld]
 // (row t of batch b <-> ring row (off + t) % R, columns [0, D)).

@@ -22,7 +22,7 @@
 #include <vector>
 
 #include "../../include/relpos_mhsa.h"
-#include "host_error.hpp"
+#include "host_common.hpp"
 #include "kernels.hpp"
 
 using mhsa::DType;
@@ -31,99 +31,6 @@ namespace {
 
 thread_local std::string g_err;
 
-int32_t fail(int32_t code, const char* fmt, ...) {
-  char buf[512];
-  va_list ap;
-  va_start(ap, fmt);
-  vsnprintf(buf, sizeof buf, fmt, ap);
-  va_end(ap);
-  g_err = buf;
-  return code;
-}
-
-#define HIPCHK(expr)                                                                               \
-  do {                                                                                             \
-    hipError_t e_ = (expr);                                                                        \
-    if (e_ != hipSuccess) return fail(MHSA_EHIP, "%s: %s (%s:%d)", #expr, hipGetErrorString(e_), \
-                                      __FILE__, __LINE__);                                         \
-  } while (0)
-
-float bits_to_f32(uint32_t u) {
-  float f;
-  std::memcpy(&f, &u, 4);
-  return f;
-}
-uint32_t f32_to_bits(float f) {
-  uint32_t u;
-  std::memcpy(&u, &f, 4);
-  return u;
-}
-// bf16 round-to-nearest-even (no NaNs on this path).
-uint16_t f32_to_bf16(float f) {
-  uint32_t u = f32_to_bits(f);
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-float bf16_to_f32(uint16_t b) { return bits_to_f32((uint32_t)b << 16); }
-float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
-float f16_to_f32(uint16_t h) {
-  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
-  uint32_t exp = (h >> 10) & 0x1Fu, man = h & 0x3FFu;
-  if (exp == 0) {
-    if (man == 0) return bits_to_f32(sign);
-    // subnormal: value = man * 2^-24
-    float v = std::ldexp((float)man, -24);
-    return sign ? -v : v;
-  }
-  if (exp == 31) return bits_to_f32(sign | 0x7F800000u | (man << 13));
-  return bits_to_f32(sign | ((exp + 112u) << 23) | (man << 13));
-}
-
-float load_host(int32_t dtype, const void* data, size_t i) {
-  switch (dtype) {
-    case MHSA_F32: return static_cast<const float*>(data)[i];
-    case MHSA_BF16: return bf16_to_f32(static_cast<const uint16_t*>(data)[i]);
-    case MHSA_F16: return f16_to_f32(static_cast<const uint16_t*>(data)[i]);
-    default: return 0.f;
-  }
-}
-bool float_dtype(int32_t d) { return d == MHSA_F32 || d == MHSA_BF16 || d == MHSA_F16; }
-
-struct HostLinear {
-  bool quantized = false;
-  std::vector<float> w;          // standard [out, in]
-  std::vector<float> bias;       // [out], empty = none
-  std::vector<uint32_t> codes;   // quantized [out, in/4]
-  std::vector<float> qs, qb;     // quantized scales / biases [out, in/64]
-};
-
-struct DevLinear {
-  bool quantized = false;
-  const void* w = nullptr;   // dense [N, K] (compute dtype) or u32 codes
-  const float* sb = nullptr; // [N, K/64, 2]
-  const float* bias = nullptr;
-};
-
-struct DevBuf {
-  void* p = nullptr;
-  size_t n = 0;
-  ~DevBuf() { release(); }
-  void release() {
-    if (p) (void)hipFree(p);
-    p = nullptr;
-    n = 0;
-  }
-  hipError_t ensure(size_t bytes) {
-    if (bytes <= n) return hipSuccess;
-    release();
-    hipError_t e = hipMalloc(&p, bytes);
-    if (e == hipSuccess) n = bytes;
-    else p = nullptr;
-    return e;
-  }
-};
-
-int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 // Per-kernel HIP-event timing on the launch stream (off unless enabled).
 struct Profiler {
@@ -502,7 +409,6 @@ int32_t check_layer(const mhsa_layer* L) {
   return MHSA_OK;
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // Offline forward shared by mhsa_forward, the sublayer and the debug export.
 // Debug outputs of the attention kernel (all null in the product path).
@@ -1538,264 +1444,6 @@ int32_t mhsa_debug_top_keys(mhsa_layer* L, const void* x, int32_t B, int32_t T, 
   if (p_out) HIPCHK(hipMemcpyAsync(p_out, L->last_pos, (size_t)pos_len * row, hipMemcpyDeviceToDevice, s));
   HIPCHK(hipStreamSynchronize(s));
   return MHSA_OK;
-}
-
-}  // extern "C"
-
-// ---------------------------------------------------------------------------
-// FeedForward (conformer.rs:2031-2088): linear2(silu(linear1(x))), each
-// projection standard or MLX affine 8-bit, on the projection GEMMs with a
-// SiLU epilogue; and the block's half-step sublayer x + 0.5 FF(LN(x))
-// (conformer.rs:1703-1729, 1827-1851).
-// ---------------------------------------------------------------------------
-
-struct mhsa_ffn {
-  int D = 0, F = 0;
-  bool use_bias = false;
-  DType dt = mhsa::kF32;
-  HostLinear lin[2];  // linear1 [F, D], linear2 [D, F]
-  bool dirty = true;
-  DevBuf wbuf;
-  DevLinear dev[2];
-  DevBuf act;      // [rows, F] silu(linear1(x))
-  DevBuf hbuf;     // sublayer: LayerNorm output
-  DevBuf ln_dev;
-  std::vector<float> ln_host;
-  DevBuf partial;  // split-K partials of small problems
-};
-
-namespace {
-
-int ffn_out(const mhsa_ffn* f, int i) { return i == 0 ? f->F : f->D; }
-int ffn_in(const mhsa_ffn* f, int i) { return i == 0 ? f->D : f->F; }
-
-int32_t prepare_ffn(mhsa_ffn* f) {
-  if (!f->dirty) return MHSA_OK;
-  const bool bf = f->dt == mhsa::kBF16;
-  const size_t es = bf ? 2 : 4;
-  auto rnd = [&](float v) { return bf ? round_bf16(v) : v; };
-  size_t woff[2], sboff[2], boff[2], off = 0;
-  for (int i = 0; i < 2; ++i) {
-    const size_t n = (size_t)ffn_out(f, i) * ffn_in(f, i);
-    woff[i] = off;
-    off = align_up(off + (f->lin[i].quantized ? n : n * es), 256);
-    sboff[i] = off;
-    if (f->lin[i].quantized) off = align_up(off + (size_t)ffn_out(f, i) * (ffn_in(f, i) / 64) * 8, 256);
-    boff[i] = off;
-    off = align_up(off + (size_t)ffn_out(f, i) * 4, 256);
-  }
-  std::vector<char> host(off, 0);
-  for (int i = 0; i < 2; ++i) {
-    const HostLinear& h = f->lin[i];
-    if (h.quantized) {
-      std::memcpy(host.data() + woff[i], h.codes.data(), h.codes.size() * 4);
-      float* sb = reinterpret_cast<float*>(host.data() + sboff[i]);
-      for (size_t e = 0; e < h.qs.size(); ++e) {
-        sb[2 * e] = rnd(h.qs[e]);
-        sb[2 * e + 1] = rnd(h.qb[e]);
-      }
-    } else if (bf) {
-      uint16_t* w = reinterpret_cast<uint16_t*>(host.data() + woff[i]);
-      for (size_t e = 0; e < h.w.size(); ++e) w[e] = f32_to_bf16(h.w[e]);
-    } else {
-      std::memcpy(host.data() + woff[i], h.w.data(), h.w.size() * 4);
-    }
-    float* b = reinterpret_cast<float*>(host.data() + boff[i]);
-    for (size_t e = 0; e < h.bias.size(); ++e) b[e] = rnd(h.bias[e]);
-  }
-  if (f->wbuf.p) HIPCHK(hipDeviceSynchronize());  // earlier launches may still read the old values
-  HIPCHK(f->wbuf.ensure(host.size()));
-  HIPCHK(hipMemcpy(f->wbuf.p, host.data(), host.size(), hipMemcpyHostToDevice));
-  const char* base = static_cast<const char*>(f->wbuf.p);
-  for (int i = 0; i < 2; ++i) {
-    f->dev[i].quantized = f->lin[i].quantized;
-    f->dev[i].w = base + woff[i];
-    f->dev[i].sb = f->lin[i].quantized ? reinterpret_cast<const float*>(base + sboff[i]) : nullptr;
-    f->dev[i].bias = f->lin[i].bias.empty() ? nullptr : reinterpret_cast<const float*>(base + boff[i]);
-  }
-  f->dirty = false;
-  return MHSA_OK;
-}
-
-int32_t ffn_impl(mhsa_ffn* f, const void* x, int rows, void* out, const void* residual, float res_scale,
-                 hipStream_t s) {
-  if (rows <= 0) return fail(MHSA_EINVAL, "rows must be positive (got %d)", rows);
-  if (!x || !out) return fail(MHSA_EINVAL, "null tensor pointer");
-  if (!aligned16(x) || !aligned16(out)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
-  int32_t rc = prepare_ffn(f);
-  if (rc) return rc;
-  const size_t es = f->dt == mhsa::kBF16 ? 2 : 4;
-  HIPCHK(f->act.ensure(align_up((int64_t)rows * f->F * es, 256)));
-  HIPCHK(f->partial.ensure((size_t)mhsa::kGemmPartialElems * 4));
-  for (int i = 0; i < 2; ++i) {
-    mhsa::GemmParams p;
-    p.A = i == 0 ? x : f->act.p;
-    p.lda = ffn_in(f, i);
-    p.W = f->dev[i].w;
-    p.sb = f->dev[i].sb;
-    p.bias = f->dev[i].bias;
-    p.C = i == 0 ? f->act.p : out;
-    p.ldc = ffn_out(f, i);
-    p.M = rows;
-    p.N = ffn_out(f, i);
-    p.K = ffn_in(f, i);
-    p.seg_rows = rows;
-    p.ring_len = rows;
-    p.partial = static_cast<float*>(f->partial.p);
-    p.partial_elems = mhsa::kGemmPartialElems;
-    if (i == 0) p.act = mhsa::kActSilu;
-    if (i == 1 && residual) {
-      p.R = residual;
-      p.ldr = f->D;
-      p.res_scale = res_scale;
-    }
-    HIPCHK(mhsa::gemm(f->dt, f->dev[i].quantized, p, s));
-  }
-  return MHSA_OK;
-}
-
-}  // namespace
-
-extern "C" {
-
-int32_t mhsa_ffn_create(int32_t d_model, int32_t ff_dim, int32_t use_bias, mhsa_ffn** out) {
-  if (!out) return fail(MHSA_EINVAL, "null output pointer");
-  *out = nullptr;
-  if (d_model <= 0 || ff_dim <= 0 || d_model % 64 || ff_dim % 64)
-    return fail(MHSA_EINVAL, "d_model %d and ff_dim %d must be positive multiples of 64", d_model, ff_dim);
-  mhsa_ffn* f = new (std::nothrow) mhsa_ffn();
-  if (!f) return fail(MHSA_ENOMEM, "out of host memory");
-  f->D = d_model;
-  f->F = ff_dim;
-  f->use_bias = use_bias != 0;
-  for (int i = 0; i < 2; ++i) {  // zero-initialised layers (conformer.rs:2046-2064)
-    f->lin[i].w.assign((size_t)ffn_out(f, i) * ffn_in(f, i), 0.f);
-    if (use_bias) f->lin[i].bias.assign(ffn_out(f, i), 0.f);
-  }
-  *out = f;
-  return MHSA_OK;
-}
-
-void mhsa_ffn_destroy(mhsa_ffn* f) { delete f; }
-
-int32_t mhsa_ffn_set_dtype(mhsa_ffn* f, int32_t dtype) {
-  if (!f) return fail(MHSA_EINVAL, "null handle");
-  if (dtype != MHSA_F32 && dtype != MHSA_BF16) return fail(MHSA_ENOTSUP, "dtype %d not supported (f32, bf16)", dtype);
-  f->dt = dtype == MHSA_F32 ? mhsa::kF32 : mhsa::kBF16;
-  f->dirty = true;
-  return MHSA_OK;
-}
-
-int32_t mhsa_ffn_load_weights(mhsa_ffn* f, const mhsa_tensor* tensors, int32_t n, const char* prefix, int32_t strict,
-                              int32_t quant_bits, int32_t quant_group) {
-  if (!f) return fail(MHSA_EINVAL, "null handle");
-  if ((n > 0 && !tensors) || !prefix) return fail(MHSA_EINVAL, "null tensor list or prefix");
-  auto find = [&](const std::string& key) -> const mhsa_tensor* {
-    for (int i = 0; i < n; ++i)
-      if (tensors[i].name && key == tensors[i].name) return &tensors[i];
-    return nullptr;
-  };
-  auto numel = [](const mhsa_tensor* t) {
-    int64_t e = 1;
-    for (int i = 0; i < t->ndim; ++i) e *= t->shape[i];
-    return e;
-  };
-  const int bits = quant_bits > 0 ? quant_bits : 8, group = quant_group > 0 ? quant_group : 64;
-  const char* names[2] = {"linear1", "linear2"};
-  HostLinear next[2] = {f->lin[0], f->lin[1]};
-  for (int i = 0; i < 2; ++i) {  // FeedForward::load_weights via fetch_linear (conformer.rs:2074-2087)
-    const std::string p = std::string(prefix) + "." + names[i];
-    const int O = ffn_out(f, i), I = ffn_in(f, i);
-    const mhsa_tensor* w = find(p + ".weight");
-    const mhsa_tensor* sc = find(p + ".scales");
-    const mhsa_tensor* qb = find(p + ".biases");
-    const mhsa_tensor* b = find(p + ".bias");
-    HostLinear& h = next[i];
-    if (w && sc && qb) {  // quantization.rs:299-304
-      if (bits != 8 || group != 64)
-        return fail(MHSA_ENOTSUP, "`%s`: quantization bits=%d group_size=%d not supported (8, 64)", p.c_str(), bits,
-                    group);
-      if (w->dtype != MHSA_U32 || sc->dtype != MHSA_F16 || qb->dtype != MHSA_F16 || numel(w) != (int64_t)O * I / 4 ||
-          numel(sc) != (int64_t)O * I / 64 || numel(qb) != numel(sc))
-        return fail(MHSA_EINVAL, "`%s`: expected u32 [%d, %d] and f16 [%d, %d] scales/biases", p.c_str(), O, I / 4, O,
-                    I / 64);
-      h.quantized = true;
-      h.w.clear();
-      const uint32_t* wp = static_cast<const uint32_t*>(w->data);
-      h.codes.assign(wp, wp + (size_t)O * I / 4);
-      h.qs.resize((size_t)O * I / 64);
-      h.qb.resize(h.qs.size());
-      for (size_t e = 0; e < h.qs.size(); ++e) {
-        h.qs[e] = f16_to_f32(static_cast<const uint16_t*>(sc->data)[e]);
-        h.qb[e] = f16_to_f32(static_cast<const uint16_t*>(qb->data)[e]);
-      }
-    } else if (w) {
-      const bool shape_ok = (w->ndim == 2 && w->shape[0] == O && w->shape[1] == I) ||
-                            (w->ndim == 3 && w->shape[0] == O && w->shape[1] == 1 && w->shape[2] == I);
-      if (!shape_ok || !float_dtype(w->dtype)) return fail(MHSA_EINVAL, "`%s.weight`: expected float [%d, %d]", p.c_str(), O, I);
-      h.quantized = false;
-      h.codes.clear();
-      h.qs.clear();
-      h.qb.clear();
-      h.w.resize((size_t)O * I);
-      for (size_t e = 0; e < h.w.size(); ++e) h.w[e] = load_host(w->dtype, w->data, e);
-    } else if (strict) {
-      return fail(MHSA_ENOENT, "missing weight `%s.weight`", p.c_str());
-    } else {
-      continue;
-    }
-    if (b) {
-      if (!float_dtype(b->dtype) || numel(b) != O) return fail(MHSA_EINVAL, "`%s.bias`: expected float [%d]", p.c_str(), O);
-      h.bias.resize(O);
-      for (int e = 0; e < O; ++e) h.bias[e] = load_host(b->dtype, b->data, e);
-    } else if (!f->use_bias) {
-      h.bias.clear();
-    }
-  }
-  f->lin[0] = std::move(next[0]);
-  f->lin[1] = std::move(next[1]);
-  f->dirty = true;
-  return MHSA_OK;
-}
-
-int32_t mhsa_ffn_forward(mhsa_ffn* f, const void* x, int32_t rows, void* out, void* hs) {
-  if (!f) return fail(MHSA_EINVAL, "null handle");
-  return ffn_impl(f, x, rows, out, nullptr, 1.f, static_cast<hipStream_t>(hs));
-}
-
-int32_t mhsa_ffn_sublayer_forward(mhsa_ffn* f, void* x, int32_t rows, const float* gamma, const float* beta, float eps,
-                                  void* hs) {
-  if (!f) return fail(MHSA_EINVAL, "null handle");
-  if (!x || rows <= 0) return fail(MHSA_EINVAL, "bad sublayer arguments");
-  if (!aligned16(x)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
-  if (f->D > mhsa::kMaxLayerNormDim)
-    return fail(MHSA_ENOTSUP, "the sublayer's LayerNorm supports d_model <= %d (got %d)", mhsa::kMaxLayerNormDim, f->D);
-  hipStream_t s = static_cast<hipStream_t>(hs);
-  const int D = f->D;
-  const float* gd = nullptr;
-  const float* bd = nullptr;
-  if (gamma || beta) {
-    std::vector<float> tmp(2 * D);
-    const bool bf = f->dt == mhsa::kBF16;
-    for (int i = 0; i < D; ++i) {
-      const float gv = gamma ? gamma[i] : 1.f, bv = beta ? beta[i] : 0.f;
-      tmp[i] = bf ? round_bf16(gv) : gv;
-      tmp[D + i] = bf ? round_bf16(bv) : bv;
-    }
-    if (tmp != f->ln_host) {
-      if (f->ln_dev.p) HIPCHK(hipDeviceSynchronize());
-      HIPCHK(f->ln_dev.ensure(tmp.size() * 4));
-      HIPCHK(hipMemcpy(f->ln_dev.p, tmp.data(), tmp.size() * 4, hipMemcpyHostToDevice));
-      f->ln_host = tmp;
-    }
-    gd = static_cast<const float*>(f->ln_dev.p);
-    bd = gd + D;
-  }
-  const size_t es = f->dt == mhsa::kBF16 ? 2 : 4;
-  HIPCHK(f->hbuf.ensure(align_up((int64_t)rows * D * es, 256)));
-  HIPCHK(mhsa::layer_norm(f->dt, x, f->hbuf.p, gd, bd, eps, rows, D, s));
-  // x + 0.5 * FF(LN(x)): the half step scales exactly (conformer.rs:1727-1729)
-  return ffn_impl(f, f->hbuf.p, rows, x, x, 0.5f, s);
 }
 
 }  // extern "C"

@@ -14,7 +14,7 @@ namespace {
 // One wave per row; two-pass statistics in fp32 from registers.
 template <typename T, int VPL>
 __global__ __launch_bounds__(256) void ln_kernel(const T* x, T* y, const float* gamma, const float* beta,
-                                                 float eps, int rows, int D) {
+                                                 float eps, int rows, int D, int act) {
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
@@ -46,6 +46,7 @@ __global__ __launch_bounds__(256) void ln_kernel(const T* x, T* y, const float* 
       float t = (v[i] - mean) * rstd;
       if (gamma) t *= gamma[c];
       if (beta) t += beta[c];
+      if (act == kActSilu) t = silu_value<T>(round_to<T>(t));
       yr[c] = from_float<T>(t);
     }
   }
@@ -55,7 +56,7 @@ __global__ __launch_bounds__(256) void ln_kernel(const T* x, T* y, const float* 
 // (D a multiple of 64 chunks), gamma and beta read as float4.
 template <typename T, int NCH>
 __global__ __launch_bounds__(256) void ln_vec_kernel(const T* x, T* y, const float* gamma, const float* beta,
-                                                     float eps, int rows, int D) {
+                                                     float eps, int rows, int D, int act) {
   constexpr int E = 16 / sizeof(T);  // elements per chunk
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -99,6 +100,7 @@ __global__ __launch_bounds__(256) void ln_vec_kernel(const T* x, T* y, const flo
         float t = (v[j][e4 + e] - mean) * rstd;
         if (gamma) t *= g[e];
         if (beta) t += b[e];
+        if (act == kActSilu) t = silu_value<T>(round_to<T>(t));
         out[e4 + e] = from_float<T>(t);
       }
     }
@@ -107,7 +109,7 @@ __global__ __launch_bounds__(256) void ln_vec_kernel(const T* x, T* y, const flo
 }
 
 template <typename T>
-hipError_t ln_launch(const void* x, void* y, const float* g, const float* b, float eps, int rows, int D,
+hipError_t ln_launch(const void* x, void* y, const float* g, const float* b, float eps, int rows, int D, int act,
                      hipStream_t s) {
   dim3 grid((rows + 3) / 4);
   constexpr int E = 16 / sizeof(T);
@@ -116,24 +118,24 @@ hipError_t ln_launch(const void* x, void* y, const float* g, const float* b, flo
   if (aligned && D % (64 * E) == 0) {
     switch (D / (64 * E)) {
       case 1:
-        hipLaunchKernelGGL((ln_vec_kernel<T, 1>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
+        hipLaunchKernelGGL((ln_vec_kernel<T, 1>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D, act);
         return hipGetLastError();
       case 2:
-        hipLaunchKernelGGL((ln_vec_kernel<T, 2>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
+        hipLaunchKernelGGL((ln_vec_kernel<T, 2>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D, act);
         return hipGetLastError();
       case 4:
-        hipLaunchKernelGGL((ln_vec_kernel<T, 4>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
+        hipLaunchKernelGGL((ln_vec_kernel<T, 4>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D, act);
         return hipGetLastError();
       default:
         break;
     }
   }
   if (D <= 512)
-    hipLaunchKernelGGL((ln_kernel<T, 8>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
+    hipLaunchKernelGGL((ln_kernel<T, 8>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D, act);
   else if (D <= 1024)
-    hipLaunchKernelGGL((ln_kernel<T, 16>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
+    hipLaunchKernelGGL((ln_kernel<T, 16>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D, act);
   else
-    hipLaunchKernelGGL((ln_kernel<T, 32>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D);
+    hipLaunchKernelGGL((ln_kernel<T, 32>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D, act);
   return hipGetLastError();
 }
 
@@ -209,11 +211,11 @@ hipError_t fill_zero(void* ptr, size_t bytes, hipStream_t s) {
 }
 
 hipError_t layer_norm(DType dt, const void* x, void* y, const float* gamma, const float* beta, float eps, int rows,
-                      int D, hipStream_t s) {
+                      int D, hipStream_t s, int act) {
   if (rows <= 0) return hipSuccess;
   if (!x || !y || D <= 0 || D > kMaxLayerNormDim) return hipErrorInvalidValue;
-  return dt == kF32 ? ln_launch<float>(x, y, gamma, beta, eps, rows, D, s)
-                    : ln_launch<bf16>(x, y, gamma, beta, eps, rows, D, s);
+  return dt == kF32 ? ln_launch<float>(x, y, gamma, beta, eps, rows, D, act, s)
+                    : ln_launch<bf16>(x, y, gamma, beta, eps, rows, D, act, s);
 }
 
 static hipError_t ring_copy(DType dt, const void* src, void* dst, int B, int n, int D, int R, int64_t ld, int off,

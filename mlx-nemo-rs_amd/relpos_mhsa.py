@@ -39,7 +39,9 @@ EXPORTS = (
     "mhsa_stream_read_cache", "mhsa_stream_fill", "mhsa_forward_with_cache", "mhsa_forward_uncached",
     "mhsa_stack_create", "mhsa_stack_destroy", "mhsa_stack_load_cache", "mhsa_stack_read_cache", "mhsa_stack_fill",
     "mhsa_stack_step", "mhsa_ffn_create", "mhsa_ffn_destroy", "mhsa_ffn_set_dtype", "mhsa_ffn_load_weights",
-    "mhsa_ffn_forward", "mhsa_ffn_sublayer_forward",
+    "mhsa_ffn_forward", "mhsa_ffn_sublayer_forward", "mhsa_conv_create", "mhsa_conv_destroy", "mhsa_conv_set_dtype",
+    "mhsa_conv_load_weights", "mhsa_conv_cache_size", "mhsa_conv_output_dtype", "mhsa_conv_forward",
+    "mhsa_conv_forward_with_cache", "mhsa_conv_sublayer_forward",
     "mhsa_pos_encoding",
     "mhsa_debug_dequantize", "mhsa_debug_linear", "mhsa_debug_offline_mask", "mhsa_debug_stream_mask", "mhsa_debug_rel_shift_index",
     "mhsa_debug_position_scores", "mhsa_debug_top_keys", "mhsa_profile_enable", "mhsa_profile_repeat",
@@ -129,6 +131,15 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_ffn_load_weights": (I, [VP, P(Tensor), I, ctypes.c_char_p, I, I, I]),
         "mhsa_ffn_forward": (I, [VP, VP, I, VP, VP]),
         "mhsa_ffn_sublayer_forward": (I, [VP, VP, I, P(ctypes.c_float), P(ctypes.c_float), F, VP]),
+        "mhsa_conv_create": (I, [I, I, I, I, I, P(VP)]),
+        "mhsa_conv_destroy": (None, [VP]),
+        "mhsa_conv_set_dtype": (I, [VP, I]),
+        "mhsa_conv_load_weights": (I, [VP, P(Tensor), I, ctypes.c_char_p, I, I, I]),
+        "mhsa_conv_cache_size": (I, [VP]),
+        "mhsa_conv_output_dtype": (I, [VP]),
+        "mhsa_conv_forward": (I, [VP, VP, I, I, PI, VP, VP]),
+        "mhsa_conv_forward_with_cache": (I, [VP, VP, I, I, VP, PI, VP, VP]),
+        "mhsa_conv_sublayer_forward": (I, [VP, VP, I, I, VP, PI, P(ctypes.c_float), P(ctypes.c_float), F, VP]),
         "mhsa_pos_encoding": (I, [I, I, I, P(ctypes.c_float)]),
         "mhsa_debug_dequantize": (I, [VP, I, VP, VP]),
         "mhsa_debug_linear": (I, [VP, I, VP, I, VP, VP]),
@@ -366,6 +377,111 @@ class FeedForward:
                                                    None if g is None else g.ctypes.data_as(fp),
                                                    None if b is None else b.ctypes.data_as(fp), float(eps),
                                                    _stream_ptr()))
+        return x
+
+
+CONV_BATCH_NORM, CONV_LAYER_NORM = 0, 1
+
+
+class ConvolutionModule:
+    """ConvolutionModule (conformer.rs:2105-2437) backed by the HIP library.
+
+    norm: "batch_norm" or "layer_norm" (ConvNormType, asr/config.rs:119-128).
+    A causal module's output is f32 whatever its dtype (the f32 causal
+    padding and conv cache promote, conformer.rs:2250-2256, 2328-2336)."""
+
+    def __init__(self, d_model: int, kernel_size: int, norm: str = "batch_norm", causal: bool = False,
+                 use_bias: bool = True):
+        codes = {"batch_norm": CONV_BATCH_NORM, "layer_norm": CONV_LAYER_NORM}
+        if norm not in codes:
+            raise MhsaError(MHSA_ENOTSUP, f"conv_norm_type `{norm}` (only batch_norm and layer_norm are supported)")
+        lib = library()
+        h = ctypes.c_void_p()
+        _check(lib.mhsa_conv_create(d_model, kernel_size, codes[norm], 1 if causal else 0, 1 if use_bias else 0,
+                                    ctypes.byref(h)))
+        self._h, self._lib = h, lib
+        self.d_model, self.kernel_size, self.causal = d_model, kernel_size, causal
+        self._dtype = F32
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            self._lib.mhsa_conv_destroy(h)
+            self._h = None
+
+    def set_dtype(self, dtype) -> None:
+        self._dtype = _dtype_code(dtype)
+        _check(self._lib.mhsa_conv_set_dtype(self._h, self._dtype))
+
+    def cache_size(self) -> int:
+        return self._lib.mhsa_conv_cache_size(self._h)
+
+    def output_dtype(self):
+        return _torch_dtype(self._lib.mhsa_conv_output_dtype(self._h))
+
+    def load_weights(self, weights: Dict[str, np.ndarray], prefix: str,
+                     quant: Optional[QuantizationConfig] = None, strict: bool = True) -> None:
+        arr_t, n, keep = _tensor_list(weights)
+        bits, group = (quant.bits, quant.group_size) if quant else (0, 0)
+        _check(self._lib.mhsa_conv_load_weights(self._h, arr_t, n, prefix.encode(), 1 if strict else 0, bits, group))
+
+    def _check_x(self, x, dtype):
+        if not x.is_cuda or x.dtype != dtype or not x.is_contiguous() or x.dim() != 3 or x.shape[-1] != self.d_model:
+            raise MhsaError(MHSA_EINVAL, f"expected a contiguous {dtype} GPU tensor [B, T, {self.d_model}]")
+
+    def _lens(self, lengths, batch):
+        if lengths is None:
+            return None
+        lens = _int_array(lengths)
+        if len(lens) != batch:
+            raise MhsaError(MHSA_EINVAL, f"lengths must have {batch} entries")
+        return lens
+
+    def _check_cache(self, cache, x):
+        import torch
+        want = (x.shape[0], self.d_model, self.cache_size())
+        if (not cache.is_cuda or cache.dtype != torch.float32 or not cache.is_contiguous()
+                or tuple(cache.shape) != want or cache.device != x.device):
+            raise MhsaError(MHSA_EINVAL, f"cache must be a contiguous float32 GPU tensor {list(want)} on x's device")
+
+    def forward(self, x, lengths=None):
+        """forward (conformer.rs:2197-2291); lengths [B] (frames past them are padding)."""
+        import torch
+        self._check_x(x, _torch_dtype(self._dtype))
+        out = torch.empty(x.shape, dtype=self.output_dtype(), device=x.device)
+        _check(self._lib.mhsa_conv_forward(self._h, _dptr(x), x.shape[0], x.shape[1],
+                                           self._lens(lengths, x.shape[0]), _dptr(out), _stream_ptr()))
+        return out
+
+    def forward_with_cache(self, x, cache=None, lengths=None):
+        """forward_with_cache (conformer.rs:2305-2378) on f32 x; `cache`
+        [B, D, K-1] f32 is updated in place (the returned new cache)."""
+        import torch
+        self._check_x(x, torch.float32)
+        if cache is not None:
+            self._check_cache(cache, x)
+        out = torch.empty_like(x)
+        _check(self._lib.mhsa_conv_forward_with_cache(self._h, _dptr(x), x.shape[0], x.shape[1],
+                                                      None if cache is None else _dptr(cache),
+                                                      self._lens(lengths, x.shape[0]), _dptr(out), _stream_ptr()))
+        return out, cache
+
+    def sublayer_forward_(self, x, gamma=None, beta=None, eps=1e-5, cache=None, lengths=None):
+        """In place x <- x + forward(LayerNorm(x)) (conformer.rs:1790-1814),
+        or with the cache on f32 x (conformer.rs:1936-1941)."""
+        import torch
+        self._check_x(x, torch.float32 if cache is not None else _torch_dtype(self._dtype))
+        if cache is not None:
+            self._check_cache(cache, x)
+        g = None if gamma is None else _host_f32(gamma)
+        b = None if beta is None else _host_f32(beta)
+        fp = ctypes.POINTER(ctypes.c_float)
+        _check(self._lib.mhsa_conv_sublayer_forward(self._h, _dptr(x), x.shape[0], x.shape[1],
+                                                    None if cache is None else _dptr(cache),
+                                                    self._lens(lengths, x.shape[0]),
+                                                    None if g is None else g.ctypes.data_as(fp),
+                                                    None if b is None else b.ctypes.data_as(fp), float(eps),
+                                                    _stream_ptr()))
         return x
 
 

@@ -658,6 +658,148 @@ def feed_forward_sublayer(p: FeedForwardParams, x, gamma=None, beta=None, dtype:
 
 
 # ---------------------------------------------------------------------------
+# ConvolutionModule (conformer.rs:2105-2437) and its sublayer
+# ---------------------------------------------------------------------------
+
+@dataclass
+class ConvModuleParams:
+    """ConvolutionModule (conformer.rs:2105-2193). depthwise_weight is in the
+    MLX Conv1d layout [D, K, 1] (loading.rs:216-224); norm is "batch_norm"
+    (weight, bias, running_mean, running_var) or "layer_norm" (weight, bias),
+    both loaded from `{prefix}.batch_norm` (conformer.rs:2419-2426)."""
+
+    pointwise_conv1: LinearLayer
+    depthwise_weight: np.ndarray
+    depthwise_bias: Optional[np.ndarray]
+    pointwise_conv2: LinearLayer
+    norm: str
+    norm_weight: np.ndarray
+    norm_bias: np.ndarray
+    running_mean: Optional[np.ndarray] = None
+    running_var: Optional[np.ndarray] = None
+    causal: bool = False
+
+    @property
+    def kernel_size(self) -> int:
+        return int(self.depthwise_weight.shape[1])
+
+
+def sigmoid(x: np.ndarray, dtype: str = F32) -> np.ndarray:
+    """mlx sigmoid, the result stored in `dtype` (float64 inside)."""
+    return _rnd(1.0 / (1.0 + np.exp(-np.asarray(x, dtype=np.float64))), dtype)
+
+
+def glu(h: np.ndarray, d_model: int, dtype: str) -> np.ndarray:
+    """conformer.rs:2221-2226: x1 * sigmoid(x2) over the two channel halves,
+    the sigmoid and the product each stored in `dtype`."""
+    return _rnd(h[..., :d_model] * sigmoid(h[..., d_model:], dtype), dtype)
+
+
+def depthwise_conv1d(u: np.ndarray, weight, bias, pad_left: int, pad_right: int,
+                     dtype: str, param_dtype: str) -> np.ndarray:
+    """nn::Conv1d with groups = channels on [B, L, D] (cross-correlation:
+    y[t, c] = sum_k w[c, k] * u_pad[t + k, c]), the conv result stored in
+    `dtype`, then the bias add stored (mlx Conv1d forward). Weights carry
+    their `param_dtype` values; zero padding on each side."""
+    w = to_dtype(np.asarray(weight, dtype=np.float64)[:, :, 0], param_dtype)  # [D, K]
+    k = w.shape[1]
+    u = np.asarray(u, dtype=np.float64)
+    b_, l_, d_ = u.shape
+    up = np.zeros((b_, pad_left + l_ + pad_right, d_))
+    up[:, pad_left:pad_left + l_] = u
+    t_out = up.shape[1] - k + 1
+    y = np.zeros((b_, t_out, d_))
+    for j in range(k):
+        y += up[:, j:j + t_out, :] * w[:, j]
+    y = _rnd(y, dtype)
+    if bias is not None:
+        y = _rnd(y + to_dtype(bias, param_dtype), dtype)
+    return y
+
+
+def batch_norm_inference(x, mean, var, weight, bias, dtype: str, param_dtype: str,
+                         eps: float = 1e-5) -> np.ndarray:
+    """mlx-rs 0.32 nn::BatchNorm with training = false (conformer.rs:2155-2163,
+    loading.rs:236-254): (x - running_mean) * rsqrt(running_var + eps), then
+    weight * x + bias, each op stored in its result dtype. The parameters and
+    eps hold their `param_dtype` values (eps cast in set_dtype,
+    conformer.rs:2127-2130), so rsqrt(var + eps) involves parameters only and
+    is stored in `param_dtype`; the ops with x are stored in `dtype`."""
+    e = _rnd(to_dtype(var, param_dtype) + to_dtype(eps, param_dtype), param_dtype)
+    inv = _rnd(1.0 / np.sqrt(e), param_dtype)
+    y = _rnd(np.asarray(x, dtype=np.float64) - to_dtype(mean, param_dtype), dtype)
+    y = _rnd(y * inv, dtype)
+    y = _rnd(to_dtype(weight, param_dtype) * y, dtype)
+    return _rnd(y + to_dtype(bias, param_dtype), dtype)
+
+
+def _pointwise(layer: LinearLayer, x, act: str, dtype: str):
+    """A pointwise conv on activations stored in `act`: in the module dtype
+    (`forward`) or f32 with the cast parameters promoted (`forward_promoted`)."""
+    if act == dtype:
+        return layer.forward(x, dtype)
+    return layer.forward_promoted(x, dtype)
+
+
+def conv_module(p: ConvModuleParams, x, dtype: str = F32, act: Optional[str] = None,
+                lengths=None, cache=None):
+    """ConvolutionModule::forward (conformer.rs:2197-2291) and
+    ::forward_with_cache (conformer.rs:2305-2378) on x [B, T, D].
+
+    `dtype` is the module dtype (set_dtype), `act` the dtype x is stored in
+    (default `dtype`; the streaming path feeds f32). `lengths` [B]: frames
+    t >= lengths[b] are zeroed after the GLU (PaddingMask.valid / pad_mask).
+    `cache` [B, D, K-1] (f32) is the conv cache: the conv then runs over
+    [cache; GLU(x)] and the new cache is its last K-1 frames; without it a
+    causal module pads K-1 zero frames on the left, a symmetric one (K-1)/2
+    on each side. The causal padding and the cache are f32 arrays, so in a
+    bf16 module MLX promotes the concatenation and everything after it to
+    f32 (conformer.rs:2250-2256, 2328-2336). Returns (out, new_cache)."""
+    act = act or dtype
+    x = np.asarray(x, dtype=np.float64)
+    b_, t_, d_ = x.shape
+    k = p.kernel_size
+    u = glu(_pointwise(p.pointwise_conv1, x, act, dtype), d_, act)
+    if lengths is not None:
+        valid = np.arange(t_)[None, :] < np.asarray(lengths)[:, None]
+        u = np.where(valid[:, :, None], u, 0.0)
+    new_cache = None
+    if cache is not None:
+        if not p.causal:
+            raise ValueError("a conv cache needs a causal module")
+        seq = np.concatenate([np.transpose(np.asarray(cache, dtype=np.float64), (0, 2, 1)), u], axis=1)
+        new_cache = np.transpose(seq[:, seq.shape[1] - (k - 1):, :], (0, 2, 1)).copy()
+        conv_dt, pad_l, pad_r = F32, 0, 0
+        u = seq
+    elif p.causal:
+        conv_dt, pad_l, pad_r = F32, k - 1, 0
+    else:
+        conv_dt, pad_l, pad_r = act, (k - 1) // 2, (k - 1) // 2
+    y = depthwise_conv1d(u, p.depthwise_weight, p.depthwise_bias, pad_l, pad_r, conv_dt, dtype)
+    if p.norm == "batch_norm":
+        y = batch_norm_inference(y, p.running_mean, p.running_var, p.norm_weight, p.norm_bias,
+                                 conv_dt, dtype)
+    else:
+        y = layer_norm(y, to_dtype(p.norm_weight, dtype), to_dtype(p.norm_bias, dtype), 1e-5, conv_dt)
+    y = silu(y, conv_dt)
+    return _pointwise(p.pointwise_conv2, y, conv_dt, dtype), new_cache
+
+
+def conv_sublayer(p: ConvModuleParams, x, gamma=None, beta=None, dtype: str = F32,
+                  act: Optional[str] = None, lengths=None, cache=None, eps: float = 1e-5):
+    """x + conv(LayerNorm(x)) (conformer.rs:1790-1814; with the cache
+    1936-1941); the conv_norm parameters hold their `dtype` values and the
+    LayerNorm output is stored in `act`. Returns (out, new_cache)."""
+    act = act or dtype
+    g = None if gamma is None else to_dtype(gamma, dtype)
+    b = None if beta is None else to_dtype(beta, dtype)
+    h = layer_norm(x, g, b, eps, act)
+    y, new_cache = conv_module(p, h, dtype, act, lengths, cache)
+    out_dt = F32 if (cache is not None or p.causal) else act
+    return _rnd(np.asarray(x, dtype=np.float64) + y, out_dt), new_cache
+
+
+# ---------------------------------------------------------------------------
 # Index maps exported for bit-exact checks
 # ---------------------------------------------------------------------------
 

@@ -666,3 +666,147 @@ def test_feed_forward_bf16_equals_native_bf16_restatement():
     # the sublayer on an input whose LayerNorm is the identity-free case
     sub = O.feed_forward_sublayer(p, x, dtype=O.BF16)
     assert np.array_equal(sub, O.bf16_round(x + 0.5 * O.feed_forward(p, O.layer_norm(x, dtype=O.BF16), O.BF16)))
+
+
+# ---------------------------------------------------------------------------
+# ConvolutionModule (conformer.rs:2105-2437)
+# ---------------------------------------------------------------------------
+
+def _conv_params(d, k, norm, causal, seed, use_bias=True):
+    from _util import conv_oracle, conv_weights
+    return conv_oracle(conv_weights(np.random.default_rng(seed), d, k, norm, False, use_bias), norm, causal)
+
+
+def _torch_conv_module(p, x, lengths=None, left=None):
+    """The module from torch library routines in float64: linear, F.glu,
+    F.conv1d (groups = channels), F.batch_norm (inference) or F.layer_norm,
+    F.silu, linear."""
+    F = torch.nn.functional
+    T_ = lambda a: None if a is None else torch.tensor(np.asarray(a, dtype=np.float64))
+    xt = T_(x)
+    d = xt.shape[-1]
+    h = F.linear(xt, T_(p.pointwise_conv1.weight), T_(p.pointwise_conv1.bias))
+    u = F.glu(h, dim=-1)
+    if lengths is not None:
+        valid = torch.arange(u.shape[1])[None, :] < torch.tensor(lengths)[:, None]
+        u = u * valid[:, :, None]
+    k = p.kernel_size
+    ut = u.transpose(1, 2)  # [B, D, T]
+    if p.causal:
+        ut = F.pad(ut, (k - 1, 0))
+        pad = 0
+    else:
+        pad = (k - 1) // 2
+    w = T_(p.depthwise_weight).permute(0, 2, 1)  # [D, 1, K]
+    y = F.conv1d(ut, w, T_(p.depthwise_bias), padding=pad, groups=d).transpose(1, 2)
+    if p.norm == "batch_norm":
+        y = F.batch_norm(y.transpose(1, 2), T_(p.running_mean), T_(p.running_var), T_(p.norm_weight),
+                         T_(p.norm_bias), training=False, eps=1e-5).transpose(1, 2)
+    else:
+        y = F.layer_norm(y, (d,), T_(p.norm_weight), T_(p.norm_bias), eps=1e-5)
+    y = F.silu(y)
+    return F.linear(y, T_(p.pointwise_conv2.weight), T_(p.pointwise_conv2.bias)).numpy()
+
+
+@pytest.mark.parametrize("norm,causal,k,lengths", [("batch_norm", False, 9, None), ("batch_norm", True, 9, [11, 6]),
+                                                   ("layer_norm", True, 4, None), ("layer_norm", False, 31, [3, 11]),
+                                                   ("batch_norm", False, 1, [11, 0])])
+def test_conv_module_f32_matches_torch(norm, causal, k, lengths):
+    """Structure and order of the module (GLU halves, padding zeroed before
+    the conv, cross-correlation over the causal / symmetric window, the
+    norm, SiLU) against torch's own conv1d / batch_norm / layer_norm / glu."""
+    p = _conv_params(16, k, norm, causal, 40 + k)
+    x = np.random.default_rng(41).standard_normal((2, 11, 16))
+    got, cache = O.conv_module(p, x, O.F32, lengths=lengths)
+    assert cache is None
+    ref = _torch_conv_module(p, x, lengths)
+    assert np.max(np.abs(got - ref)) < 1e-12
+
+
+@pytest.mark.parametrize("chunk", [5, 3, 13])
+def test_conv_cache_chunks_equal_offline_causal(chunk):
+    """Streaming a causal module chunk by chunk through its [B, D, K-1]
+    cache, starting from zeros, reproduces the offline forward of the whole
+    sequence (the left zero padding is the initial cache), whatever the
+    chunk size relative to K-1 = 8; the cache after each chunk holds the
+    last K-1 GLU frames of everything seen (or zeros before them)."""
+    d, k, T = 16, 9, 27
+    p = _conv_params(d, k, "layer_norm", True, 42)
+    x = np.random.default_rng(43).standard_normal((2, T, d))
+    whole, _ = O.conv_module(p, x, O.F32)
+    cache = np.zeros((2, d, k - 1))
+    outs = []
+    for t0 in range(0, T, chunk):
+        y, cache = O.conv_module(p, x[:, t0:t0 + chunk], O.F32, cache=cache)
+        outs.append(y)
+        seen = O.glu(O.LinearLayer.forward(p.pointwise_conv1, x[:, :t0 + y.shape[1]]), d, O.F32)
+        want = np.concatenate([np.zeros((2, k - 1, d)), seen], axis=1)[:, -(k - 1):]
+        assert np.max(np.abs(cache - np.transpose(want, (0, 2, 1)))) < 1e-12
+    assert np.max(np.abs(np.concatenate(outs, axis=1) - whole)) < 1e-12
+    with pytest.raises(ValueError):
+        O.conv_module(_conv_params(d, k, "layer_norm", False, 42), x, O.F32, cache=cache)
+
+
+def _bf16_rsqrt(s):
+    """rsqrt of a bf16 tensor, correctly rounded to bf16 (torch's CPU bf16
+    rsqrt is off by 1-2 ulps on some inputs; the value is a float64 sqrt and
+    division, rounded once through f32)."""
+    return (1.0 / torch.sqrt(s.double())).float().to(torch.bfloat16)
+
+
+def test_conv_module_bf16_symmetric_equals_native_bf16_restatement():
+    """A symmetric bf16 module stays bf16: every op result is rounded --
+    pointwise matmul and bias add, sigmoid, GLU product, depthwise conv and
+    its bias add, (x - mean), rsqrt(var + eps) with eps cast to bf16, the
+    product, weight * x, + bias, sigmoid, SiLU product, pointwise_conv2."""
+    d, k = 16, 5
+    p = _conv_params(d, k, "batch_norm", False, 44)
+    x = O.bf16_round(np.random.default_rng(45).standard_normal((2, 9, d)))
+    bf = torch.bfloat16
+    t = lambda a: torch.tensor(np.asarray(a, dtype=np.float32)).to(bf)
+    h = t(x) @ t(p.pointwise_conv1.weight).T + t(p.pointwise_conv1.bias)
+    u = h[..., :d] * torch.sigmoid(h[..., d:])
+    up = torch.nn.functional.pad(u.double(), (0, 0, 2, 2))
+    w = t(p.depthwise_weight[:, :, 0]).double()  # [D, K]
+    y = sum(up[:, j:j + 9, :] * w[:, j] for j in range(k)).to(bf) + t(p.depthwise_bias)
+    y = (y - t(p.running_mean)) * _bf16_rsqrt(t(p.running_var) + torch.tensor(1e-5).to(bf))
+    y = t(p.norm_weight) * y + t(p.norm_bias)
+    y = y * torch.sigmoid(y)
+    ref = y @ t(p.pointwise_conv2.weight).T + t(p.pointwise_conv2.bias)
+    got, _ = O.conv_module(p, x, O.BF16)
+    assert np.array_equal(got, ref.double().numpy())
+
+
+def test_conv_module_bf16_causal_promotes_to_f32():
+    """A causal bf16 module: pointwise_conv1 and the GLU in bf16, then the
+    f32 zero padding promotes the conv, norm, SiLU and pointwise_conv2 to f32
+    with bf16-valued parameters -- except rsqrt(var + eps), which involves
+    bf16 parameters only and stays bf16. torch applies the same promotion
+    rules; its f32 ops round to f32, the oracle does not (1e-6 apart)."""
+    d, k = 16, 4
+    p = _conv_params(d, k, "batch_norm", True, 46)
+    x = O.bf16_round(np.random.default_rng(47).standard_normal((2, 9, d)))
+    bf = torch.bfloat16
+    t = lambda a: torch.tensor(np.asarray(a, dtype=np.float32)).to(bf)
+    h = t(x) @ t(p.pointwise_conv1.weight).T + t(p.pointwise_conv1.bias)
+    u = h[..., :d] * torch.sigmoid(h[..., d:])
+    up = torch.cat([torch.zeros(2, k - 1, d, dtype=torch.float32), u], dim=1)  # f32 zeros promote
+    assert up.dtype == torch.float32
+    w = t(p.depthwise_weight[:, :, 0])
+    y = sum(up[:, j:j + 9, :] * w[:, j] for j in range(k)) + t(p.depthwise_bias)
+    assert y.dtype == torch.float32
+    s = t(p.running_var) + torch.tensor(1e-5).to(bf)
+    assert s.dtype == bf
+
+    def tail(inv):
+        z = (y - t(p.running_mean)) * inv
+        z = t(p.norm_weight) * z + t(p.norm_bias)
+        z = z * torch.sigmoid(z)
+        return (z @ t(p.pointwise_conv2.weight).float().T + t(p.pointwise_conv2.bias)).double().numpy()
+
+    ref = tail(_bf16_rsqrt(s))
+    got, _ = O.conv_module(p, x, O.BF16)
+    assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) < 1e-6
+    # the bf16 rounding of the rsqrt term is load-bearing: an f32 one moves the result
+    alt = tail(torch.rsqrt(s.float()))
+    assert np.max(np.abs(alt - got)) / np.max(np.abs(ref)) > 1e-4
