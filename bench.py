@@ -17,6 +17,11 @@ resident in HBM:
                              70-frame cache ring, fp32 (frames = 16 * 14)
   xl_stream_f32_24l          that chunk through 24 distinct streaming layers
                              (~680 MB of weights and rings: not cache-resident)
+  conv_offline_bf16          the block's ConvolutionModule (K=9, BatchNorm),
+                             B=8, T=375, bf16
+  conv_stream_f32            its causal streaming form (K=9, LayerNorm): one
+                             14-frame chunk for 16 sessions through the conv
+                             cache, fp32
 Prints one JSON line: whole-step throughput in encoder frames/s; the roofline
 of the path's bounding kernel (the largest kernel; for streaming, the chunk
 attention kernel against HBM), whose average launch time is measured with HIP
@@ -196,6 +201,162 @@ def cpu_baseline(cfg, layers_w, x, ex, budget_s):
                       f"softmax, streaming K/V re-projected over cache + chunk) with OpenBLAS sgemm; CPU: {model}"}
 
 
+def time_steps(step, args):
+    """Warm up, then time exactly args.steps steps between two synchronisations:
+    (wall seconds, GPU milliseconds between events on the current stream)."""
+    import torch
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    return time.perf_counter() - t0, ev0.elapsed_time(ev1)
+
+
+def profile_kernels(handles, step, nsteps, rep_tag, repeat):
+    """{tag: (total ms, launches)} from the handles' event profilers over
+    nsteps steps; launches tagged rep_tag are issued `repeat` times per pair."""
+    import torch
+    for h in handles:
+        h.profile_reset()
+        h.profile_repeat(rep_tag, repeat if rep_tag else 1)
+        h.profile(True)
+    for _ in range(nsteps):
+        step()
+    torch.cuda.synchronize()
+    kernels = {}
+    for h in handles:
+        for tag, (ms, n) in h.profile_read().items():
+            tot, cnt = kernels.get(tag, (0.0, 0))
+            kernels[tag] = (tot + ms, cnt + n)
+        h.profile(False)
+        h.profile_repeat(None, 1)
+    return kernels
+
+
+def roofline(cfg, kernel, work, avg_ms, dtag, repeat):
+    """The roofline object of one kernel from its algorithmic work per launch
+    and its average launch time."""
+    if not work:
+        return None
+    amount, unit, bound = work
+    if unit == "TFLOP/s":
+        ach, peak = amount / (avg_ms * 1e-3) / 1e12, PEAK[dtag]
+    else:
+        ach, peak = amount / (avg_ms * 1e-3) / 1e9, HBM_PEAK
+    return {"bound": bound, "kernel": kernel, "achieved": round(ach, 2), "peak": peak, "unit": unit,
+            "frac": round(ach / peak, 4), "traffic": measured_traffic(cfg.name, kernel),
+            "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_per_launch": amount,
+            "timing": f"HIP events around {repeat} back-to-back launches on the launch stream"}
+
+
+def bench_conv(args, cfg):
+    """The ConvolutionModule workloads: one module pass per step (offline: the
+    batch through forward; streaming: one chunk per session through
+    forward_with_cache and the in-place conv cache)."""
+    import torch
+    import relpos_mhsa as M
+    import workloads as W
+
+    ws, x, ex = W.instantiate(cfg)
+    D, T, B, K = cfg.d_model, cfg.seq_len, cfg.batch, cfg.conv_kernel
+    dt = torch.bfloat16 if cfg.dtype == "bfloat16" else torch.float32
+    m = M.ConvolutionModule(D, K, cfg.conv_norm, causal=cfg.causal, use_bias=cfg.use_bias)
+    m.load_weights(ws[0], "conv")
+    m.set_dtype(dt)
+    lengths = ex.get("lengths")
+    lens = M._int_array(lengths)
+    if cfg.steps:
+        chunks = torch.from_numpy(ex["chunks"]).cuda().contiguous()
+        cache = torch.from_numpy(ex["cache"]).cuda().contiguous()
+        out = torch.empty_like(chunks[0])
+        state = {"i": 0}
+
+        def step():
+            xc = chunks[state["i"] % cfg.steps]
+            M._check(m._lib.mhsa_conv_forward_with_cache(m._h, M._dptr(xc), B, T, M._dptr(cache), None,
+                                                         M._dptr(out), M._stream_ptr()))
+            state["i"] += 1
+    else:
+        xd = torch.from_numpy(x).cuda().to(dt).contiguous()
+        out = torch.empty(xd.shape, dtype=m.output_dtype(), device="cuda")
+
+        def step():
+            M._check(m._lib.mhsa_conv_forward(m._h, M._dptr(xd), B, T, lens, M._dptr(out), M._stream_ptr()))
+
+    wall, gpu_ms = time_steps(step, args)
+    ms_per_step = wall * 1e3 / args.steps
+    kernels = profile_kernels([m], step, max(1, min(args.steps, 50)), None, 1)
+    dom = max(kernels, key=lambda k: kernels[k][0])
+    rep = profile_kernels([m], step, max(1, min(args.steps, 10)), dom, args.repeat)
+    dtag = "bf16" if cfg.dtype == "bfloat16" else "f32"
+    roof = roofline(cfg, dom, W.conv_work(cfg, dom), rep[dom][0] / rep[dom][1], dtag,
+                    1 if (cfg.steps and dom == "conv") else args.repeat)
+    # every kernel against its own roofline (the fused conv kernel is HBM-bound)
+    per_kernel = {}
+    for tag in kernels:
+        r = rep if tag == dom else profile_kernels([m], step, max(1, min(args.steps, 10)), tag, args.repeat)
+        # the library does not repeat the in-place cache update
+        reps = 1 if (cfg.steps and tag == "conv") else args.repeat
+        ro = roofline(cfg, tag, W.conv_work(cfg, tag), r[tag][0] / r[tag][1], dtag, reps)
+        if ro:
+            per_kernel[tag] = {k: ro[k] for k in ("bound", "achieved", "unit", "frac", "avg_launch_us")}
+    result = {
+        "metric": METRIC, "value": round(B * T * args.steps / wall, 1), "unit": "frames/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": dtag,
+        "data": "synthetic (seeded numpy PCG64; Xavier-uniform pointwise weights)",
+        "config": {"workload": cfg.name, "module": "ConvolutionModule", "d_model": D, "kernel_size": K,
+                   "norm": cfg.conv_norm, "causal": cfg.causal, "batch": B, "seq_len": T,
+                   "key_padding": bool(lengths), "streaming": bool(cfg.steps)},
+        "gpu_ms_per_step": round(gpu_ms / args.steps, 4),
+        "step_tflops": round(W.conv_flops(cfg) / (ms_per_step * 1e-3) / 1e12, 2),
+        "roofline": roof,
+        "kernel_rooflines": per_kernel,
+        "kernels_avg_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in sorted(kernels.items())},
+    }
+    result["cpu_baseline"] = None if args.no_cpu else cpu_baseline_conv(cfg, ws[0], x, ex, args.cpu_seconds)
+    print(json.dumps(result))
+
+
+def cpu_baseline_conv(cfg, w, x, ex, budget_s):
+    """The float32 BLAS restatement of the ConvolutionModule (oracle/cpu_blas.py)
+    timed on the host over a bounded sample."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import cpu_blas
+    P = cpu_blas.conv_params(w, cfg.dtype == "bfloat16")
+    B, T = cfg.batch, cfg.seq_len
+    if cfg.steps:
+        state = {"i": 0, "cache": ex["cache"].copy()}
+
+        def one():
+            _, state["cache"] = cpu_blas.conv_module(P, ex["chunks"][state["i"] % cfg.steps], None, state["cache"],
+                                                     True)
+            state["i"] += 1
+        what = f"{B} sessions x {T}-frame chunk through the conv cache"
+    else:
+        lens = ex.get("lengths")
+
+        def one():
+            cpu_blas.conv_module(P, x, lens, None, cfg.causal)
+        what = f"{B} utterances x {T} frames"
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        one()
+        passes += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    el = time.perf_counter() - t0
+    return {"value": round(passes * B * T / el, 2), "unit": "frames/s", "cores": cpu_blas.threads(), "kind": "port",
+            "sample": f"{passes} pass(es) of {what} in {el:.1f} s; float32 numpy restatement of the "
+                      f"ConvolutionModule (pointwise convs as OpenBLAS sgemm, K shifted multiply-adds)"}
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -214,6 +375,9 @@ def main():
         return
     M.library()  # fails loudly if the HIP library is missing
     cfg = W.CONFIGS[args.config]
+    if cfg.module == "conv":
+        bench_conv(args, cfg)
+        return
     layers_w, x, ex = W.instantiate(cfg)
     dt = torch.bfloat16 if cfg.dtype == "bfloat16" else torch.float32
     D, T, B = cfg.d_model, cfg.seq_len, cfg.batch
@@ -269,60 +433,24 @@ def main():
                                                  M._dptr(out), M._stream_ptr()))
     frames_per_step = B * T
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
     n_before = len(fills_log)
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    ev0.record()
-    for _ in range(args.steps):
-        step()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    gpu_ms = ev0.elapsed_time(ev1)
+    wall, gpu_ms = time_steps(step, args)
     ms_per_step = wall * 1e3 / args.steps
     value = frames_per_step * args.steps / wall
     timed_fills = fills_log[n_before:] if cfg.cache_size else None
 
     # per-kernel averages from the library's event profiler (separate pass)
     def profile_pass(nsteps, rep_tag=None):
-        for layer in layers:
-            layer.profile_reset()
-            layer.profile_repeat(rep_tag, args.repeat if rep_tag else 1)
-            layer.profile(True)
         n0 = len(fills_log)
-        for _ in range(nsteps):
-            step()
-        torch.cuda.synchronize()
-        kernels = {}
-        for layer in layers:
-            for tag, (ms, n) in layer.profile_read().items():
-                tot, cnt = kernels.get(tag, (0.0, 0))
-                kernels[tag] = (tot + ms, cnt + n)
-            layer.profile(False)
-            layer.profile_repeat(None, 1)
-        return kernels, fills_log[n0:]
+        return profile_kernels(layers, step, nsteps, rep_tag, args.repeat), fills_log[n0:]
 
     prof_steps = max(1, min(args.steps, 50 if cfg.layers == 1 else 3))
     kernels, _ = profile_pass(prof_steps)
     dom = "attention" if cfg.cache_size else max(kernels, key=lambda k: kernels[k][0])
     rep, rep_fills = profile_pass(max(1, min(args.steps, 10 if cfg.layers == 1 else 2)), dom)
     avg_ms = rep[dom][0] / rep[dom][1]
-    work = kernel_work(cfg, dom, lengths, rep_fills)
     dtag = "bf16" if cfg.dtype == "bfloat16" else "f32"
-    roof = None
-    if work:
-        amount, unit, bound = work
-        if unit == "TFLOP/s":
-            ach, peak = amount / (avg_ms * 1e-3) / 1e12, PEAK[dtag]
-        else:
-            ach, peak = amount / (avg_ms * 1e-3) / 1e9, HBM_PEAK
-        roof = {"bound": bound, "kernel": dom, "achieved": round(ach, 2), "peak": peak, "unit": unit,
-                "frac": round(ach / peak, 4), "traffic": measured_traffic(cfg.name, dom),
-                "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_per_launch": amount,
-                "timing": f"HIP events around {args.repeat} back-to-back launches on the launch stream"}
+    roof = roofline(cfg, dom, kernel_work(cfg, dom, lengths, rep_fills), avg_ms, dtag, args.repeat)
 
     if cfg.cache_size:
         total_flops = float(np.mean([W.algorithmic_flops(cfg, None, f) for f in timed_fills]))

@@ -360,6 +360,17 @@ int32_t mhsa_conv_sublayer_forward(mhsa_conv* conv, void* x_inout, int32_t batch
                                    const int32_t* lengths, const float* ln_gamma_host, const float* ln_beta_host,
                                    float eps, void* hip_stream);
 
+/* Per-kernel HIP-event timing of the module's launches, as mhsa_profile_*
+ * does for a layer (tags pointwise_conv1, conv, layer_norm, pointwise_conv2;
+ * repeats skip launches whose repetition would change state: the in-place
+ * cache update and the residual form). No reference counterpart. */
+int32_t mhsa_conv_profile_enable(mhsa_conv* conv, int32_t enable);
+int32_t mhsa_conv_profile_repeat(mhsa_conv* conv, const char* tag, int32_t n);
+int32_t mhsa_conv_profile_reset(mhsa_conv* conv);
+int32_t mhsa_conv_profile_count(mhsa_conv* conv);
+int32_t mhsa_conv_profile_entry(mhsa_conv* conv, int32_t idx, const char** name, double* total_ms,
+                                int32_t* launches);
+
 /* ---- encoder-level streaming ---------------------------------------------- */
 
 /* The per-chunk layer loop of ConformerEncoder::forward_streaming

@@ -260,6 +260,7 @@ struct mhsa_conv {
   DevBuf ln_dev;
   std::vector<float> ln_host;
   DevBuf partial;
+  Profiler prof;
 };
 
 namespace {
@@ -409,7 +410,11 @@ int32_t conv_impl(mhsa_conv* m, const void* x, int B, int T, DType act, const in
   HIPCHK(m->gbuf.ensure(align_up(rows * 2 * D * mhsa::dtype_size(act), 256)));
   HIPCHK(m->ybuf.ensure(align_up(rows * D * mhsa::dtype_size(cdt), 256)));
   HIPCHK(m->partial.ensure((size_t)mhsa::kGemmPartialElems * 4));
-  if (int32_t rc = conv_pointwise(m, 0, act, x, (int)rows, m->gbuf.p, nullptr, s)) return rc;
+  {
+    ProfScope ps(m->prof, "pointwise_conv1", s);
+    for (int r = m->prof.reps("pointwise_conv1"); r > 0; --r)
+      if (int32_t rc = conv_pointwise(m, 0, act, x, (int)rows, m->gbuf.p, nullptr, s)) return rc;
+  }
   // several frame tiles of one item would read the cache while the last one
   // rewrites it: read a copy then
   const float* cache_in = cache;
@@ -419,6 +424,8 @@ int32_t conv_impl(mhsa_conv* m, const void* x, int B, int T, DType act, const in
     HIPCHK(hipMemcpyAsync(m->cache_prev.p, cache, bytes, hipMemcpyDeviceToDevice, s));
     cache_in = static_cast<const float*>(m->cache_prev.p);
   }
+  // (a cache updated in place is not repeated: each pass would advance it)
+  ProfScope ps(m->prof, "conv", s);
   for (int b0 = 0; b0 < B; b0 += mhsa::kMaxBatch) {
     const int nb = std::min(mhsa::kMaxBatch, B - b0);
     mhsa::ConvParams p;
@@ -436,12 +443,18 @@ int32_t conv_impl(mhsa_conv* m, const void* x, int B, int T, DType act, const in
     p.K = K;
     p.left = m->causal ? C : C / 2;
     for (int b = 0; b < nb; ++b) p.len[b] = lens ? std::max(0, std::min(lens[b0 + b], T)) : T;
-    HIPCHK(mhsa::conv_glu_depthwise(act, cdt, p, nb, s));
+    for (int r = cache ? 1 : m->prof.reps("conv"); r > 0; --r) HIPCHK(mhsa::conv_glu_depthwise(act, cdt, p, nb, s));
   }
-  if (m->norm == MHSA_CONV_LAYER_NORM)  // nn::LayerNorm (eps 1e-5) then SiLU, in place
+  if (m->norm == MHSA_CONV_LAYER_NORM) {  // nn::LayerNorm (eps 1e-5) then SiLU, in place
+    ps.next("layer_norm");
     HIPCHK(mhsa::layer_norm(cdt, m->ybuf.p, m->ybuf.p, m->norm_pack, m->norm_pack + D, 1e-5f, (int)rows, D, s,
                             mhsa::kActSilu));
-  return conv_pointwise(m, 1, cdt, m->ybuf.p, (int)rows, out, residual, s);
+  }
+  ps.next("pointwise_conv2");
+  // (the residual form is not repeated: out aliases the residual)
+  for (int r = residual ? 1 : m->prof.reps("pointwise_conv2"); r > 0; --r)
+    if (int32_t rc = conv_pointwise(m, 1, cdt, m->ybuf.p, (int)rows, out, residual, s)) return rc;
+  return MHSA_OK;
 }
 
 int32_t check_conv(const mhsa_conv* m) { return m ? MHSA_OK : fail(MHSA_EINVAL, "null conv handle"); }
@@ -498,6 +511,28 @@ int32_t mhsa_conv_set_dtype(mhsa_conv* m, int32_t dtype) {
 }
 
 int32_t mhsa_conv_cache_size(const mhsa_conv* m) { return m ? m->K - 1 : -1; }
+
+int32_t mhsa_conv_profile_enable(mhsa_conv* m, int32_t enable) {
+  if (int32_t rc = check_conv(m)) return rc;
+  return m->prof.enable(enable);
+}
+
+int32_t mhsa_conv_profile_repeat(mhsa_conv* m, const char* tag, int32_t n) {
+  if (int32_t rc = check_conv(m)) return rc;
+  return m->prof.set_repeat(tag, n);
+}
+
+int32_t mhsa_conv_profile_reset(mhsa_conv* m) {
+  if (int32_t rc = check_conv(m)) return rc;
+  return m->prof.reset();
+}
+
+int32_t mhsa_conv_profile_count(mhsa_conv* m) { return m ? m->prof.entries() : -1; }
+
+int32_t mhsa_conv_profile_entry(mhsa_conv* m, int32_t idx, const char** name, double* total_ms, int32_t* launches) {
+  if (int32_t rc = check_conv(m)) return rc;
+  return m->prof.entry(idx, name, total_ms, launches);
+}
 
 int32_t mhsa_conv_output_dtype(const mhsa_conv* m) {
   if (!m) return -1;

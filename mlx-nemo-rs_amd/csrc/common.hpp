@@ -71,9 +71,12 @@ template <typename T> __device__ __forceinline__ T from_float(float v) { return 
 
 // sigmoid(v) = 1 / (1 + e^-v) stored in T, and nn::silu as the reference
 // evaluates it: the sigmoid stored, then the product stored (conformer.rs:2069).
+// e^-v is the hardware exp2 of -v log2(e) and the division a hardware
+// reciprocal (each ~1 ulp, as the fast-math transcendentals of MLX's GPU
+// kernels): e^-v = inf for v < -88 gives 0, e^-v = 0 gives 1.
 template <typename T>
 __device__ __forceinline__ float sigmoid_value(float v) {
-  return round_to<T>(1.f / (1.f + expf(-v)));
+  return round_to<T>(__builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(v * -1.4426950408889634f)));
 }
 template <typename T>
 __device__ __forceinline__ float silu_value(float v) {

@@ -178,4 +178,112 @@ inline int64_t align_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// Per-kernel HIP-event timing on the launch stream (off unless enabled).
+struct Profiler {
+  bool on = false;
+  // while on: launches tagged repeat_tag are issued repeat_n times inside
+  // one event pair, which spreads the event overhead over repeat_n launches
+  std::string repeat_tag;
+  int repeat_n = 1;
+  struct Pair {
+    hipEvent_t a = nullptr, b = nullptr;
+    std::string tag;
+    int n = 1;
+  };
+  std::vector<Pair> pool;
+  size_t used = 0;
+  std::vector<std::string> names;
+  std::vector<double> ms;
+  std::vector<int> count;
+
+  ~Profiler() {
+    for (Pair& p : pool) {
+      if (p.a) (void)hipEventDestroy(p.a);
+      if (p.b) (void)hipEventDestroy(p.b);
+    }
+  }
+  int begin(const char* tag, hipStream_t s) {
+    if (!on) return -1;
+    if (used == pool.size()) {
+      Pair p;
+      if (hipEventCreate(&p.a) != hipSuccess || hipEventCreate(&p.b) != hipSuccess) return -1;
+      pool.push_back(p);
+    }
+    Pair& p = pool[used];
+    p.tag = tag;
+    p.n = reps(tag);
+    if (hipEventRecord(p.a, s) != hipSuccess) return -1;
+    return (int)used++;
+  }
+  // How many times the launches tagged `tag` are issued.
+  int reps(const char* tag) const { return on && repeat_n > 1 && repeat_tag == tag ? repeat_n : 1; }
+  void end(int idx, hipStream_t s) {
+    if (idx >= 0) (void)hipEventRecord(pool[idx].b, s);
+  }
+  // Wait for the recorded pairs and fold them into the totals.
+  void flush() {
+    for (size_t i = 0; i < used; ++i) {
+      float t = 0.f;
+      if (hipEventSynchronize(pool[i].b) != hipSuccess || hipEventElapsedTime(&t, pool[i].a, pool[i].b) != hipSuccess)
+        continue;
+      size_t k = 0;
+      while (k < names.size() && names[k] != pool[i].tag) ++k;
+      if (k == names.size()) {
+        names.push_back(pool[i].tag);
+        ms.push_back(0.0);
+        count.push_back(0);
+      }
+      ms[k] += t;
+      count[k] += pool[i].n;
+    }
+    used = 0;
+  }
+  // The C-ABI profile calls shared by every handle type.
+  int32_t enable(int32_t e) {
+    flush();
+    on = e != 0;
+    return MHSA_OK;
+  }
+  int32_t set_repeat(const char* tag, int32_t n) {
+    if (n < 1 || (n > 1 && !tag)) return fail(MHSA_EINVAL, "repeat count must be >= 1 (with a tag)");
+    repeat_tag = tag ? tag : "";
+    repeat_n = n;
+    return MHSA_OK;
+  }
+  int32_t reset() {
+    flush();
+    names.clear();
+    ms.clear();
+    count.clear();
+    return MHSA_OK;
+  }
+  int32_t entries() {
+    flush();
+    return (int32_t)names.size();
+  }
+  int32_t entry(int32_t idx, const char** name, double* total_ms, int32_t* launches) {
+    flush();
+    if (idx < 0 || idx >= (int32_t)names.size()) return fail(MHSA_EINVAL, "profile entry %d out of range", idx);
+    if (name) *name = names[idx].c_str();
+    if (total_ms) *total_ms = ms[idx];
+    if (launches) *launches = count[idx];
+    return MHSA_OK;
+  }
+};
+
+// Brackets the kernels launched in its scope with a profiling event pair.
+struct ProfScope {
+  Profiler& p;
+  hipStream_t s;
+  int idx;
+  ProfScope(Profiler& prof, const char* tag, hipStream_t s_, bool enabled = true)
+      : p(prof), s(s_), idx(enabled ? prof.begin(tag, s_) : -1) {}
+  ~ProfScope() { p.end(idx, s); }
+  // Close the current span and open the next one.
+  void next(const char* tag) {
+    p.end(idx, s);
+    idx = idx >= 0 || p.on ? p.begin(tag, s) : -1;
+  }
+};
+
 }  // namespace

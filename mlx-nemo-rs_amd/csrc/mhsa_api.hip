@@ -32,68 +32,6 @@ namespace {
 thread_local std::string g_err;
 
 
-// Per-kernel HIP-event timing on the launch stream (off unless enabled).
-struct Profiler {
-  bool on = false;
-  // while on: launches tagged repeat_tag are issued repeat_n times inside
-  // one event pair, which spreads the event overhead over repeat_n launches
-  std::string repeat_tag;
-  int repeat_n = 1;
-  struct Pair {
-    hipEvent_t a = nullptr, b = nullptr;
-    std::string tag;
-    int n = 1;
-  };
-  std::vector<Pair> pool;
-  size_t used = 0;
-  std::vector<std::string> names;
-  std::vector<double> ms;
-  std::vector<int> count;
-
-  ~Profiler() {
-    for (Pair& p : pool) {
-      if (p.a) (void)hipEventDestroy(p.a);
-      if (p.b) (void)hipEventDestroy(p.b);
-    }
-  }
-  int begin(const char* tag, hipStream_t s) {
-    if (!on) return -1;
-    if (used == pool.size()) {
-      Pair p;
-      if (hipEventCreate(&p.a) != hipSuccess || hipEventCreate(&p.b) != hipSuccess) return -1;
-      pool.push_back(p);
-    }
-    Pair& p = pool[used];
-    p.tag = tag;
-    p.n = reps(tag);
-    if (hipEventRecord(p.a, s) != hipSuccess) return -1;
-    return (int)used++;
-  }
-  // How many times the launches tagged `tag` are issued.
-  int reps(const char* tag) const { return on && repeat_n > 1 && repeat_tag == tag ? repeat_n : 1; }
-  void end(int idx, hipStream_t s) {
-    if (idx >= 0) (void)hipEventRecord(pool[idx].b, s);
-  }
-  // Wait for the recorded pairs and fold them into the totals.
-  void flush() {
-    for (size_t i = 0; i < used; ++i) {
-      float t = 0.f;
-      if (hipEventSynchronize(pool[i].b) != hipSuccess || hipEventElapsedTime(&t, pool[i].a, pool[i].b) != hipSuccess)
-        continue;
-      size_t k = 0;
-      while (k < names.size() && names[k] != pool[i].tag) ++k;
-      if (k == names.size()) {
-        names.push_back(pool[i].tag);
-        ms.push_back(0.0);
-        count.push_back(0);
-      }
-      ms[k] += t;
-      count[k] += pool[i].n;
-    }
-    used = 0;
-  }
-};
-
 }  // namespace
 
 int32_t mhsa::set_error(int32_t code, const char* msg) {
@@ -142,19 +80,10 @@ struct mhsa_layer {
 };
 
 namespace {
-// Brackets the kernels launched in its scope with a profiling event pair.
-struct ProfScope {
-  Profiler& p;
-  hipStream_t s;
-  int idx;
-  ProfScope(mhsa_layer* L, const char* tag, hipStream_t s_, bool enabled = true)
-      : p(L->prof), s(s_), idx(enabled ? L->prof.begin(tag, s_) : -1) {}
-  ~ProfScope() { p.end(idx, s); }
-  // Close the current span and open the next one.
-  void next(const char* tag) {
-    p.end(idx, s);
-    idx = idx >= 0 || p.on ? p.begin(tag, s) : -1;
-  }
+// ProfScope over a layer's profiler.
+struct LayerProf : ProfScope {
+  LayerProf(mhsa_layer* L, const char* tag, hipStream_t s_, bool enabled = true)
+      : ProfScope(L->prof, tag, s_, enabled) {}
 };
 }  // namespace
 
@@ -523,12 +452,12 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   L->last_pos = P;
 
   {
-    ProfScope ps(L, "gemm_qkv", s, prof);
+    LayerProf ps(L, "gemm_qkv", s, prof);
     for (int r = prof ? L->prof.reps("gemm_qkv") : 1; r > 0; --r)
       if ((rc = project_qkv(L, x, (int)M, qkv, 3 * D, s, use_vt ? &vt : nullptr))) return rc;
   }
   {
-    ProfScope ps(L, "gemm_pos", s, prof);
+    LayerProf ps(L, "gemm_pos", s, prof);
     for (int r = prof ? L->prof.reps("gemm_pos") : 1; r > 0; --r)
       if ((rc = run_gemm(L, L->dt, L->dev[4], D, static_cast<const char*>(pos_emb) + (size_t)row0 * D * es, D, nrows,
                          P, D, nullptr, 0, s)))
@@ -556,13 +485,13 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
     a.vt_bs = vt.Tpad;
   }
   {
-    ProfScope ps(L, "attention", s, prof);
+    LayerProf ps(L, "attention", s, prof);
     for (int r = prof ? L->prof.reps("attention") : 1; r > 0 && !rc; --r)
       rc = run_attention(L, L->dt, a, B, key_bounds, s);
   }
   if (rc) return rc;
   if (!out) return MHSA_OK;
-  ProfScope ps(L, "gemm_out", s, prof);
+  LayerProf ps(L, "gemm_out", s, prof);
   for (int r = prof ? L->prof.reps("gemm_out") : 1; r > 0 && !rc; --r)
     rc = run_gemm(L, L->dt, L->dev[3], D, cx, D, (int)M, out, D, residual, D, s);
   return rc;
@@ -906,7 +835,7 @@ int32_t mhsa_sublayer_forward(mhsa_layer* L, void* x, int32_t batch, int32_t seq
   }
   HIPCHK(L->hbuf.ensure(align_up(M * D * esz(L), 256)));
   {
-    ProfScope ps(L, "layer_norm", s);
+    LayerProf ps(L, "layer_norm", s);
     for (int r = L->prof.reps("layer_norm"); r > 0; --r)
       HIPCHK(mhsa::layer_norm(dtype_of(L), x, L->hbuf.p, gd, bd, eps, (int)M, D, s));
   }
@@ -997,7 +926,7 @@ int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, 
   // a bf16 layer projects its bf16 table in bf16 and widens the result
   if (L->pmemo_len != pos_len) {
     HIPCHK(L->pmemo.ensure(align_up((int64_t)pos_len * D * 4, 256)));
-    ProfScope ps(L, "gemm_pos", s);
+    LayerProf ps(L, "gemm_pos", s);
     if (L->dt == mhsa::kBF16) {
       HIPCHK(L->pmemo_bf16.ensure(align_up((int64_t)pos_len * D * 2, 256)));
       if ((rc = run_gemm(L, mhsa::kBF16, L->dev[4], D, pos_emb, D, pos_len, L->pmemo_bf16.p, D, nullptr, 0, s)))
@@ -1042,7 +971,7 @@ int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, 
     fp.ring_len = R;
   }
   const bool one_launch = !S || (L->qkv_fused && mhsa::gemm_split_fused_ok(mhsa::kF32, fp));
-  ProfScope ps_kv(L, one_launch ? "gemm_qkv" : "gemm_q", s);
+  LayerProf ps_kv(L, one_launch ? "gemm_qkv" : "gemm_q", s);
   if (!S) {
     if (L->qkv_fused) {
       if ((rc = run_gemm(L, mhsa::kF32, L->sdev[0], 3 * D, x, D, (int)M, q, 3 * D, nullptr, 0, s))) return rc;
@@ -1250,7 +1179,7 @@ int32_t mhsa_stack_step(mhsa_stack* K, void* x, const float* gamma, const float*
   for (int l = 0; l < n; ++l) {
     mhsa_layer* L = K->layers[l];
     {
-      ProfScope ps(L, "layer_norm", s);
+      LayerProf ps(L, "layer_norm", s);
       HIPCHK(mhsa::layer_norm(mhsa::kF32, x, K->h.p, g ? g + (size_t)2 * l * D : nullptr,
                               g ? g + (size_t)(2 * l + 1) * D : nullptr, eps, (int)M, D, s));
     }
@@ -1282,42 +1211,24 @@ int32_t mhsa_pos_encoding(int32_t d_model, int32_t max_len, int32_t seq_len, flo
 
 int32_t mhsa_profile_enable(mhsa_layer* L, int32_t enable) {
   if (int32_t rc = check_layer(L)) return rc;
-  L->prof.flush();
-  L->prof.on = enable != 0;
-  return MHSA_OK;
+  return L->prof.enable(enable);
 }
 
 int32_t mhsa_profile_repeat(mhsa_layer* L, const char* tag, int32_t n) {
   if (int32_t rc = check_layer(L)) return rc;
-  if (n < 1 || (n > 1 && !tag)) return fail(MHSA_EINVAL, "repeat count must be >= 1 (with a tag)");
-  L->prof.repeat_tag = tag ? tag : "";
-  L->prof.repeat_n = n;
-  return MHSA_OK;
+  return L->prof.set_repeat(tag, n);
 }
 
 int32_t mhsa_profile_reset(mhsa_layer* L) {
   if (int32_t rc = check_layer(L)) return rc;
-  L->prof.flush();
-  L->prof.names.clear();
-  L->prof.ms.clear();
-  L->prof.count.clear();
-  return MHSA_OK;
+  return L->prof.reset();
 }
 
-int32_t mhsa_profile_count(mhsa_layer* L) {
-  if (!L) return -1;
-  L->prof.flush();
-  return (int32_t)L->prof.names.size();
-}
+int32_t mhsa_profile_count(mhsa_layer* L) { return L ? L->prof.entries() : -1; }
 
 int32_t mhsa_profile_entry(mhsa_layer* L, int32_t idx, const char** name, double* total_ms, int32_t* launches) {
   if (int32_t rc = check_layer(L)) return rc;
-  L->prof.flush();
-  if (idx < 0 || idx >= (int32_t)L->prof.names.size()) return fail(MHSA_EINVAL, "profile entry %d out of range", idx);
-  if (name) *name = L->prof.names[idx].c_str();
-  if (total_ms) *total_ms = L->prof.ms[idx];
-  if (launches) *launches = L->prof.count[idx];
-  return MHSA_OK;
+  return L->prof.entry(idx, name, total_ms, launches);
 }
 
 int32_t mhsa_debug_dequantize(mhsa_layer* L, int32_t which, float* out, void* hs) {

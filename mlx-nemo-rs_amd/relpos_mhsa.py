@@ -41,7 +41,8 @@ EXPORTS = (
     "mhsa_stack_step", "mhsa_ffn_create", "mhsa_ffn_destroy", "mhsa_ffn_set_dtype", "mhsa_ffn_load_weights",
     "mhsa_ffn_forward", "mhsa_ffn_sublayer_forward", "mhsa_conv_create", "mhsa_conv_destroy", "mhsa_conv_set_dtype",
     "mhsa_conv_load_weights", "mhsa_conv_cache_size", "mhsa_conv_output_dtype", "mhsa_conv_forward",
-    "mhsa_conv_forward_with_cache", "mhsa_conv_sublayer_forward",
+    "mhsa_conv_forward_with_cache", "mhsa_conv_sublayer_forward", "mhsa_conv_profile_enable",
+    "mhsa_conv_profile_repeat", "mhsa_conv_profile_reset", "mhsa_conv_profile_count", "mhsa_conv_profile_entry",
     "mhsa_pos_encoding",
     "mhsa_debug_dequantize", "mhsa_debug_linear", "mhsa_debug_offline_mask", "mhsa_debug_stream_mask", "mhsa_debug_rel_shift_index",
     "mhsa_debug_position_scores", "mhsa_debug_top_keys", "mhsa_profile_enable", "mhsa_profile_repeat",
@@ -140,6 +141,11 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_conv_forward": (I, [VP, VP, I, I, PI, VP, VP]),
         "mhsa_conv_forward_with_cache": (I, [VP, VP, I, I, VP, PI, VP, VP]),
         "mhsa_conv_sublayer_forward": (I, [VP, VP, I, I, VP, PI, P(ctypes.c_float), P(ctypes.c_float), F, VP]),
+        "mhsa_conv_profile_enable": (I, [VP, I]),
+        "mhsa_conv_profile_repeat": (I, [VP, ctypes.c_char_p, I]),
+        "mhsa_conv_profile_reset": (I, [VP]),
+        "mhsa_conv_profile_count": (I, [VP]),
+        "mhsa_conv_profile_entry": (I, [VP, I, P(ctypes.c_char_p), P(ctypes.c_double), PI]),
         "mhsa_pos_encoding": (I, [I, I, I, P(ctypes.c_float)]),
         "mhsa_debug_dequantize": (I, [VP, I, VP, VP]),
         "mhsa_debug_linear": (I, [VP, I, VP, I, VP, VP]),
@@ -210,6 +216,35 @@ class QuantizationConfig:
 
     bits: int = 8
     group_size: int = 64
+
+
+class _Profiled:
+    """Per-kernel HIP-event timing of a handle's launches (the C ABI's
+    <prefix>profile_* calls)."""
+
+    _PROFILE = "mhsa_profile_"
+
+    def _pf(self, name):
+        return getattr(self._lib, self._PROFILE + name)
+
+    def profile(self, enable: bool = True) -> None:
+        _check(self._pf("enable")(self._h, 1 if enable else 0))
+
+    def profile_repeat(self, tag: Optional[str], n: int = 1) -> None:
+        """Issue launches tagged `tag` n times per event pair while profiling."""
+        _check(self._pf("repeat")(self._h, tag.encode() if tag else None, int(n)))
+
+    def profile_reset(self) -> None:
+        _check(self._pf("reset")(self._h))
+
+    def profile_read(self) -> Dict[str, Tuple[float, int]]:
+        """{kernel tag: (total ms, launches)} accumulated since the last reset."""
+        out = {}
+        for i in range(self._pf("count")(self._h)):
+            name, ms, n = ctypes.c_char_p(), ctypes.c_double(), ctypes.c_int32()
+            _check(self._pf("entry")(self._h, i, ctypes.byref(name), ctypes.byref(ms), ctypes.byref(n)))
+            out[name.value.decode()] = (ms.value, n.value)
+        return out
 
 
 @dataclass
@@ -383,12 +418,14 @@ class FeedForward:
 CONV_BATCH_NORM, CONV_LAYER_NORM = 0, 1
 
 
-class ConvolutionModule:
+class ConvolutionModule(_Profiled):
     """ConvolutionModule (conformer.rs:2105-2437) backed by the HIP library.
 
     norm: "batch_norm" or "layer_norm" (ConvNormType, asr/config.rs:119-128).
     A causal module's output is f32 whatever its dtype (the f32 causal
     padding and conv cache promote, conformer.rs:2250-2256, 2328-2336)."""
+
+    _PROFILE = "mhsa_conv_profile_"
 
     def __init__(self, d_model: int, kernel_size: int, norm: str = "batch_norm", causal: bool = False,
                  use_bias: bool = True):
@@ -532,7 +569,7 @@ class Checkpoint:
 # the attention module
 # ---------------------------------------------------------------------------
 
-class RelPositionMultiHeadAttention:
+class RelPositionMultiHeadAttention(_Profiled):
     """RelPositionMultiHeadAttention (attention.rs:328-893) backed by the HIP library."""
 
     def __init__(self, d_model: int, n_heads: int, use_bias: bool):
@@ -686,25 +723,6 @@ class RelPositionMultiHeadAttention:
         return out
 
     # per-kernel HIP-event timing (no counterpart in the reference)
-    def profile(self, enable: bool = True) -> None:
-        _check(self._lib.mhsa_profile_enable(self._h, 1 if enable else 0))
-
-    def profile_repeat(self, tag: Optional[str], n: int = 1) -> None:
-        """Issue launches tagged `tag` n times per event pair while profiling."""
-        _check(self._lib.mhsa_profile_repeat(self._h, tag.encode() if tag else None, int(n)))
-
-    def profile_reset(self) -> None:
-        _check(self._lib.mhsa_profile_reset(self._h))
-
-    def profile_read(self) -> Dict[str, Tuple[float, int]]:
-        """{kernel tag: (total ms, launches)} accumulated since the last reset."""
-        out = {}
-        for i in range(self._lib.mhsa_profile_count(self._h)):
-            name, ms, n = ctypes.c_char_p(), ctypes.c_double(), ctypes.c_int32()
-            _check(self._lib.mhsa_profile_entry(self._h, i, ctypes.byref(name), ctypes.byref(ms), ctypes.byref(n)))
-            out[name.value.decode()] = (ms.value, n.value)
-        return out
-
     def debug_linear(self, name: str, x):
         """One projection alone through the forward pass's GEMM kernels."""
         import torch

@@ -19,6 +19,14 @@ Six configurations of the FastConformer attention sublayer:
                       biases N(0, 0.01), codes U{0..255}), B=4, T=1500, bf16,
                       valid lengths U{1000..1500}, seed 4
 
+and two of the block's ConvolutionModule (conformer.rs:2105-2437):
+
+* ``conv_offline_bf16`` D=1024, K=9, BatchNorm, symmetric, B=8, T=375, bf16,
+                      valid lengths U{188..375}, seed 5
+* ``conv_stream_f32``  D=1024, K=9, LayerNorm, causal, 16 sessions, 14-frame
+                      chunks through the [16, 1024, 8] f32 conv cache, 50
+                      steps, fp32, seed 6
+
 Weights are Xavier-uniform U(+-sqrt(6 / 2D)), pos_bias_u/v ~ N(0, 0.02^2),
 inputs x ~ N(0, 1); every array comes from numpy's PCG64 with the stated
 seed, so the same bytes reach the GPU and the oracle.
@@ -50,6 +58,11 @@ class Workload:
     cache_size: int = 0
     steps: int = 0
     fills: Optional[List[int]] = None
+    # "mhsa" (the attention sublayer) or "conv" (ConvolutionModule)
+    module: str = "mhsa"
+    conv_kernel: int = 0
+    conv_norm: str = "batch_norm"
+    causal: bool = False
 
     @property
     def head_dim(self) -> int:
@@ -106,7 +119,44 @@ CONFIGS: Dict[str, Workload] = {
     "xl_local_bf16": Workload("xl_local_bf16", 1024, 8, 2, 7500, "bfloat16", seed=3,
                               context=(128, 128, "regular"), pos_band=257),
     "xl_stack_u8": Workload("xl_stack_u8", 1024, 8, 4, 1500, "bfloat16", seed=4, quantized=True, layers=24),
+    "conv_offline_bf16": Workload("conv_offline_bf16", 1024, 8, 8, 375, "bfloat16", seed=5, use_bias=True,
+                                  module="conv", conv_kernel=9, conv_norm="batch_norm"),
+    "conv_stream_f32": Workload("conv_stream_f32", 1024, 8, 16, 14, "float32", seed=6, use_bias=True, steps=50,
+                                module="conv", conv_kernel=9, conv_norm="layer_norm", causal=True),
 }
+
+
+def make_conv_weights(rng, d: int, k: int, norm: str = "batch_norm", quantized: bool = False,
+                      use_bias: bool = True, prefix: str = "conv") -> Dict[str, np.ndarray]:
+    """ConvolutionModule tensors keyed like a checkpoint (conformer.rs:2389-2427):
+    pointwise convs Xavier-uniform (or affine u8 with zero-mean weights:
+    scales U(2e-4, 1e-3), biases -128 s + N(0, 1e-3)), biases N(0, 0.1),
+    depthwise [D, K, 1] ~ N(0, 1/K), norm weight U(0.5, 1.5) and bias
+    N(0, 0.1), running mean N(0, 0.1) and variance U(0.5, 2)."""
+    w: Dict[str, np.ndarray] = {}
+    for name, o in (("pointwise_conv1", 2 * d), ("pointwise_conv2", d)):
+        if quantized:
+            codes = rng.integers(0, 256, size=(o, d))
+            sc = rng.uniform(2e-4, 1e-3, size=(o, d // 64)).astype(np.float16)
+            w[f"{prefix}.{name}.weight"] = pack_u8(codes)
+            w[f"{prefix}.{name}.scales"] = sc
+            w[f"{prefix}.{name}.biases"] = (-128.0 * sc.astype(np.float64)
+                                            + rng.normal(0, 1e-3, sc.shape)).astype(np.float16)
+            if use_bias:
+                w[f"{prefix}.{name}.bias"] = rng.normal(0, 0.1, o).astype(np.float16)
+        else:
+            w[f"{prefix}.{name}.weight"] = xavier(rng, o, d)
+            if use_bias:
+                w[f"{prefix}.{name}.bias"] = rng.normal(0, 0.1, o).astype(np.float32)
+    w[f"{prefix}.depthwise_conv.weight"] = (rng.standard_normal((d, k, 1)) / np.sqrt(k)).astype(np.float32)
+    if use_bias:
+        w[f"{prefix}.depthwise_conv.bias"] = rng.normal(0, 0.1, d).astype(np.float32)
+    w[f"{prefix}.batch_norm.weight"] = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    w[f"{prefix}.batch_norm.bias"] = rng.normal(0, 0.1, d).astype(np.float32)
+    if norm == "batch_norm":
+        w[f"{prefix}.batch_norm.running_mean"] = rng.normal(0, 0.1, d).astype(np.float32)
+        w[f"{prefix}.batch_norm.running_var"] = rng.uniform(0.5, 2.0, d).astype(np.float32)
+    return w
 
 
 def instantiate(cfg: Workload, centred: bool = False):
@@ -114,6 +164,15 @@ def instantiate(cfg: Workload, centred: bool = False):
     layers: list of per-layer weight dicts; x: float32 [B, T, D] (or the first
     chunk for streaming); extras: lengths / fills / per-step chunks."""
     rng = np.random.default_rng(cfg.seed)
+    if cfg.module == "conv":
+        w = make_conv_weights(rng, cfg.d_model, cfg.conv_kernel, cfg.conv_norm, cfg.quantized, cfg.use_bias)
+        extras = {}
+        if cfg.steps:  # streaming chunks through the conv cache
+            extras["chunks"] = rng.standard_normal((cfg.steps, cfg.batch, cfg.seq_len, cfg.d_model)).astype(np.float32)
+            extras["cache"] = np.zeros((cfg.batch, cfg.d_model, cfg.conv_kernel - 1), dtype=np.float32)
+            return [w], extras["chunks"][0], extras
+        extras["lengths"] = [int(v) for v in rng.integers(cfg.seq_len // 2, cfg.seq_len + 1, size=cfg.batch)]
+        return [w], rng.standard_normal((cfg.batch, cfg.seq_len, cfg.d_model)).astype(np.float32), extras
     layers = [make_layer_weights(rng, cfg.d_model, cfg.n_heads, cfg.use_bias, cfg.quantized, centred)
               for _ in range(cfg.layers)]
     extras = {}
@@ -157,6 +216,34 @@ def algorithmic_flops(cfg: Workload, lengths=None, fills=None) -> float:
         pairs = sum(T * ln for ln in lens)
         pos_rows = 2 * T - 1
     return cfg.layers * (2.0 * D * D * (4 * B * T + pos_rows) + 6.0 * D * pairs)
+
+
+def conv_work(cfg: Workload, tag: str):
+    """Algorithmic work of one launch of a ConvolutionModule kernel:
+    (amount, "TFLOP/s" | "GB/s", "mfma" | "hbm"). The fused conv kernel
+    reads pointwise_conv1's output [rows, 2D], writes [rows, D] and, in
+    streaming, reads and rewrites the [B, D, K-1] f32 cache; parameters
+    (K + 5) D floats."""
+    D, rows, K = cfg.d_model, cfg.batch * cfg.seq_len, cfg.conv_kernel
+    es_in = 2 if cfg.dtype == "bfloat16" and not cfg.steps else 4
+    es_out = 2 if es_in == 2 and not cfg.causal else 4
+    if tag == "pointwise_conv1":
+        return 2.0 * rows * 2 * D * D, "TFLOP/s", "mfma"
+    if tag == "pointwise_conv2":
+        return 2.0 * rows * D * D, "TFLOP/s", "mfma"
+    if tag == "conv":
+        cache = 2 * 4 * cfg.batch * D * (K - 1) if cfg.steps else 0
+        return float(rows * D * (2 * es_in + es_out) + (K + 5) * D * 4 + cache), "GB/s", "hbm"
+    if tag == "layer_norm":
+        return float(2 * rows * D * es_out), "GB/s", "hbm"
+    return None
+
+
+def conv_flops(cfg: Workload) -> float:
+    """Useful work of one ConvolutionModule pass: both pointwise convs and
+    the depthwise conv (2 K FLOPs per output element)."""
+    D, rows = cfg.d_model, cfg.batch * cfg.seq_len
+    return 2.0 * rows * D * (3 * D + cfg.conv_kernel)
 
 
 def chunk_attention_bytes(cfg: Workload, fills) -> float:

@@ -207,3 +207,77 @@ class Streamer:
         out = _linear(o.transpose(0, 2, 1, 3).reshape(B, T, D), P["linear_out.weight"], P["linear_out.bias"])
         self.cache = np.concatenate([self.cache[:, T:], x], axis=1)  # 670-676 (cache_drop_size 0)
         return out
+
+
+# ---------------------------------------------------------------------------
+# ConvolutionModule (conformer.rs:2105-2437)
+# ---------------------------------------------------------------------------
+
+def conv_params(weights, dtype_bf16: bool = False, prefix: str = "conv"):
+    """float32 parameters of a ConvolutionModule from checkpoint-style tensors,
+    at bf16 values for a bf16 model, as f32 activations meet them: quantized
+    pointwise convs dequantised in f32 from the cast scales and biases; the
+    BatchNorm rsqrt(var + eps) term precomputed in the parameter dtype."""
+    def bf(a):
+        a = _f32(a)
+        if not dtype_bf16:
+            return a
+        u = a.view(np.uint32).astype(np.uint64)
+        return ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+
+    out = {}
+    for name in ("pointwise_conv1", "pointwise_conv2"):
+        k = f"{prefix}.{name}"
+        if f"{k}.scales" in weights:
+            w = np.asarray(weights[f"{k}.weight"], dtype=np.uint32)
+            codes = np.stack([(w >> (8 * i)) & 0xFF for i in range(4)], axis=-1).reshape(w.shape[0], -1)
+            s, b = bf(weights[f"{k}.scales"]), bf(weights[f"{k}.biases"])
+            # dequantised in f32 from the cast scales and biases (the promoted path)
+            out[f"{name}.weight"] = codes.astype(np.float32) * np.repeat(s, 64, axis=1) + np.repeat(b, 64, axis=1)
+        else:
+            out[f"{name}.weight"] = bf(weights[f"{k}.weight"])
+        bias = weights.get(f"{k}.bias")
+        out[f"{name}.bias"] = None if bias is None else bf(bias)
+    out["taps"] = bf(np.asarray(weights[f"{prefix}.depthwise_conv.weight"])[:, :, 0].T)  # [K, D]
+    dwb = weights.get(f"{prefix}.depthwise_conv.bias")
+    out["taps_bias"] = None if dwb is None else bf(dwb)
+    out["norm_weight"] = bf(weights[f"{prefix}.batch_norm.weight"])
+    out["norm_bias"] = bf(weights[f"{prefix}.batch_norm.bias"])
+    if f"{prefix}.batch_norm.running_var" in weights:
+        out["mean"] = bf(weights[f"{prefix}.batch_norm.running_mean"])
+        out["inv"] = bf(1.0 / np.sqrt(bf(bf(weights[f"{prefix}.batch_norm.running_var"]) + bf(np.float32(1e-5)))))
+    return out
+
+
+def conv_module(P, x, lengths=None, cache=None, causal=False):
+    """ConvolutionModule::forward / forward_with_cache (conformer.rs:2197-2291,
+    2305-2378): pointwise_conv1 (sgemm), GLU, padding frames zeroed, the
+    depthwise conv as K shifted multiply-adds over the zero- or cache-padded
+    sequence, BatchNorm or LayerNorm, SiLU, pointwise_conv2. cache [B, D, K-1]
+    is returned updated."""
+    b_, t_, d_ = x.shape
+    k = P["taps"].shape[0]
+    h = _linear(x, P["pointwise_conv1.weight"], P["pointwise_conv1.bias"])
+    u = h[..., :d_] * (np.float32(1.0) / (np.float32(1.0) + np.exp(-h[..., d_:])))
+    if lengths is not None:
+        u = u * (np.arange(t_)[None, :, None] < np.asarray(lengths)[:, None, None])
+    new_cache = None
+    if cache is not None:
+        seq = np.concatenate([cache.transpose(0, 2, 1), u], axis=1)
+        new_cache = np.ascontiguousarray(seq[:, seq.shape[1] - (k - 1):].transpose(0, 2, 1))
+    elif causal:
+        seq = np.concatenate([np.zeros((b_, k - 1, d_), np.float32), u], axis=1)
+    else:
+        p = (k - 1) // 2
+        seq = np.concatenate([np.zeros((b_, p, d_), np.float32), u, np.zeros((b_, p, d_), np.float32)], axis=1)
+    y = seq[:, 0:t_] * P["taps"][0]
+    for j in range(1, k):
+        y += seq[:, j:j + t_] * P["taps"][j]
+    if P["taps_bias"] is not None:
+        y += P["taps_bias"]
+    if "inv" in P:
+        y = ((y - P["mean"]) * P["inv"]) * P["norm_weight"] + P["norm_bias"]
+    else:
+        y = layer_norm(y) * P["norm_weight"] + P["norm_bias"]
+    y = y * (np.float32(1.0) / (np.float32(1.0) + np.exp(-y)))
+    return _linear(y, P["pointwise_conv2.weight"], P["pointwise_conv2.bias"]), new_cache

@@ -68,35 +68,9 @@ def random_weights(rng, d_model, n_heads, use_bias=True, scale=None, quantized=F
 
 
 def conv_weights(rng, d, k, norm="batch_norm", quant=False, use_bias=True, prefix="conv"):
-    """ConvolutionModule tensors keyed like a checkpoint (conformer.rs:2389-2427):
-    pointwise convs dense Xavier (or affine u8 with zero-mean weights),
-    depthwise [D, K, 1] ~ N(0, 1/K), norm parameters around identity, running
-    statistics mean N(0, 0.1), variance U(0.5, 2)."""
+    """ConvolutionModule tensors keyed like a checkpoint (the workloads' generator)."""
     import workloads as W
-    w = {}
-    for name, o in (("pointwise_conv1", 2 * d), ("pointwise_conv2", d)):
-        if quant:
-            codes = rng.integers(0, 256, size=(o, d))
-            sc = rng.uniform(2e-4, 1e-3, size=(o, d // 64)).astype(np.float16)
-            w[f"{prefix}.{name}.weight"] = W.pack_u8(codes)
-            w[f"{prefix}.{name}.scales"] = sc
-            w[f"{prefix}.{name}.biases"] = (-128.0 * sc.astype(np.float64)
-                                            + rng.normal(0, 1e-3, sc.shape)).astype(np.float16)
-            if use_bias:
-                w[f"{prefix}.{name}.bias"] = rng.normal(0, 0.1, o).astype(np.float16)
-        else:
-            w[f"{prefix}.{name}.weight"] = W.xavier(rng, o, d)
-            if use_bias:
-                w[f"{prefix}.{name}.bias"] = rng.normal(0, 0.1, o).astype(np.float32)
-    w[f"{prefix}.depthwise_conv.weight"] = (rng.standard_normal((d, k, 1)) / np.sqrt(k)).astype(np.float32)
-    if use_bias:
-        w[f"{prefix}.depthwise_conv.bias"] = rng.normal(0, 0.1, d).astype(np.float32)
-    w[f"{prefix}.batch_norm.weight"] = rng.uniform(0.5, 1.5, d).astype(np.float32)
-    w[f"{prefix}.batch_norm.bias"] = rng.normal(0, 0.1, d).astype(np.float32)
-    if norm == "batch_norm":
-        w[f"{prefix}.batch_norm.running_mean"] = rng.normal(0, 0.1, d).astype(np.float32)
-        w[f"{prefix}.batch_norm.running_var"] = rng.uniform(0.5, 2.0, d).astype(np.float32)
-    return w
+    return W.make_conv_weights(rng, d, k, norm, quant, use_bias, prefix)
 
 
 def conv_oracle(w, norm="batch_norm", causal=False, prefix="conv") -> O.ConvModuleParams:

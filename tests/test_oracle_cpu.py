@@ -96,3 +96,33 @@ def test_cpu_blas_streaming_matches_oracle():
         ref, caches = O.mhsa_forward_with_cache(p, x, pos, caches, mask)
         assert rel_err(got, ref) < 1e-5, step
         filled = O.next_fill(filled, T, 0, C)
+
+
+@pytest.mark.parametrize("norm,causal,stream,quant,bf", [("batch_norm", False, False, False, False),
+                                                         ("batch_norm", False, False, True, True),
+                                                         ("layer_norm", True, True, False, False),
+                                                         ("layer_norm", True, False, True, True)])
+def test_cpu_blas_conv_module_matches_oracle(norm, causal, stream, quant, bf):
+    """The baseline's ConvolutionModule against the float64 oracle: f32
+    activations on the module's (bf16-valued when bf) parameters, offline
+    with ragged lengths and streaming over two chunks through the cache."""
+    from _util import conv_oracle
+    rng = np.random.default_rng(77)
+    d, k = 128, 9
+    w = W.make_conv_weights(rng, d, k, norm, quant)
+    p = conv_oracle(w, norm, causal)
+    P = cpu_blas.conv_params(w, bf)
+    dt = O.BF16 if bf else O.F32
+    x = rng.standard_normal((3, 20, d)).astype(np.float32)
+    lens = [20, 13, 2]
+    if stream:
+        c_ref = np.zeros((3, d, k - 1))
+        c = c_ref.astype(np.float32)
+        for _ in range(2):
+            got, c = cpu_blas.conv_module(P, x, lens, c, causal)
+            ref, c_ref = O.conv_module(p, x, dt, act=O.F32, lengths=lens, cache=c_ref)
+            assert rel_err(got, ref) < 1e-4 and rel_err(c, c_ref) < 1e-4
+    else:
+        got, _ = cpu_blas.conv_module(P, x, lens, None, causal)
+        ref, _ = O.conv_module(p, x, dt, act=O.F32, lengths=lens)
+        assert rel_err(got, ref) < 1e-4
