@@ -753,25 +753,43 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 
     // x = q_u k + bd for this lane's keys jl(u, r) = 32u + 16(r / 8) + 8hh + r % 8:
     // 8 consecutive keys per 16-byte read
-    const bf16* rq = Rs + 31 - c + 8 * hh;
+    // Strip column 31 - c + jl holds key jl's value: an odd column for even c.
+    // The 8 keys of a read come from 5 bf16 pairs read 4-byte aligned and
+    // shifted by 0 or 16 bits per lane (unaligned 16-byte LDS reads cost the
+    // strip phase about 600 cycles per tile).
+    const int n0 = 31 - c + 8 * hh;
+    const bf16x2* rd = reinterpret_cast<const bf16x2*>(Rs) + (n0 >> 1);
+    const unsigned sh = 16u * (unsigned)(n0 & 1);
     float tmax = -INFINITY;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
-        // (read as bf16, the type the strip is written with, so no
-        // type-based alias analysis can move it across those writes)
-        const bf16x8 q8 = *reinterpret_cast<const bf16x8_a2*>(rq + 32 * u + 16 * g);
+        // (read as bf16 pairs, the element type the strip is written with, so
+        // no type-based alias analysis can move it across those writes)
+        const bf16x2* d = rd + 16 * u + 8 * g;
+        uint32_t wv[5];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
+        for (int k = 0; k < 5; ++k) wv[k] = __builtin_bit_cast(uint32_t, d[k]);
+        u32x4 al;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) al[k] = __builtin_amdgcn_alignbit(wv[k + 1], wv[k], sh);
+        const bf16x8 q8 = __builtin_bit_cast(bf16x8, al);
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) {
           // the position term as the reference materialises it:
-          // bf16(bf16(bd) * bf16(s)) (attention.rs:308-311)
-          const float tb = (float)(bf16)((float)q8[e] * p.scale_bd);
-          if (DEBUG && p.dbg_bd) {
-            const int j = j0 + 32 * u + 16 * g + 8 * hh + e;
-            if (qi < p.T && j < p.L) p.dbg_bd[(((int64_t)b * p.H + h) * p.T + qi) * p.L + j] = tb;
+          // bf16(bf16(bd) * bf16(s)) (attention.rs:308-311), two per conversion
+          const floatx2 prod = {(float)q8[e] * p.scale_bd, (float)q8[e + 1] * p.scale_bd};
+          const bf16x2 tb2 = __builtin_convertvector(prod, bf16x2);
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const float tb = (float)tb2[k];
+            if (DEBUG && p.dbg_bd) {
+              const int j = j0 + 32 * u + 16 * g + 8 * hh + e + k;
+              if (qi < p.T && j < p.L) p.dbg_bd[(((int64_t)b * p.H + h) * p.T + qi) * p.L + j] = tb;
+            }
+            s[u][8 * g + e + k] = __builtin_fmaf(s[u][8 * g + e + k], p.scale, tb);
           }
-          s[u][8 * g + e] = __builtin_fmaf(s[u][8 * g + e], p.scale, tb);
         }
       }
     __builtin_amdgcn_wave_barrier();
