@@ -296,6 +296,14 @@ int32_t mhsa_ffn_forward(mhsa_ffn* ffn, const void* x, int32_t rows, void* out, 
  * NULL, eps as nn::LayerNorm; the residual is fused into linear2's epilogue. */
 int32_t mhsa_ffn_sublayer_forward(mhsa_ffn* ffn, void* x_inout, int32_t rows, const float* ln_gamma_host,
                                   const float* ln_beta_host, float eps, void* hip_stream);
+/* The same two on f32 activations with the module's parameters (the streaming
+ * path's form: its activations derive from the f32 caches, so in a bf16
+ * model MLX promotes every op they meet to f32, conformer.rs:1914-1919,
+ * 1956-1960; quantized weights dequantise in f32 from their cast scales).
+ * x, out, x_inout f32. */
+int32_t mhsa_ffn_forward_f32(mhsa_ffn* ffn, const float* x, int32_t rows, float* out, void* hip_stream);
+int32_t mhsa_ffn_sublayer_forward_f32(mhsa_ffn* ffn, float* x_inout, int32_t rows, const float* ln_gamma_host,
+                                      const float* ln_beta_host, float eps, void* hip_stream);
 
 /* ---- ConvolutionModule (the Conformer block's convolution sublayer) ------- */
 

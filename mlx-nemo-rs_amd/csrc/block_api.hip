@@ -29,6 +29,7 @@ struct mhsa_ffn {
   bool dirty = true;
   DevBuf wbuf;
   DevLinear dev[2];
+  DevLinear dev32[2];  // the same values in fp32 (for f32 activations)
   DevBuf act;      // [rows, F] silu(linear1(x))
   DevBuf hbuf;     // sublayer: LayerNorm output
   DevBuf ln_dev;
@@ -46,7 +47,7 @@ int32_t prepare_ffn(mhsa_ffn* f) {
   const bool bf = f->dt == mhsa::kBF16;
   const size_t es = bf ? 2 : 4;
   auto rnd = [&](float v) { return bf ? round_bf16(v) : v; };
-  size_t woff[2], sboff[2], boff[2], off = 0;
+  size_t woff[2], sboff[2], boff[2], w32off[2], off = 0;
   for (int i = 0; i < 2; ++i) {
     const size_t n = (size_t)ffn_out(f, i) * ffn_in(f, i);
     woff[i] = off;
@@ -55,6 +56,8 @@ int32_t prepare_ffn(mhsa_ffn* f) {
     if (f->lin[i].quantized) off = align_up(off + (size_t)ffn_out(f, i) * (ffn_in(f, i) / 64) * 8, 256);
     boff[i] = off;
     off = align_up(off + (size_t)ffn_out(f, i) * 4, 256);
+    w32off[i] = off;
+    if (!f->lin[i].quantized && bf) off = align_up(off + n * 4, 256);
   }
   std::vector<char> host(off, 0);
   for (int i = 0; i < 2; ++i) {
@@ -68,7 +71,11 @@ int32_t prepare_ffn(mhsa_ffn* f) {
       }
     } else if (bf) {
       uint16_t* w = reinterpret_cast<uint16_t*>(host.data() + woff[i]);
-      for (size_t e = 0; e < h.w.size(); ++e) w[e] = f32_to_bf16(h.w[e]);
+      float* w32 = reinterpret_cast<float*>(host.data() + w32off[i]);
+      for (size_t e = 0; e < h.w.size(); ++e) {
+        w[e] = f32_to_bf16(h.w[e]);
+        w32[e] = bf16_to_f32(w[e]);
+      }
     } else {
       std::memcpy(host.data() + woff[i], h.w.data(), h.w.size() * 4);
     }
@@ -84,28 +91,34 @@ int32_t prepare_ffn(mhsa_ffn* f) {
     f->dev[i].w = base + woff[i];
     f->dev[i].sb = f->lin[i].quantized ? reinterpret_cast<const float*>(base + sboff[i]) : nullptr;
     f->dev[i].bias = f->lin[i].bias.empty() ? nullptr : reinterpret_cast<const float*>(base + boff[i]);
+    f->dev32[i] = f->dev[i];
+    if (!f->lin[i].quantized && bf) f->dev32[i].w = base + w32off[i];
   }
   f->dirty = false;
   return MHSA_OK;
 }
 
-int32_t ffn_impl(mhsa_ffn* f, const void* x, int rows, void* out, const void* residual, float res_scale,
+// FeedForward on activations of dtype `act`: the module dtype, or f32 on the
+// streaming path, where a bf16 module's ops meet f32 activations and MLX
+// promotes them (its parameters keep their bf16 values).
+int32_t ffn_impl(mhsa_ffn* f, const void* x, int rows, void* out, const void* residual, float res_scale, DType act,
                  hipStream_t s) {
   if (rows <= 0) return fail(MHSA_EINVAL, "rows must be positive (got %d)", rows);
   if (!x || !out) return fail(MHSA_EINVAL, "null tensor pointer");
   if (!aligned16(x) || !aligned16(out)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
   int32_t rc = prepare_ffn(f);
   if (rc) return rc;
-  const size_t es = f->dt == mhsa::kBF16 ? 2 : 4;
+  const size_t es = mhsa::dtype_size(act);
   HIPCHK(f->act.ensure(align_up((int64_t)rows * f->F * es, 256)));
   HIPCHK(f->partial.ensure((size_t)mhsa::kGemmPartialElems * 4));
   for (int i = 0; i < 2; ++i) {
+    const DevLinear& d = act == f->dt ? f->dev[i] : f->dev32[i];
     mhsa::GemmParams p;
     p.A = i == 0 ? x : f->act.p;
     p.lda = ffn_in(f, i);
-    p.W = f->dev[i].w;
-    p.sb = f->dev[i].sb;
-    p.bias = f->dev[i].bias;
+    p.W = d.w;
+    p.sb = d.sb;
+    p.bias = d.bias;
     p.C = i == 0 ? f->act.p : out;
     p.ldc = ffn_out(f, i);
     p.M = rows;
@@ -121,9 +134,41 @@ int32_t ffn_impl(mhsa_ffn* f, const void* x, int rows, void* out, const void* re
       p.ldr = f->D;
       p.res_scale = res_scale;
     }
-    HIPCHK(mhsa::gemm(f->dt, f->dev[i].quantized, p, s));
+    HIPCHK(mhsa::gemm(act, d.quantized, p, s));
   }
   return MHSA_OK;
+}
+
+int32_t ffn_sublayer(mhsa_ffn* f, void* x, int32_t rows, const float* gamma, const float* beta, float eps, DType act,
+                     hipStream_t s) {
+  if (!x || rows <= 0) return fail(MHSA_EINVAL, "bad sublayer arguments");
+  if (!aligned16(x)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  if (f->D > mhsa::kMaxLayerNormDim)
+    return fail(MHSA_ENOTSUP, "the sublayer's LayerNorm supports d_model <= %d (got %d)", mhsa::kMaxLayerNormDim, f->D);
+  const int D = f->D;
+  const float* gd = nullptr;
+  const float* bd = nullptr;
+  if (gamma || beta) {
+    std::vector<float> tmp(2 * D);
+    const bool bf = f->dt == mhsa::kBF16;
+    for (int i = 0; i < D; ++i) {
+      const float gv = gamma ? gamma[i] : 1.f, bv = beta ? beta[i] : 0.f;
+      tmp[i] = bf ? round_bf16(gv) : gv;
+      tmp[D + i] = bf ? round_bf16(bv) : bv;
+    }
+    if (tmp != f->ln_host) {
+      if (f->ln_dev.p) HIPCHK(hipDeviceSynchronize());
+      HIPCHK(f->ln_dev.ensure(tmp.size() * 4));
+      HIPCHK(hipMemcpy(f->ln_dev.p, tmp.data(), tmp.size() * 4, hipMemcpyHostToDevice));
+      f->ln_host = tmp;
+    }
+    gd = static_cast<const float*>(f->ln_dev.p);
+    bd = gd + D;
+  }
+  HIPCHK(f->hbuf.ensure(align_up((int64_t)rows * D * mhsa::dtype_size(act), 256)));
+  HIPCHK(mhsa::layer_norm(act, x, f->hbuf.p, gd, bd, eps, rows, D, s));
+  // x + 0.5 * FF(LN(x)): the half step scales exactly (conformer.rs:1727-1729)
+  return ffn_impl(f, f->hbuf.p, rows, x, x, 0.5f, act, s);
 }
 
 }  // namespace
@@ -180,42 +225,25 @@ int32_t mhsa_ffn_load_weights(mhsa_ffn* f, const mhsa_tensor* tensors, int32_t n
 
 int32_t mhsa_ffn_forward(mhsa_ffn* f, const void* x, int32_t rows, void* out, void* hs) {
   if (!f) return fail(MHSA_EINVAL, "null handle");
-  return ffn_impl(f, x, rows, out, nullptr, 1.f, static_cast<hipStream_t>(hs));
+  return ffn_impl(f, x, rows, out, nullptr, 1.f, f->dt, static_cast<hipStream_t>(hs));
 }
+
+int32_t mhsa_ffn_forward_f32(mhsa_ffn* f, const float* x, int32_t rows, float* out, void* hs) {
+  if (!f) return fail(MHSA_EINVAL, "null handle");
+  return ffn_impl(f, x, rows, out, nullptr, 1.f, mhsa::kF32, static_cast<hipStream_t>(hs));
+}
+
 
 int32_t mhsa_ffn_sublayer_forward(mhsa_ffn* f, void* x, int32_t rows, const float* gamma, const float* beta, float eps,
                                   void* hs) {
   if (!f) return fail(MHSA_EINVAL, "null handle");
-  if (!x || rows <= 0) return fail(MHSA_EINVAL, "bad sublayer arguments");
-  if (!aligned16(x)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
-  if (f->D > mhsa::kMaxLayerNormDim)
-    return fail(MHSA_ENOTSUP, "the sublayer's LayerNorm supports d_model <= %d (got %d)", mhsa::kMaxLayerNormDim, f->D);
-  hipStream_t s = static_cast<hipStream_t>(hs);
-  const int D = f->D;
-  const float* gd = nullptr;
-  const float* bd = nullptr;
-  if (gamma || beta) {
-    std::vector<float> tmp(2 * D);
-    const bool bf = f->dt == mhsa::kBF16;
-    for (int i = 0; i < D; ++i) {
-      const float gv = gamma ? gamma[i] : 1.f, bv = beta ? beta[i] : 0.f;
-      tmp[i] = bf ? round_bf16(gv) : gv;
-      tmp[D + i] = bf ? round_bf16(bv) : bv;
-    }
-    if (tmp != f->ln_host) {
-      if (f->ln_dev.p) HIPCHK(hipDeviceSynchronize());
-      HIPCHK(f->ln_dev.ensure(tmp.size() * 4));
-      HIPCHK(hipMemcpy(f->ln_dev.p, tmp.data(), tmp.size() * 4, hipMemcpyHostToDevice));
-      f->ln_host = tmp;
-    }
-    gd = static_cast<const float*>(f->ln_dev.p);
-    bd = gd + D;
-  }
-  const size_t es = f->dt == mhsa::kBF16 ? 2 : 4;
-  HIPCHK(f->hbuf.ensure(align_up((int64_t)rows * D * es, 256)));
-  HIPCHK(mhsa::layer_norm(f->dt, x, f->hbuf.p, gd, bd, eps, rows, D, s));
-  // x + 0.5 * FF(LN(x)): the half step scales exactly (conformer.rs:1727-1729)
-  return ffn_impl(f, f->hbuf.p, rows, x, x, 0.5f, s);
+  return ffn_sublayer(f, x, rows, gamma, beta, eps, f->dt, static_cast<hipStream_t>(hs));
+}
+
+int32_t mhsa_ffn_sublayer_forward_f32(mhsa_ffn* f, float* x, int32_t rows, const float* gamma, const float* beta,
+                                      float eps, void* hs) {
+  if (!f) return fail(MHSA_EINVAL, "null handle");
+  return ffn_sublayer(f, x, rows, gamma, beta, eps, mhsa::kF32, static_cast<hipStream_t>(hs));
 }
 
 }  // extern "C"

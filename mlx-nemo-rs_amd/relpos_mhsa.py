@@ -39,7 +39,8 @@ EXPORTS = (
     "mhsa_stream_read_cache", "mhsa_stream_fill", "mhsa_forward_with_cache", "mhsa_forward_uncached",
     "mhsa_stack_create", "mhsa_stack_destroy", "mhsa_stack_load_cache", "mhsa_stack_read_cache", "mhsa_stack_fill",
     "mhsa_stack_step", "mhsa_ffn_create", "mhsa_ffn_destroy", "mhsa_ffn_set_dtype", "mhsa_ffn_load_weights",
-    "mhsa_ffn_forward", "mhsa_ffn_sublayer_forward", "mhsa_conv_create", "mhsa_conv_destroy", "mhsa_conv_set_dtype",
+    "mhsa_ffn_forward", "mhsa_ffn_sublayer_forward", "mhsa_ffn_forward_f32", "mhsa_ffn_sublayer_forward_f32",
+    "mhsa_conv_create", "mhsa_conv_destroy", "mhsa_conv_set_dtype",
     "mhsa_conv_load_weights", "mhsa_conv_cache_size", "mhsa_conv_output_dtype", "mhsa_conv_forward",
     "mhsa_conv_forward_with_cache", "mhsa_conv_sublayer_forward", "mhsa_conv_profile_enable",
     "mhsa_conv_profile_repeat", "mhsa_conv_profile_reset", "mhsa_conv_profile_count", "mhsa_conv_profile_entry",
@@ -132,6 +133,8 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_ffn_load_weights": (I, [VP, P(Tensor), I, ctypes.c_char_p, I, I, I]),
         "mhsa_ffn_forward": (I, [VP, VP, I, VP, VP]),
         "mhsa_ffn_sublayer_forward": (I, [VP, VP, I, P(ctypes.c_float), P(ctypes.c_float), F, VP]),
+        "mhsa_ffn_forward_f32": (I, [VP, VP, I, VP, VP]),
+        "mhsa_ffn_sublayer_forward_f32": (I, [VP, VP, I, P(ctypes.c_float), P(ctypes.c_float), F, VP]),
         "mhsa_conv_create": (I, [I, I, I, I, I, P(VP)]),
         "mhsa_conv_destroy": (None, [VP]),
         "mhsa_conv_set_dtype": (I, [VP, I]),
@@ -390,28 +393,33 @@ class FeedForward:
         _check(self._lib.mhsa_ffn_load_weights(self._h, arr_t, n, prefix.encode(), 1 if strict else 0, bits, group))
 
     def _check(self, x):
+        """x in the module dtype, or f32 (the streaming path's promoted form)."""
         import torch
         want = _torch_dtype(self._dtype)
-        if not x.is_cuda or x.dtype != want or not x.is_contiguous() or x.shape[-1] != self.d_model:
-            raise MhsaError(MHSA_EINVAL, f"expected a contiguous {want} GPU tensor [..., {self.d_model}]")
+        if (not x.is_cuda or x.dtype not in (want, torch.float32) or not x.is_contiguous()
+                or x.shape[-1] != self.d_model):
+            raise MhsaError(MHSA_EINVAL, f"expected a contiguous {want} or float32 GPU tensor [..., {self.d_model}]")
+        return x.dtype == torch.float32 and want != torch.float32
 
     def forward(self, x):
+        """forward (conformer.rs:2066-2072); an f32 x in a bf16 module runs
+        the promoted form (mhsa_ffn_forward_f32)."""
         import torch
-        self._check(x)
+        promoted = self._check(x)
         out = torch.empty_like(x)
-        _check(self._lib.mhsa_ffn_forward(self._h, _dptr(x), x.numel() // self.d_model, _dptr(out), _stream_ptr()))
+        fn = self._lib.mhsa_ffn_forward_f32 if promoted else self._lib.mhsa_ffn_forward
+        _check(fn(self._h, _dptr(x), x.numel() // self.d_model, _dptr(out), _stream_ptr()))
         return out
 
     def sublayer_forward_(self, x, gamma=None, beta=None, eps=1e-5):
         """In place x <- x + 0.5 * forward(LayerNorm(x)) (conformer.rs:1703-1729)."""
-        self._check(x)
+        promoted = self._check(x)
         g = None if gamma is None else _host_f32(gamma)
         b = None if beta is None else _host_f32(beta)
         fp = ctypes.POINTER(ctypes.c_float)
-        _check(self._lib.mhsa_ffn_sublayer_forward(self._h, _dptr(x), x.numel() // self.d_model,
-                                                   None if g is None else g.ctypes.data_as(fp),
-                                                   None if b is None else b.ctypes.data_as(fp), float(eps),
-                                                   _stream_ptr()))
+        fn = self._lib.mhsa_ffn_sublayer_forward_f32 if promoted else self._lib.mhsa_ffn_sublayer_forward
+        _check(fn(self._h, _dptr(x), x.numel() // self.d_model, None if g is None else g.ctypes.data_as(fp),
+                  None if b is None else b.ctypes.data_as(fp), float(eps), _stream_ptr()))
         return x
 
 

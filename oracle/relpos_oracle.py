@@ -637,6 +637,14 @@ def silu(x: np.ndarray, dtype: str = F32) -> np.ndarray:
     return _rnd(x * sig, dtype)
 
 
+def _pointwise(layer: LinearLayer, x, act: str, dtype: str):
+    """A pointwise conv on activations stored in `act`: in the module dtype
+    (`forward`) or f32 with the cast parameters promoted (`forward_promoted`)."""
+    if act == dtype:
+        return layer.forward(x, dtype)
+    return layer.forward_promoted(x, dtype)
+
+
 @dataclass
 class FeedForwardParams:
     """linear1 [ff_dim, d_model], linear2 [d_model, ff_dim] (conformer.rs:2031-2064)."""
@@ -645,16 +653,27 @@ class FeedForwardParams:
     linear2: LinearLayer
 
 
-def feed_forward(p: FeedForwardParams, x: np.ndarray, dtype: str = F32) -> np.ndarray:
-    """FeedForward::forward (conformer.rs:2066-2072): linear2(silu(linear1(x)))."""
-    return p.linear2.forward(silu(p.linear1.forward(np.asarray(x, dtype=np.float64), dtype), dtype), dtype)
+def feed_forward(p: FeedForwardParams, x: np.ndarray, dtype: str = F32, act: Optional[str] = None) -> np.ndarray:
+    """FeedForward::forward (conformer.rs:2066-2072): linear2(silu(linear1(x))).
+    `act` is the dtype x is stored in (default `dtype`): f32 activations in a
+    bf16 module (the streaming path) promote every op to f32 over the
+    parameters' bf16 values."""
+    act = act or dtype
+    x = np.asarray(x, dtype=np.float64)
+    return _pointwise(p.linear2, silu(_pointwise(p.linear1, x, act, dtype), act), act, dtype)
 
 
-def feed_forward_sublayer(p: FeedForwardParams, x, gamma=None, beta=None, dtype: str = F32, eps: float = 1e-5):
-    """x + 0.5 * FeedForward(LayerNorm(x)) (conformer.rs:1703-1729): the half
-    is cast to the output dtype, the scaled output and the sum stored."""
-    y = feed_forward(p, layer_norm(x, gamma, beta, eps, dtype), dtype)
-    return _rnd(np.asarray(x, dtype=np.float64) + _rnd(to_dtype(0.5, dtype) * y, dtype), dtype)
+def feed_forward_sublayer(p: FeedForwardParams, x, gamma=None, beta=None, dtype: str = F32, eps: float = 1e-5,
+                          act: Optional[str] = None):
+    """x + 0.5 * FeedForward(LayerNorm(x)) (conformer.rs:1703-1729, 1914-1919):
+    the half is cast to the output's dtype, the scaled output and the sum
+    stored; the LayerNorm parameters hold their `dtype` values, its output is
+    stored in `act`."""
+    act = act or dtype
+    g = None if gamma is None else to_dtype(gamma, dtype)
+    b = None if beta is None else to_dtype(beta, dtype)
+    y = feed_forward(p, layer_norm(x, g, b, eps, act), dtype, act)
+    return _rnd(np.asarray(x, dtype=np.float64) + _rnd(to_dtype(0.5, act) * y, act), act)
 
 
 # ---------------------------------------------------------------------------
@@ -731,14 +750,6 @@ def batch_norm_inference(x, mean, var, weight, bias, dtype: str, param_dtype: st
     y = _rnd(y * inv, dtype)
     y = _rnd(to_dtype(weight, param_dtype) * y, dtype)
     return _rnd(y + to_dtype(bias, param_dtype), dtype)
-
-
-def _pointwise(layer: LinearLayer, x, act: str, dtype: str):
-    """A pointwise conv on activations stored in `act`: in the module dtype
-    (`forward`) or f32 with the cast parameters promoted (`forward_promoted`)."""
-    if act == dtype:
-        return layer.forward(x, dtype)
-    return layer.forward_promoted(x, dtype)
 
 
 def conv_module(p: ConvModuleParams, x, dtype: str = F32, act: Optional[str] = None,

@@ -84,6 +84,7 @@ def test_conv_forward_against_oracle(dtype, norm, causal, k, quant, B, T, d, len
     (O.BF16, "layer_norm", True, 16, 14, 1024),
     (O.F32, "batch_norm", False, 4, 5, 256),
     (O.BF16, "batch_norm", False, 2, 100, 512),
+    (O.F32, "layer_norm", False, 70, 3, 128),
 ])
 def test_conv_streaming_cache_against_oracle(dtype, norm, quant, B, chunk, d):
     """forward_with_cache over consecutive chunks (K = 9, cache [B, D, 8]
@@ -91,7 +92,8 @@ def test_conv_streaming_cache_against_oracle(dtype, norm, quant, B, chunk, d):
     the oracle; the last chunk has ragged lengths (padding frames zeroed
     before they reach the cache). Chunks of 14 (the streaming shape) and 5
     (< K - 1, so part of the old cache stays) update in place from one frame
-    tile; 100 frames span two tiles and read a copy of the cache."""
+    tile; 100 frames span two tiles and read a copy of the cache; 70 sessions
+    take two launches' batch chunks, each with its own cache slice."""
     rng = np.random.default_rng(2000 + chunk)
     k = 9
     w = conv_weights(rng, d, k, norm, quant)

@@ -1082,3 +1082,33 @@ def test_feed_forward_against_oracle(dtype, quant, rows):
     err = row_rel_err(host(xd), ref)
     print(f"  sublayer: per-row error / row max {err:.3e}")
     assert err < (BF16_TOL if dtype == O.BF16 else F32_TOL)
+
+
+@pytest.mark.parametrize("quant", [False, True])
+def test_feed_forward_f32_activations_in_bf16_module(quant):
+    """The streaming path's FeedForward: f32 activations meet a bf16 module,
+    so every op promotes to f32 over the parameters' bf16 values (quantized
+    weights dequantised in f32 from their bf16-cast scales), and nothing is
+    rounded to bf16; forward and the half-step sublayer, within the fp32
+    bound, 224 rows (16 sessions x 14 frames)."""
+    rng = np.random.default_rng(93)
+    d, f = 1024, 4096
+    w = _ffn_weights(rng, d, f, quant)
+    p = _ffn_oracle(w)
+    ff = M.FeedForward(d, f, True)
+    ff.load_weights(w, "ff")
+    ff.set_dtype(O.BF16)
+    x = rng.standard_normal((224, d)).astype(np.float32).astype(np.float64)
+    got = host(ff.forward(dev(x, O.F32)))
+    ref = O.feed_forward(p, x, O.BF16, act=O.F32)
+    err = row_rel_err(got, ref)
+    print(f"feed_forward bf16 module, f32 activations, quant={quant}: per-row error {err:.3e}")
+    assert err < F32_TOL
+    gamma = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    beta = rng.normal(0, 0.1, d).astype(np.float32)
+    xd = dev(x, O.F32)
+    ff.sublayer_forward_(xd, gamma, beta)
+    ref = O.feed_forward_sublayer(p, x, gamma, beta, O.BF16, act=O.F32)
+    err = row_rel_err(host(xd), ref)
+    print(f"  sublayer: per-row error {err:.3e}")
+    assert err < F32_TOL

@@ -810,3 +810,22 @@ def test_conv_module_bf16_causal_promotes_to_f32():
     # the bf16 rounding of the rsqrt term is load-bearing: an f32 one moves the result
     alt = tail(torch.rsqrt(s.float()))
     assert np.max(np.abs(alt - got)) / np.max(np.abs(ref)) > 1e-4
+
+
+def test_feed_forward_promoted_matches_torch_promotion():
+    """f32 activations through a bf16 FeedForward: torch's own type
+    promotion of an f32 tensor against bf16 parameters gives the oracle's
+    promoted form (f32 ops on bf16-valued weights, no bf16 rounding), within
+    torch's f32 rounding; the bf16-rounded module form differs by far more."""
+    p = _ffn_params(16, 64, 35)
+    x = np.random.default_rng(36).standard_normal((5, 16)).astype(np.float32)
+    bf = torch.bfloat16
+    t = lambda a: torch.tensor(np.asarray(a, dtype=np.float32)).to(bf)
+    X = torch.tensor(x)
+    h = X @ t(p.linear1.weight).float().T + t(p.linear1.bias)
+    assert h.dtype == torch.float32
+    h = h * torch.sigmoid(h)
+    y = (h @ t(p.linear2.weight).float().T + t(p.linear2.bias)).double().numpy()
+    got = O.feed_forward(p, x, O.BF16, act=O.F32)
+    assert np.max(np.abs(got - y)) / np.max(np.abs(y)) < 1e-6
+    assert np.max(np.abs(O.feed_forward(p, O.bf16_round(x), O.BF16) - got)) / np.max(np.abs(y)) > 1e-3
