@@ -368,14 +368,16 @@ struct TileCfg {
   static constexpr int ABYTES = BM * 128, STAGE = BM * 128 + BN * BROW;
   static constexpr int NA = BM / 32;               // A loads per wave per stage (1 KB each)
   static constexpr int NB = BN * BROW / 4096;      // B loads per wave per stage (1 KB each)
-  static constexpr int OP = WN * 2 + 16;           // staged output row pitch (bytes)
+  static constexpr int OP = WN * 2 + 16;           // staged output row pitch (bytes), row-major
+  static constexpr int OPT = WM * 2 + 16;          // staged column pitch (bytes), transposed
+  static constexpr int REG = WM * OP > WN * OPT ? WM * OP : WN * OPT;  // one wave's staging region
   // loads spread between MFMAs whenever a tile of at least 128 x 128 has a
   // CU to itself (a 64 x 64 tile has one MFMA per wave and k-step)
   static constexpr bool ILV = BM * BN >= 192 * 192 || (NS > 2 && BM * BN >= 128 * 128);
   // a wave block holding both C and V^T columns stages them twice (row-major
   // and transposed) where LDS allows: 8 staging regions
-  static constexpr bool VMIX = 8 * WM * OP <= 160 * 1024;
-  static constexpr int STG = (VMIX ? 8 : 4) * WM * OP;
+  static constexpr bool VMIX = 8 * REG <= 160 * 1024;
+  static constexpr int STG = (VMIX ? 8 : 4) * REG;
   static constexpr int LDS = NS * STAGE > STG ? NS * STAGE : STG;
   static_assert(LDS <= 160 * 1024, "tile exceeds LDS");
 };
@@ -620,15 +622,14 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
   // contiguous), so that a V^T run of 8 tokens is one 16-byte LDS read (read
   // from a row-major block, the run's rows 8 apart share two banks across the
   // wave: measured 6.2 against 2.5 us for the epilogue of a V block)
-  static_assert(C::WM == C::WN, "square wave blocks (the transposed staging reuses the row pitch)");
   __syncthreads();
-  char* st = smem + w * (C::WM * C::OP);
+  char* st = smem + w * C::REG;
   const int row0 = m0 + wm * C::WM, col0 = n0 + wn * C::WN;
   // columns [col0, col0 + ncn) go to C, the rest of the block to V^T
   const int ncn = p.vt ? min(max(p.vt_col0 - col0, 0), C::WN) : C::WN;
   const bool vtw = ncn < C::WN;
   const bool both = vtw && ncn > 0 && C::VMIX;  // C columns row-major in st, V^T columns transposed in stv
-  char* stv = both ? smem + (4 + w) * (C::WM * C::OP) : st;
+  char* stv = both ? smem + (4 + w) * C::REG : st;
   if (!vtw || both) {
 #pragma unroll
     for (int i = 0; i < C::TM; ++i)
@@ -651,7 +652,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
         for (int q = 0; q < 4; ++q)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            *reinterpret_cast<bf16*>(stv + (j * 32 + 8 * q + 4 * (lane >> 5) + e) * C::OP + (i * 32 + (lane & 31)) * 2) =
+            *reinterpret_cast<bf16*>(stv + (j * 32 + 8 * q + 4 * (lane >> 5) + e) * C::OPT + (i * 32 + (lane & 31)) * 2) =
                 (bf16)acc[j][i][4 * q + e];
   }
   constexpr int CPR = C::WN / 8;
@@ -702,7 +703,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
       if (row0 + r >= m_end) continue;
       bf16x8 v;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = *reinterpret_cast<const bf16*>(st + (c * 8 + e) * C::OP + r * 2);
+      for (int e = 0; e < 8; ++e) v[e] = *reinterpret_cast<const bf16*>(st + (c * 8 + e) * C::OPT + r * 2);
       store_c(r, col0 + c * 8, v);
     }
   }
@@ -719,7 +720,7 @@ __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
       const int tok = t0 + mc * 8;
       if (tok >= p.vt_Tpad) continue;
       const int col = col0 + nl;
-      bf16x8 v = *reinterpret_cast<const bf16x8*>(stv + nl * C::OP + mc * 16);
+      bf16x8 v = *reinterpret_cast<const bf16x8*>(stv + nl * C::OPT + mc * 16);
       if (p.bias) {
         const float b = p.bias[col];
 #pragma unroll
@@ -1100,12 +1101,14 @@ int split_count(const GemmParams& p) {
 // Estimated duration of one launch of the tile kernel, in units of one
 // 192 x 192 tile pass at K = 1024 with every CU busy (measured: a 256 x 256
 // pass 1.45; 128 x 128 0.5 alone on a CU with four stages, 0.75 for a pass of
-// two per CU with two stages).
+// two per CU with two stages; 192 x 128 taken as 0.7, two thirds of the
+// MFMAs of a 192 x 192 pass plus its fixed prologue and epilogue).
 template <int BM, int BN>
 double tile_cost(const GemmParams& p) {
   const int64_t tiles = m_tiles<BM>(p) * (p.N / BN);
   double c;
   if (BM == 128 && BN == 128) c = tiles <= 256 ? 0.5 : (double)((tiles + 511) / 512) * 0.75;
+  else if (BM == 192 && BN == 128) c = (double)((tiles + 255) / 256) * 0.7;
   else c = (double)((tiles + 255) / 256) * (BM * BN == 256 * 256 ? 1.45 : 1.0);
   return c * p.K / 1024.0;
 }
@@ -1147,10 +1150,13 @@ bool dispatch_tile(const GemmParams& p, hipStream_t s, hipError_t& err) {
   int pick = 128;
   if (p.N % 192 == 0 && tile_cost<192, 192>(p) < best) best = tile_cost<192, 192>(p), pick = 192;
   if (p.N % 256 == 0 && tile_cost<256, 256>(p) < best) best = tile_cost<256, 256>(p), pick = 256;
-  // stages: three (loads two ahead) for 192 x 192; four for a 128 x 128 tile
-  // that has its CU to itself, two when two share one; 256 x 256 fits two
+  if (tile_cost<192, 128>(p) < best) best = tile_cost<192, 128>(p), pick = 1;
+  // stages: three (loads two ahead) for 192 x 192 and 192 x 128; four for a
+  // 128 x 128 tile that has its CU to itself, two when two share one;
+  // 256 x 256 fits two
   if (pick == 256) err = launch_tile<256, 256, QUANT, 2>(p, s);
   else if (pick == 192) err = launch_tile<192, 192, QUANT, 3>(p, s);
+  else if (pick == 1) err = launch_tile<192, 128, QUANT, 3>(p, s);
   else if (m_tiles<128>(p) * (p.N / 128) <= 256) err = launch_tile<128, 128, QUANT, 4>(p, s);
   else err = launch_tile<128, 128, QUANT, 2>(p, s);
   return true;

@@ -268,10 +268,11 @@ def _biased_weights(seed, d_model, n_heads, sigma):
     return w, rng
 
 
-@pytest.mark.parametrize("rows", [3000, 1537])
+@pytest.mark.parametrize("rows", [3000, 1537, 6000])
 def test_linear_bf16_bias_large(rows):
     """y = T(T(x W^T) + b) (quantization.rs:126-162) on row counts that take
-    the tiled bf16 GEMM, including a ragged last tile. The fp32 sum may round
+    the tiled bf16 GEMM (6000 rows: 192 x 128 tiles), including a ragged last
+    tile. The fp32 sum may round
     T(x W^T) one ulp away from the float64 product before the bias add, so each
     output is within one ulp of the pre-bias value, one ulp of the result and
     one fp32 rounding unit of sum |x||w| of the oracle."""
@@ -358,6 +359,26 @@ def test_forward_bf16_more_blocks_than_cus():
     got = host(layer.forward(dev(x, O.BF16), dev(pos, O.BF16), None, M.key_padding_mask(lengths, T)))
     err = abs_err(got, ref)
     print(f"bf16 two rounds: max abs error {err:.3e} (max |ref| {np.max(np.abs(ref)):.2f})")
+    assert err < BF16_TOL
+
+
+def test_forward_bf16_4000_rows():
+    """The 0.6B-shape offline bf16 layer at B=4, T=1000 (4000 rows): its
+    Q/K/V projection runs as 192 x 128 tiles whose blocks hold both K and V^T
+    columns, and its 8 query blocks per item over 16 key tiles; key padding,
+    against the oracle within the bf16 tolerance."""
+    D, H, T, B = 1024, 8, 1000, 4
+    w, rng = _biased_weights(83, D, H, 0.1)
+    x = rng.normal(size=(B, T, D))
+    lengths = [int(v) for v in rng.integers(700, T + 1, size=B)]
+    lengths[1] = T
+    p = oracle_params(w, D, H)
+    pos = O.RelPositionalEncoding(D, 5000, True).get_encoding(T)
+    ref = O.mhsa_forward(p, O.bf16_round(x), O.bf16_round(pos), None, O.key_padding_mask(lengths, T), dtype=O.BF16)
+    layer = gpu_layer(w, D, H, True, O.BF16)
+    got = host(layer.forward(dev(x, O.BF16), dev(pos, O.BF16), None, M.key_padding_mask(lengths, T)))
+    err = abs_err(got, ref)
+    print(f"bf16 4000 rows: max abs error {err:.3e} (max |ref| {np.max(np.abs(ref)):.2f})")
     assert err < BF16_TOL
 
 
