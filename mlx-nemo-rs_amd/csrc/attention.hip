@@ -413,24 +413,27 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
 
 // ---------------------------------------------------------------------------
 // bf16 path with 32x32x16 MFMAs: 32 queries per wave, NW waves per
-// workgroup, 64-key tiles. Every operand a tile needs is in LDS before the
-// tile starts; the next tile's operands stream in meanwhile with
-// direct-to-LDS loads (global_load_lds, 64 lanes per load, lane l at LDS
-// base + l * size), so the loop waits on global memory only at its single
-// barrier per tile.
+// workgroup, NK-key tiles, in two forms: 4 waves over 64-key tiles (one wave
+// per SIMD) and 8 waves over 32-key tiles (d_k = 128 only; two waves per
+// SIMD, so one issues while the other waits on LDS or on an MFMA result).
+// Every operand a tile needs is in LDS before the tile starts; the next
+// tile's operands stream in meanwhile with direct-to-LDS loads
+// (global_load_lds, 64 lanes per load, lane l at LDS base + l * size), so the
+// loop waits on global memory only at its single barrier per tile.
 //  * K rows and a V^T tile (written transposed by the projection GEMM) are
 //    double-buffered and shared by the waves. K rows are staged in the order
 //    key(m) = m with bits 2 and 3 swapped, so the score MFMA's output
 //    registers hold, per lane, 8 consecutive keys of each 16-key step:
 //    exactly the B operand layout of the PV MFMA, whose V^T operand is then
 //    one 16-byte LDS read.
-//  * Position rows live in a 256-row ring. Wave w needs, for key tile k,
-//    96 rows starting at pb_w = center - qoff - (i_w + 31) + j0 (three 32-row
-//    band tiles covering the pairs of its 32 queries and 64 keys); the last
-//    band tile of one key tile is the first of the next, so two are computed
-//    per step. Ring row rr holds position row R0 + rr with R0 the first row
-//    any wave needs: tile k uses rr in [64k + 32, 64k + 192) and loads
-//    [64k + 192, 64k + 256) for tile k + 1, 224 live rows.
+//  * Position rows live in a ring of QB + 2 NK rows. Wave w needs, for key
+//    tile k, 32 (NU + 1) rows (NU = NK / 32) starting at
+//    pb_w = center - qoff - (i_w + 31) + j0: NU + 1 band tiles of 32 rows
+//    covering the pairs of its 32 queries and NK keys; the last band tile of
+//    one key tile is the first of the next, so NU are computed per step.
+//    Ring row rr holds position row R0 + rr with R0 the first row any wave
+//    needs: tile k uses rr in [NK k, NK k + QB + NK) and loads
+//    [NK k + QB + NK, NK k + QB + 2 NK) for tile k + 1.
 //  * LDS rows are unpadded; 16-byte chunk j of a K, V^T or ring row r sits
 //    at chunk j ^ (r % chunks-per-row), so the 8 lanes an LDS read serves
 //    together hit 8 distinct bank groups.
@@ -449,12 +452,13 @@ template <int DK, int NW>
 struct Cfg2 {
   static constexpr int NT = 64 * NW;
   static constexpr int QB = 32 * NW;
-  static constexpr int NK = 64;
-  static constexpr int RB = DK * 2;        // bytes per K / position row
-  static constexpr int KCN = RB / 16;      // 16-byte chunks per K / position row
-  static constexpr int VCN = NK * 2 / 16;  // 16-byte chunks per V^T row (8)
-  static constexpr int RING = 256;         // position ring rows
-  static constexpr int RMP = 100;          // remap row pitch (bf16 elements)
+  static constexpr int NK = NW == 8 ? 32 : 64;   // keys per tile
+  static constexpr int NU = NK / 32;             // 32-key score blocks (and new band tiles) per tile
+  static constexpr int RB = DK * 2;              // bytes per K / position row
+  static constexpr int KCN = RB / 16;            // 16-byte chunks per K / position row
+  static constexpr int VCN = NK * 2 / 16;        // 16-byte chunks per V^T row
+  static constexpr int RING = QB + 2 * NK;       // position ring rows
+  static constexpr int RMP = 32 * (NU + 1) + 4;  // remap row pitch (bf16 elements)
   static constexpr int KBUF = NK * RB;
   static constexpr int VBUF = DK * NK * 2;
   static constexpr int K_OFF = 0;                    // two K tiles
@@ -466,13 +470,13 @@ struct Cfg2 {
   static constexpr int KDMA = KBUF / 1024 / NW;      // 1 KB direct-to-LDS loads per wave and tile
   static constexpr int VDMA = VBUF / 1024 / NW;
   static constexpr int RPL = 1024 / RB;              // position rows per 1 KB load
-  static constexpr int PDMA = 64 / RPL / NW;         // position loads per wave for 64 rows
-  static_assert(KDMA * NW * 1024 == KBUF && VDMA * NW * 1024 == VBUF && PDMA * NW * RPL == 64, "tile split");
+  static constexpr int PDMA = NK / RPL / NW;         // position loads per wave for NK rows
+  static_assert(KDMA * NW * 1024 == KBUF && VDMA * NW * 1024 == VBUF && PDMA * NW * RPL == NK, "tile split");
   static_assert(KDMA + VDMA <= NS && PDMA <= NS, "one load per band / score MFMA step");
   static_assert(LDS <= 160 * 1024, "LDS");
 };
 
-// Tile-local key held by LDS K row m (an involution on [0, 64)).
+// Tile-local key held by LDS K row m (an involution on [0, 32) and [0, 64)).
 __device__ __forceinline__ constexpr int swap23(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -481,7 +485,7 @@ typedef __bf16 bf16x8_a2 __attribute__((ext_vector_type(8), aligned(2)));
 template <int DK, int NW, bool DEBUG>
 __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, int nb) {
   using C = Cfg2<DK, NW>;
-  constexpr int QB = C::QB, NK = C::NK, NS = C::NS, RB = C::RB;
+  constexpr int QB = C::QB, NK = C::NK, NU = C::NU, NS = C::NS, RB = C::RB;
   constexpr int PF = 3;  // MFMA steps an LDS operand read is issued ahead
   __shared__ __attribute__((aligned(16))) char smem[C::LDS];
 
@@ -544,7 +548,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   int top_j = -1;
   const int jfirst = (jbeg / NK) * NK;
   // ring row rr holds position row R0 + rr
-  const int R0 = p.center - p.qoff - (i0 + 31) + jfirst - 96;
+  const int R0 = p.center - p.qoff - (i0 + 31) + jfirst - 32 * (NW - 1);
 
   const char* kbase = reinterpret_cast<const char*>(p.k) + ((int64_t)b * p.kv_bs + h * DK) * 2;
   const char* vtbase = reinterpret_cast<const char*>(p.vt) + ((int64_t)h * DK * p.vt_ld + (int64_t)b * p.vt_bs) * 2;
@@ -613,7 +617,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
         rp, (lds_void*)(smem + C::P_OFF + ((rr0 + (w * C::PDMA + g) * C::RPL) % C::RING) * RB), 16, (int)roff[g],
         n0 * (int)p.p_rs * 2, 0, 0);
   };
-  // Ring rows [rr0, rr0 + 64) (rr0 a multiple of 64): this wave's share of
+  // Ring rows [rr0, rr0 + NK) (rr0 a multiple of NK): this wave's share of
   // the position rows. Rows outside the table read the p_pad slack around it
   // (finite).
   // Every pair reading such a row lies outside its query's interval (past the
@@ -670,14 +674,13 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 #pragma unroll
   for (int d = 0; d < DK / 32; ++d) o[d] = floatx16{};
   l_run = 0.f;
-  // ring row of band tile 0 of this wave for key tile k: 64k + 96 - 32w
-  int rrw = 96 - 32 * w;
+  // ring row of band tile 0 of this wave for key tile k: NK k + 32 (NW - 1 - w)
+  int rrw = 32 * (NW - 1 - w);
   bf16x16 carry = bf16x16{};  // band tile 0 of the current key tile, as stored
   if (jfirst < jend) {
     load_tile(jfirst, 0);
-    load_ring(0);
-    load_ring(64);
-    load_ring(128);
+#pragma unroll
+    for (int rr = 0; rr < QB + NK; rr += NK) load_ring(rr);
   }
   __syncthreads();
   if (jfirst < jend) carry = pack(band_tile(rrw));
@@ -690,60 +693,65 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
     // step of the band and score loops below: in one burst they stall the
     // wave while the memory pipe takes them. The last tile reloads itself,
     // unused, so that every iteration issues the same loads.
-    const int jn = more ? j0 + NK : j0, rr0n = rrw + 32 * w + 96;
+    const int jn = more ? j0 + NK : j0, rr0n = rrw - 32 * (NW - 1 - w) + QB + NK;
 
     // Band tiles first, each stored to the remap strip as soon as it is
     // done (rel_shift: strip column n of query column c pairs with key
     // j0 + n - 31 + c), so few accumulators are live at once.
     put(carry, 0);
     {
-      // band tiles 1 and 2 as two interleaved MFMA chains
-      floatx16 b1 = floatx16{}, b2 = floatx16{};
-      const char* r1 = smem + C::P_OFF + ((rrw + 32) % C::RING) * RB;
-      const char* r2 = smem + C::P_OFF + ((rrw + 64) % C::RING) * RB;
+      // band tiles 1 .. NU as interleaved MFMA chains
+      floatx16 bt[NU];
+      const char* rbt[NU];
+#pragma unroll
+      for (int u = 0; u < NU; ++u) {
+        bt[u] = floatx16{};
+        rbt[u] = smem + C::P_OFF + ((rrw + 32 * (u + 1)) % C::RING) * RB;
+      }
       // operand reads run PF steps ahead of the MFMAs; the sched_barriers pin
       // that order (the LDS latency is several MFMAs long)
-      bf16x8 a1[PF], a2[PF];
+      bf16x8 ab[PF][NU];
 #pragma unroll
-      for (int st = 0; st < PF; ++st) {
-        a1[st] = *reinterpret_cast<const bf16x8*>(r1 + lo[st]);
-        a2[st] = *reinterpret_cast<const bf16x8*>(r2 + lo[st]);
-      }
+      for (int st = 0; st < PF; ++st)
+#pragma unroll
+        for (int u = 0; u < NU; ++u) ab[st][u] = *reinterpret_cast<const bf16x8*>(rbt[u] + lo[st]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
-        b1 = mma32(a1[st % PF], qv[st], b1);
-        b2 = mma32(a2[st % PF], qv[st], b2);
-        if (st + PF < NS) {
-          a1[st % PF] = *reinterpret_cast<const bf16x8*>(r1 + lo[st + PF]);
-          a2[st % PF] = *reinterpret_cast<const bf16x8*>(r2 + lo[st + PF]);
-        }
+#pragma unroll
+        for (int u = 0; u < NU; ++u) bt[u] = mma32(ab[st % PF][u], qv[st], bt[u]);
+        if (st + PF < NS)
+#pragma unroll
+          for (int u = 0; u < NU; ++u) ab[st % PF][u] = *reinterpret_cast<const bf16x8*>(rbt[u] + lo[st + PF]);
         if (st < C::KDMA + C::VDMA) dma_kv(st, jn, buf ^ 1);
         __builtin_amdgcn_sched_barrier(0);
       }
-      put(pack(b1), 1);
-      carry = pack(b2);
-      put(carry, 2);
+#pragma unroll
+      for (int u = 0; u + 1 < NU; ++u) put(pack(bt[u]), u + 1);
+      carry = pack(bt[NU - 1]);
+      put(carry, NU);
     }
     rrw += NK;
 
     // S = K . q_u: output row m of block u is key 32u + swap23(m)
     const char* Ks = smem + C::K_OFF + buf * C::KBUF;
-    floatx16 s[2] = {floatx16{}, floatx16{}};
+    floatx16 s[NU];
+#pragma unroll
+    for (int u = 0; u < NU; ++u) s[u] = floatx16{};
     {
-      bf16x8 ka[PF][2];
+      bf16x8 ka[PF][NU];
 #pragma unroll
       for (int st = 0; st < PF; ++st)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) ka[st][u] = *reinterpret_cast<const bf16x8*>(Ks + 32 * u * RB + lo[st]);
+        for (int u = 0; u < NU; ++u) ka[st][u] = *reinterpret_cast<const bf16x8*>(Ks + 32 * u * RB + lo[st]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
 #pragma unroll
-        for (int u = 0; u < 2; ++u) s[u] = mma32(ka[st % PF][u], qu[st], s[u]);
+        for (int u = 0; u < NU; ++u) s[u] = mma32(ka[st % PF][u], qu[st], s[u]);
         if (st + PF < NS)
 #pragma unroll
-          for (int u = 0; u < 2; ++u)
+          for (int u = 0; u < NU; ++u)
             ka[st % PF][u] = *reinterpret_cast<const bf16x8*>(Ks + 32 * u * RB + lo[st + PF]);
         if (st < C::PDMA) dma_ring(st, rr0n);
         __builtin_amdgcn_sched_barrier(0);
@@ -762,7 +770,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
     const unsigned sh = 16u * (unsigned)(n0 & 1);
     float tmax = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < NU; ++u)
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
         // (read as bf16 pairs, the element type the strip is written with, so
@@ -801,7 +809,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
       asm volatile("" : "+v"(jb));
       const unsigned span = (unsigned)(iv.y - iv.x);
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < NU; ++u)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           if ((unsigned)(jb + 32 * u + 16 * (r >> 3) + (r & 7)) >= span) s[u][r] = -INFINITY;
@@ -809,7 +817,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
     if (DEBUG && p.dbg_top) {
       // keys in increasing order within the lane; strict > keeps the lowest
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+      for (int u = 0; u < NU; ++u)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           if (s[u][r] > top_v) {
@@ -818,7 +826,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
           }
     }
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < NU; ++u)
 #pragma unroll
       for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[u][r]);
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
@@ -835,7 +843,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
     const float msc = m_ref == -INFINITY ? 0.f : m_ref * sc;
     float psum = 0.f;
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int u = 0; u < NU; ++u)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         s[u][r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[u][r], sc, -msc));  // exp2(-inf) = 0
@@ -857,8 +865,8 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
       vread(0, vo[0]);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int step = 0; step < 4; ++step) {
-        if (step + 1 < 4) vread(step + 1, vo[(step + 1) & 1]);
+      for (int step = 0; step < NK / 16; ++step) {
+        if (step + 1 < NK / 16) vread(step + 1, vo[(step + 1) & 1]);
         const int u = step >> 1, jj = step & 1;
         bf16x8 pb8;
 #pragma unroll
@@ -902,9 +910,9 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   }
 }
 
-template <int DK, bool DEBUG>
+template <int DK, int NW, bool DEBUG>
 hipError_t launch2(AttnParams p, int nb, hipStream_t s) {
-  using C = Cfg2<DK, 4>;
+  using C = Cfg2<DK, NW>;
   const int64_t work = (int64_t)(p.T + C::QB - 1) / C::QB * p.H * nb;
   if (work > (1 << 30)) return hipErrorInvalidValue;
   // items by descending work (query blocks x key tiles), ties in item order
@@ -918,13 +926,31 @@ hipError_t launch2(AttnParams p, int nb, hipStream_t s) {
   }
   std::stable_sort(p.order, p.order + nb, [&](int a, int b) { return cost[a] > cost[b]; });
   const dim3 grid((unsigned)((work + 7) / 8 * 8));
-  hipLaunchKernelGGL((attn_bf16_kernel<DK, 4, DEBUG>), grid, dim3(C::NT), 0, s, p, nb);
+  hipLaunchKernelGGL((attn_bf16_kernel<DK, NW, DEBUG>), grid, dim3(C::NT), 0, s, p, nb);
   return hipGetLastError();
+}
+
+// The 8-wave form (d_k = 128) where its 256-query blocks give at least
+// kWide8 workgroups and every query sees every key up to the padding;
+// otherwise the 4-wave form. (Under a limited context every wave of a block
+// computes the key tiles of all the block's windows: 512 keys per query on
+// +-128-frame windows against 384 with 128-query blocks, and the 8-wave form
+// measured 5% slower there, over 7500 frames.)
+constexpr int kWide8 = 160;
+template <int DK>
+bool use_wide(const AttnParams& p, int nb) {
+  if constexpr (DK != 128) return false;
+  if (p.has_ctx && (p.left >= 0 || p.right >= 0)) return false;
+  return (int64_t)(p.T + Cfg2<128, 8>::QB - 1) / Cfg2<128, 8>::QB * p.H * nb >= kWide8;
 }
 
 template <int DK>
 hipError_t dispatch_bf16(const AttnParams& p, int nb, hipStream_t s) {
-  return (p.dbg_bd || p.dbg_top) ? launch2<DK, true>(p, nb, s) : launch2<DK, false>(p, nb, s);
+  const bool dbg = p.dbg_bd || p.dbg_top;
+  if constexpr (DK == 128) {
+    if (use_wide<DK>(p, nb)) return dbg ? launch2<DK, 8, true>(p, nb, s) : launch2<DK, 8, false>(p, nb, s);
+  }
+  return dbg ? launch2<DK, 4, true>(p, nb, s) : launch2<DK, 4, false>(p, nb, s);
 }
 
 // One row per DK/8 lanes: each lane takes 8 d_k values, then a lane-group sum.
@@ -1202,9 +1228,10 @@ __global__ void pos_index_kernel(int T, int L, int qoff, int center, int32_t* ou
 
 }  // namespace
 
-int bf16_pos_pad(const AttnParams& p, int nb) {
-  constexpr int QB = Cfg2<128, 4>::QB, NK = Cfg2<128, 4>::NK;
-  static_assert(Cfg2<64, 4>::QB == QB, "one query block size");
+template <int NW>
+int pos_pad_for(const AttnParams& p, int nb) {
+  // (query block and key tile of a form do not depend on d_k)
+  constexpr int QB = Cfg2<128, NW>::QB, NK = Cfg2<128, NW>::NK;
   int need = 0;
   const int nqb = (p.T + QB - 1) / QB;
   for (int bl = 0; bl < nb; ++bl)
@@ -1214,13 +1241,16 @@ int bf16_pos_pad(const AttnParams& p, int nb) {
       key_range(p, bl, i0, imin(i0 + QB, p.T), jbeg, jend);
       const int jfirst = jbeg / NK * NK;
       if (jfirst >= jend) continue;
-      // the kernel reads ring rows rr in [0, 64 * tiles + 192): position rows R0 + rr
-      const int64_t R0 = (int64_t)p.center - p.qoff - (i0 + 31) + jfirst - 96;
-      const int64_t hi = R0 + (int64_t)(jend - jfirst + NK - 1) / NK * NK + 192;
+      // the kernel reads ring rows rr in [0, NK * tiles + QB + NK): position rows R0 + rr
+      const int64_t R0 = (int64_t)p.center - p.qoff - (i0 + 31) + jfirst - 32 * (NW - 1);
+      const int64_t hi = R0 + (int64_t)(jend - jfirst + NK - 1) / NK * NK + QB + NK;
       need = (int)std::max<int64_t>(need, std::max<int64_t>(-R0, hi - p.p_rows));
     }
   return need;
 }
+
+// (the larger of both forms' needs: the form is chosen at launch)
+int bf16_pos_pad(const AttnParams& p, int nb) { return std::max(pos_pad_for<4>(p, nb), pos_pad_for<8>(p, nb)); }
 
 hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStream_t s) {
   if (nb <= 0 || p.T <= 0) return hipSuccess;

@@ -52,6 +52,20 @@ def abs_err(got, ref, mask=None) -> float:
     return float(np.max(np.abs(got - ref)))
 
 
+def bf16_abs_excess(got, ref, tol) -> tuple[float, int]:
+    """The bf16 absolute bound read on the bf16 grid: each output within
+    max(tol, one bf16 ulp of its reference value) (above |x| = 4 one ulp is
+    0.03125, so a value there either equals the reference or lies at least
+    one ulp away). Returns (max of |got - ref| / that bound, number of outputs
+    farther than tol)."""
+    got = np.asarray(got, dtype=np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    _, e = np.frexp(np.abs(ref))
+    bound = np.maximum(tol, np.ldexp(1.0, e - 8))
+    d = np.abs(got - ref)
+    return float(np.max(d / bound)), int(np.sum(d > tol))
+
+
 def random_weights(rng, d_model, n_heads, use_bias=True, scale=None, quantized=False):
     """Random layer weights (Xavier-like unless `scale`), keyed like a checkpoint."""
     import workloads as W

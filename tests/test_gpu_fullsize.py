@@ -22,7 +22,7 @@ import torch
 import relpos_oracle as O
 import relpos_mhsa as M
 import workloads as W
-from _util import abs_err, oracle_params, rel_err, row_rel_err
+from _util import abs_err, bf16_abs_excess, oracle_params, rel_err, row_rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -108,12 +108,15 @@ def test_stack_u8_layer_full_shape_zero_mean():
     xb = O.bf16_round(x)
     pos = O.bf16_round(O.RelPositionalEncoding(D, 5000, True).get_encoding(T))
     layer = gpu_layer(w, D, H, False, O.BF16)
-    # the bare forward: abs 2e-2
+    # the bare forward: abs 2e-2, or one bf16 ulp where that is larger
+    # (outputs reach |x| ~ 4, where one ulp is 0.03125)
     got = host(layer.forward(dev(xb), dev(pos), None, M.key_padding_mask(lengths, T)))
     ref = O.mhsa_forward(p, xb, pos, None, O.key_padding_mask(lengths, T), O.BF16)
     err = abs_err(got, ref)
-    print(f"u8 layer B={B} T={T}: forward max abs error {err:.3e} (max |ref| {np.max(np.abs(ref)):.3f})")
-    assert err < BF16_TOL
+    excess, n_far = bf16_abs_excess(got, ref, BF16_TOL)
+    print(f"u8 layer B={B} T={T}: forward max abs error {err:.3e} (max |ref| {np.max(np.abs(ref)):.3f}), "
+          f"{n_far} outputs beyond {BF16_TOL} (each one bf16 ulp at |x| >= 4)")
+    assert excess <= 1.0
     # the sublayer x + MHSA(LN(x)): the residual stream is ~N(0,1), where one
     # bf16 ulp is up to 0.03, so the bound is per row, 2e-2 of the row's max
     xd = dev(xb)
