@@ -434,9 +434,9 @@ __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
 //    Ring row rr holds position row R0 + rr with R0 the first row any wave
 //    needs: tile k uses rr in [NK k, NK k + QB + NK) and loads
 //    [NK k + QB + NK, NK k + QB + 2 NK) for tile k + 1.
-//  * LDS rows are unpadded; 16-byte chunk j of a K, V^T or ring row r sits
-//    at chunk j ^ (r % chunks-per-row), so the 8 lanes an LDS read serves
-//    together hit 8 distinct bank groups.
+//  * LDS rows are unpadded; 16-byte chunk j of a K or ring row r sits at
+//    chunk j ^ (r % 16), so the 16 lanes an LDS read serves together hit 16
+//    distinct bank groups; V^T rows are keyed by Cfg2::vkey.
 //  * q_u = q + pos_bias_u and q_v = q + pos_bias_v are both held in
 //    registers (bf16, as the reference adds them in the activation dtype,
 //    attention.rs:501-508): q_u for the scores, q_v for the band.
@@ -457,6 +457,12 @@ struct Cfg2 {
   static constexpr int RB = DK * 2;              // bytes per K / position row
   static constexpr int KCN = RB / 16;            // 16-byte chunks per K / position row
   static constexpr int VCN = NK * 2 / 16;        // 16-byte chunks per V^T row
+  // XOR key of V^T row d's chunks. A 16-lane group of an LDS read takes 16
+  // consecutive rows at one chunk index: with 128-byte rows (8 chunks) two
+  // rows share each 16-byte bank group, keyed by d % 8; with 64-byte rows
+  // (4 chunks) rows d, d + 4, d + 8, d + 12 share one quarter of the banks
+  // and take distinct chunks by (d / 4) % 4.
+  static __device__ __forceinline__ int vkey(int d) { return VCN == 4 ? (d >> 2) & 3 : d % VCN; }
   static constexpr int RING = QB + 2 * NK;       // position ring rows
   static constexpr int RMP = 32 * (NU + 1) + 4;  // remap row pitch (bf16 elements)
   static constexpr int KBUF = NK * RB;
@@ -579,7 +585,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 #pragma unroll
   for (int g = 0; g < C::VDMA; ++g) {
     const int pos = (w * C::VDMA + g) * 64 + lane, d = pos / C::VCN;
-    voff[g] = (int)(d * p.vt_ld * 2 + 16 * ((pos % C::VCN) ^ (d % C::VCN)));
+    voff[g] = (int)(d * p.vt_ld * 2 + 16 * ((pos % C::VCN) ^ C::vkey(d)));
   }
 #pragma unroll
   for (int g = 0; g < C::PDMA; ++g) {
@@ -858,7 +864,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
     {
       bf16x8 vo[2][DK / 32];
       auto vread = [&](int step, bf16x8* dst) {
-        const char* va = Vrow + 16 * ((2 * step + hh) ^ (c % C::VCN));  // step = 2u + jj
+        const char* va = Vrow + 16 * ((2 * step + hh) ^ C::vkey(c));  // step = 2u + jj (row 32d + c: same key)
 #pragma unroll
         for (int d = 0; d < DK / 32; ++d) dst[d] = *reinterpret_cast<const bf16x8*>(va + 32 * d * (NK * 2));
       };
