@@ -421,8 +421,7 @@ def main():
 
             def step():
                 xs.copy_(xd)
-                for layer in layers:
-                    layer.sublayer_forward_(xs, pos, ctx, kmask)
+                M.stack_sublayer_forward_(layers, xs, pos, ctx, kmask)
         else:
             out = torch.empty_like(xd)
             layer = layers[0]

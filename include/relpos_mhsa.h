@@ -223,6 +223,21 @@ int32_t mhsa_sublayer_forward(mhsa_layer* layer, void* x_inout, int32_t batch, i
                               const void* pos_emb, int32_t pos_len, const mhsa_context* ctx,
                               const int32_t* key_lengths_host, void* hip_stream);
 
+/* The offline encoder's layer loop over the MHSA sublayers
+ * (conformer.rs:542-550: one pos_emb, context and padding mask for every
+ * layer): x <- x + forward_l(LayerNorm_l(x)) for l = 0 .. n_layers - 1, with
+ * the results of n_layers mhsa_sublayer_forward calls in order, bit for bit.
+ * ln_gamma_host / ln_beta_host: HOST fp32 [n_layers, d_model] (NULL = 1 / 0),
+ * as mhsa_stack_step takes them. Every layer has the same d_model and dtype.
+ * Layer l + 1's position projection does not depend on layer l, so where the
+ * bf16 attention leaves CUs idle it runs in the same launch as layer l's
+ * attention. */
+int32_t mhsa_stack_sublayer_forward(mhsa_layer* const* layers, int32_t n_layers, void* x_inout, int32_t batch,
+                                    int32_t seq_len, const float* ln_gamma_host, const float* ln_beta_host,
+                                    float eps, const void* pos_emb,
+                                    int32_t pos_len, const mhsa_context* ctx, const int32_t* key_lengths_host,
+                                    void* hip_stream);
+
 /* ---- cache-aware streaming ---------------------------------------------- */
 
 /* Streaming state of one layer for `batch` sessions: the attention cache of

@@ -24,9 +24,12 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "quant.hpp"
 
 namespace mhsa {
 namespace {
+
+#include "gemm_tile.hpp"
 
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -488,19 +491,20 @@ __device__ __forceinline__ constexpr int swap23(int m) { return (m & ~12) | ((m 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __bf16 bf16x8_a2 __attribute__((ext_vector_type(8), aligned(2)));
 
+// The kernel's work as workgroup `block` of `nblocks` (a multiple of 8), in
+// `smem` (C::LDS bytes, 16-byte aligned).
 template <int DK, int NW, bool DEBUG>
-__global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, int nb) {
+__device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int block, int nblocks, char* smem) {
   using C = Cfg2<DK, NW>;
   constexpr int QB = C::QB, NK = C::NK, NU = C::NU, NS = C::NS, RB = C::RB;
   constexpr int PF = 3;  // MFMA steps an LDS operand read is issued ahead
-  __shared__ __attribute__((aligned(16))) char smem[C::LDS];
 
   // Work order for 8 XCDs: workgroup L runs on XCD L % 8, so each XCD gets a
   // contiguous range of (head, item, query block) work items and keeps those
-  // heads' position rows and K/V in its own L2. The grid is a multiple of 8.
+  // heads' position rows and K/V in its own L2.
   const int nqb = (p.T + QB - 1) / QB;
-  const int per = (int)gridDim.x / 8;
-  const int W = ((int)blockIdx.x % 8) * per + (int)blockIdx.x / 8;
+  const int per = nblocks / 8;
+  const int W = (int)((unsigned)block % 8u) * per + (int)((unsigned)block / 8u);
   if (W >= nqb * nb * p.H) return;
   const int tid = threadIdx.x, lane = tid & 63, hh = lane >> 5, c = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index (uniform)
@@ -917,10 +921,34 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
 }
 
 template <int DK, int NW, bool DEBUG>
-hipError_t launch2(AttnParams p, int nb, hipStream_t s) {
+__global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, int nb) {
+  __shared__ __attribute__((aligned(16))) char smem[Cfg2<DK, NW>::LDS];
+  attn_bf16_body<DK, NW, DEBUG>(p, nb, (int)blockIdx.x, (int)gridDim.x, smem);
+}
+
+// The 8-wave attention of `p` in workgroups [0, nattn) and, in the
+// workgroups after them, the tile GEMM `g`: a projection that does not
+// depend on the attention (the next layer's position rows). Workgroups are
+// dispatched in order, so the GEMM's tiles take the CUs the attention leaves
+// idle once every attention workgroup has one. Waves 4-7 of a GEMM
+// workgroup end at once (the tile body runs on 4 waves).
+template <int GBM, int GBN, bool GQ, int GNS>
+__global__ __launch_bounds__(512) void attn_bf16_gemm_kernel(const AttnParams p, int nb, int nattn, const GemmParams g) {
+  constexpr int LA = Cfg2<128, 8>::LDS, LG = TileCfg<GBM, GBN, GQ, GNS>::LDS;
+  __shared__ __attribute__((aligned(1024))) char smem[LA > LG ? LA : LG];
+  const int block = (int)blockIdx.x;
+  if (block < nattn) attn_bf16_body<128, 8, false>(p, nb, block, nattn, smem);
+  else if (threadIdx.x < 256) gemm_tile_body<GBM, GBN, GQ, GNS>(g, block - nattn, smem);
+}
+
+// Items in launch order, longest key range first, so that the work left for
+// a second round of workgroups is the shortest; returns the workgroup count
+// (a multiple of 8), or -1 when the grid would be too large.
+template <int DK, int NW>
+int64_t order_items(AttnParams& p, int nb) {
   using C = Cfg2<DK, NW>;
   const int64_t work = (int64_t)(p.T + C::QB - 1) / C::QB * p.H * nb;
-  if (work > (1 << 30)) return hipErrorInvalidValue;
+  if (work > (1 << 30)) return -1;
   // items by descending work (query blocks x key tiles), ties in item order
   int64_t cost[kMaxBatch];
   for (int bl = 0; bl < nb; ++bl) {
@@ -931,8 +959,14 @@ hipError_t launch2(AttnParams p, int nb, hipStream_t s) {
     p.order[bl] = bl;
   }
   std::stable_sort(p.order, p.order + nb, [&](int a, int b) { return cost[a] > cost[b]; });
-  const dim3 grid((unsigned)((work + 7) / 8 * 8));
-  hipLaunchKernelGGL((attn_bf16_kernel<DK, NW, DEBUG>), grid, dim3(C::NT), 0, s, p, nb);
+  return (work + 7) / 8 * 8;
+}
+
+template <int DK, int NW, bool DEBUG>
+hipError_t launch2(AttnParams p, int nb, hipStream_t s) {
+  const int64_t grid = order_items<DK, NW>(p, nb);
+  if (grid < 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((attn_bf16_kernel<DK, NW, DEBUG>), dim3((unsigned)grid), dim3(Cfg2<DK, NW>::NT), 0, s, p, nb);
   return hipGetLastError();
 }
 
@@ -1258,8 +1292,9 @@ int pos_pad_for(const AttnParams& p, int nb) {
 // (the larger of both forms' needs: the form is chosen at launch)
 int bf16_pos_pad(const AttnParams& p, int nb) { return std::max(pos_pad_for<4>(p, nb), pos_pad_for<8>(p, nb)); }
 
-hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStream_t s) {
-  if (nb <= 0 || p.T <= 0) return hipSuccess;
+namespace {
+// attention()'s argument checks for nb > 0 and T > 0.
+hipError_t check_attention(DType dt, int head_dim, const AttnParams& p, int nb) {
   if (nb > kMaxBatch || p.L <= 0 || p.H <= 0 || p.p_rows <= 0) return hipErrorInvalidValue;
   if (!p.q || !p.k || !p.v || !p.p || !p.o || !p.bias_u || !p.bias_v) return hipErrorInvalidValue;
   if (!aligned16(p.q) || !aligned16(p.k) || !aligned16(p.v) || !aligned16(p.p) || !aligned16(p.o))
@@ -1282,12 +1317,18 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
   if (p.vt) {
     // V^T columns of each batch are read in whole 64-key tiles
     if (dt != kBF16 || p.ring_len || !aligned16(p.vt) || p.vt_ld % 8 || p.vt_bs % 64 || p.vt_bs < p.T ||
-        p.vt_ld < (int64_t)(p.b0 + nb) * p.vt_bs || p.L != p.T || p.kv_pad < 63 || p.p_pad < bf16_pos_pad(p, nb))
+        p.vt_ld < (int64_t)(p.b0 + nb) * p.vt_bs || p.L != p.T || p.kv_pad < 63 || p.p_pad < bf16_pos_pad(p, nb) ||
+        (head_dim != 64 && head_dim != 128))
       return hipErrorInvalidValue;
-    if (head_dim == 64) return dispatch_bf16<64>(p, nb, s);
-    if (head_dim == 128) return dispatch_bf16<128>(p, nb, s);
-    return hipErrorInvalidValue;
   }
+  return hipSuccess;
+}
+}  // namespace
+
+hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStream_t s) {
+  if (nb <= 0 || p.T <= 0) return hipSuccess;
+  if (hipError_t e = check_attention(dt, head_dim, p, nb)) return e;
+  if (p.vt) return head_dim == 64 ? dispatch_bf16<64>(p, nb, s) : dispatch_bf16<128>(p, nb, s);
   if (dt == kF32) {
     if (p.T <= CfgS<128>::NQ && p.L <= CfgS<128>::LMAX && !p.dbg_bd) {
       const dim3 grid(p.H, nb);
@@ -1303,6 +1344,26 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
     if (head_dim == 128) return dispatch_nw<bf16, 128>(p, nb, s);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t attention_with_gemm(DType dt, int head_dim, const AttnParams& p, int nb, const GemmParams& g, bool gquant,
+                               hipStream_t s) {
+  if (nb <= 0 || p.T <= 0 || g.M <= 0) return hipErrorNotSupported;
+  if (dt != kBF16 || head_dim != 128 || !p.vt || p.dbg_bd || p.dbg_top || !use_wide<128>(p, nb))
+    return hipErrorNotSupported;
+  if (check_attention(dt, head_dim, p, nb) != hipSuccess) return hipErrorNotSupported;
+  TileForm f;
+  if (!gemm_tile_form(dt, gquant, g, f) || f.bm != 128 || f.bn != 128 || f.ns != 4) return hipErrorNotSupported;
+  AttnParams a = p;
+  const int64_t nattn = order_items<128, 8>(a, nb);
+  const int64_t tiles = m_tiles<128>(g) * (g.N / 128);
+  if (nattn < 0 || nattn + (tiles + 7) / 8 * 8 > (1 << 30)) return hipErrorNotSupported;
+  const dim3 grid((unsigned)(nattn + (tiles + 7) / 8 * 8));
+  if (gquant)
+    hipLaunchKernelGGL((attn_bf16_gemm_kernel<128, 128, true, 4>), grid, dim3(512), 0, s, a, nb, (int)nattn, g);
+  else
+    hipLaunchKernelGGL((attn_bf16_gemm_kernel<128, 128, false, 4>), grid, dim3(512), 0, s, a, nb, (int)nattn, g);
+  return hipGetLastError();
 }
 
 hipError_t export_mask(const AttnParams& p, int nb, uint8_t* out, hipStream_t s) {

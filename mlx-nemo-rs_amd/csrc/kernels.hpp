@@ -65,6 +65,14 @@ constexpr int kActSilu = 1;
 // workgroups, so M*N*splits <= kGemmPartialElems.
 constexpr int64_t kGemmPartialElems = (int64_t)1 << 22;
 hipError_t gemm(DType dt, bool quantized, const GemmParams& p, hipStream_t s);
+// gemm()'s argument checks alone (p.M > 0 assumed).
+hipError_t gemm_check(DType dt, bool quantized, const GemmParams& p);
+// The tile GEMM form (tile rows, tile columns, LDS stages) gemm() launches
+// for a valid bf16 problem; false when it takes another kernel.
+struct TileForm {
+  int bm = 0, bn = 0, ns = 0;
+};
+bool gemm_tile_form(DType dt, bool quantized, const GemmParams& p, TileForm& f);
 // Whether gemm() takes this problem with C2 / acopy set (fp32, few rows).
 bool gemm_split_fused_ok(DType dt, const GemmParams& p);
 
@@ -116,6 +124,13 @@ struct AttnParams {
   int q_valid[kMaxBatch];
 };
 hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nbatch, hipStream_t s);
+// attention() and, in the same launch, the tile GEMM `g`: a projection that
+// does not depend on the attention (nor the attention on it), whose tiles
+// take the CUs the attention leaves idle. Only for the bf16 8-wave form with
+// a GEMM of 128 x 128 tiles; otherwise hipErrorNotSupported and nothing is
+// launched (the caller launches the two apart). Same results as apart.
+hipError_t attention_with_gemm(DType dt, int head_dim, const AttnParams& p, int nbatch, const GemmParams& g,
+                               bool gquant, hipStream_t s);
 // Position rows the bf16 kernel reads beyond the table on either side for
 // these items' key ranges (key_lo / key_hi / q_valid, context, T, center).
 int bf16_pos_pad(const AttnParams& p, int nbatch);

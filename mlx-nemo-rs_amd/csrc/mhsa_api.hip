@@ -192,10 +192,11 @@ struct VtOut {
   int T = 0, Tpad = 0;
 };
 
-int32_t run_gemm(mhsa_layer* L, DType dt, const DevLinear& lin, int n_rows_w, const void* A, int64_t lda, int M,
-                 void* C, int64_t ldc, const void* R, int64_t ldr, hipStream_t s, int seg_rows = 0,
-                 int seg_stride = 0, int ring_off = 0, int ring_len = 0, const VtOut* vt = nullptr) {
-  mhsa::GemmParams p;
+// GEMM parameters of y = A W^T (+ bias) (+ R) for one of the layer's linears.
+int32_t make_gemm(mhsa_layer* L, const DevLinear& lin, int n_rows_w, const void* A, int64_t lda, int M, void* C,
+                  int64_t ldc, const void* R, int64_t ldr, mhsa::GemmParams& p, int seg_rows = 0, int seg_stride = 0,
+                  int ring_off = 0, int ring_len = 0, const VtOut* vt = nullptr) {
+  p = mhsa::GemmParams();
   p.A = A;
   p.lda = lda;
   p.W = lin.w;
@@ -226,6 +227,16 @@ int32_t run_gemm(mhsa_layer* L, DType dt, const DevLinear& lin, int n_rows_w, co
     p.vt_Tpad = vt->Tpad;
     p.seg_T = vt->T;  // per-utterance M tiles
   }
+  return MHSA_OK;
+}
+
+int32_t run_gemm(mhsa_layer* L, DType dt, const DevLinear& lin, int n_rows_w, const void* A, int64_t lda, int M,
+                 void* C, int64_t ldc, const void* R, int64_t ldr, hipStream_t s, int seg_rows = 0,
+                 int seg_stride = 0, int ring_off = 0, int ring_len = 0, const VtOut* vt = nullptr) {
+  mhsa::GemmParams p;
+  if (int32_t rc = make_gemm(L, lin, n_rows_w, A, lda, M, C, ldc, R, ldr, p, seg_rows, seg_stride, ring_off, ring_len,
+                             vt))
+    return rc;
   HIPCHK(mhsa::gemm(dt, lin.quantized, p, s));
   return MHSA_OK;
 }
@@ -356,9 +367,121 @@ struct Arena {
   size_t cap = 0;
 };
 
+// Key range and valid rows of item b of an offline call (attention.rs:281-285).
+void offline_key_bounds(const int32_t* lens, int T, int b, int& lo, int& hi, int& qv) {
+  lo = 0;
+  hi = lens ? std::min(std::max(lens[b], 1), T) : T;
+  qv = T;
+}
+
+// What an offline forward derives before its launches: the position rows it
+// projects and where its workspace puts [q|k|v], the position rows, the
+// attention output and (bf16) V^T.
+struct OfflineLayout {
+  int row0 = 0, nrows = 0, center = 0, pad = 0, kv_pad = 0;
+  int64_t M = 0;
+  bool use_vt = false;
+  char* qkv = nullptr;
+  char* P = nullptr;   // table rows [0, nrows) after `pad` slack rows
+  char* cx = nullptr;
+  VtOut vt;
+};
+
+int32_t offline_layout(mhsa_layer* L, int B, int T, int pos_len, const mhsa_context* ctx, const int32_t* lens,
+                       hipStream_t s, const Arena* arena, OfflineLayout& o) {
+  const int D = L->D;
+  const size_t es = esz(L);
+  const DistRange dr = context_distances(ctx, 0, T, T);
+  int32_t rc;
+  if ((rc = plan_positions(pos_len, T, dr, o.row0, o.nrows, o.center))) return rc;
+  o.M = (int64_t)B * T;
+  o.use_vt = L->dt == mhsa::kBF16;
+  // bf16: position rows the kernel may read on either side of the table
+  // (they only meet masked pairs) and key rows past the last item, kept as
+  // finite slack in the workspace
+  o.pad = 0;
+  o.kv_pad = o.use_vt ? 64 : 0;
+  if (o.use_vt) {
+    mhsa::AttnParams a;
+    fill_attn_common(L, a);
+    a.T = T;
+    a.L = T;
+    a.qoff = 0;
+    a.p_rows = o.nrows;
+    a.center = o.center;
+    set_ctx(a, ctx);
+    for (int b0 = 0; b0 < B; b0 += mhsa::kMaxBatch) {
+      const int nb = std::min(mhsa::kMaxBatch, B - b0);
+      for (int i = 0; i < nb; ++i) offline_key_bounds(lens, T, b0 + i, a.key_lo[i], a.key_hi[i], a.q_valid[i]);
+      o.pad = std::max(o.pad, mhsa::bf16_pos_pad(a, nb));
+    }
+  }
+  o.pad = (int)align_up(o.pad, 8);
+  const int64_t prow_n = o.nrows + 2 * (int64_t)o.pad;
+  const size_t qkv_b = align_up((o.M + o.kv_pad) * 3 * D * es, 256), p_b = align_up(prow_n * D * es, 256),
+               ctx_b = align_up(o.M * D * es, 256);
+  // bf16: V also transposed per batch, [D][B * Tpad], for the MFMA PV operand.
+  // The QKV GEMM writes every column the attention kernel reads (whole tiles
+  // of tokens: projections of the next utterance's rows, or of zero rows past
+  // the last one), so it needs no clearing.
+  size_t vt_b = 0;
+  if (o.use_vt) {
+    o.vt.T = T;
+    o.vt.Tpad = (int)align_up(T, 256);  // whole GEMM tiles of tokens per utterance
+    o.vt.ld = (int64_t)B * o.vt.Tpad;
+    vt_b = align_up((int64_t)D * o.vt.ld * 2, 256);
+  }
+  if (arena) {
+    if (qkv_b + p_b + ctx_b + vt_b > arena->cap)
+      return fail(MHSA_EINVAL, "batch %d x seq_len %d needs %zu bytes of workspace; the allocation-free forward "
+                  "has %zu", B, T, qkv_b + p_b + ctx_b + vt_b, arena->cap);
+    o.qkv = arena->base;
+    if (o.use_vt) o.vt.p = arena->base + qkv_b + p_b + ctx_b;
+    // the slack rows the bf16 kernel may read (key rows past the last item,
+    // position rows around the table) hold the previous call's values: clear them
+    if (o.kv_pad) HIPCHK(mhsa::fill_zero(o.qkv + (size_t)o.M * 3 * D * es, (size_t)o.kv_pad * 3 * D * es, s));
+    if (o.pad) {
+      HIPCHK(mhsa::fill_zero(o.qkv + qkv_b, (size_t)o.pad * D * es, s));
+      HIPCHK(mhsa::fill_zero(o.qkv + qkv_b + (size_t)(o.pad + o.nrows) * D * es, (size_t)o.pad * D * es, s));
+    }
+  } else {
+    const size_t ws_before = L->ws.n;
+    HIPCHK(L->ws.ensure(qkv_b + p_b + ctx_b));
+    if (L->ws.n != ws_before) HIPCHK(mhsa::fill_zero(L->ws.p, L->ws.n, s));  // slack rows start finite
+    o.qkv = static_cast<char*>(L->ws.p);
+    if (o.use_vt) {
+      const size_t before = L->vtbuf.n;
+      HIPCHK(L->vtbuf.ensure(vt_b));
+      if (L->vtbuf.n != before) HIPCHK(mhsa::fill_zero(L->vtbuf.p, L->vtbuf.n, s));
+      o.vt.p = L->vtbuf.p;
+    }
+  }
+  o.P = o.qkv + qkv_b + (size_t)o.pad * D * es;
+  o.cx = o.qkv + qkv_b + p_b;
+  return MHSA_OK;
+}
+
+// The position projection P = pos_emb[row0 : row0 + nrows] W_pos^T of a layout.
+int32_t pos_gemm(mhsa_layer* L, const OfflineLayout& o, const void* pos_emb, mhsa::GemmParams& g) {
+  return make_gemm(L, L->dev[4], L->D, static_cast<const char*>(pos_emb) + (size_t)o.row0 * L->D * esz(L), L->D,
+                   o.nrows, o.P, L->D, nullptr, 0, g);
+}
+
+// A projection to launch together with this call's attention (the next
+// stacked layer's position rows), or none.
+struct FusedNext {
+  mhsa::GemmParams g;
+  bool quant = false;
+  DType dt = mhsa::kBF16;
+};
+
+// With `pos_ready` the layout's position rows are already projected. With
+// `next`, that projection runs in the attention's launch where a fused form
+// exists, else right after it.
 int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos_emb, int pos_len,
                      const mhsa_context* ctx, const int32_t* lens, void* out, const void* residual,
-                     const AttnDebug& dbg, hipStream_t s, const Arena* arena = nullptr) {
+                     const AttnDebug& dbg, hipStream_t s, const Arena* arena = nullptr,
+                     const OfflineLayout* ready = nullptr, const FusedNext* next = nullptr) {
   if (B <= 0 || T <= 0) return fail(MHSA_EINVAL, "batch and seq_len must be positive (got %d, %d)", B, T);
   if (!x || !pos_emb || (!out && !dbg.any())) return fail(MHSA_EINVAL, "null tensor pointer");
   if (!aligned16(x) || !aligned16(pos_emb) || (out && !aligned16(out)))
@@ -374,126 +497,78 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   const bool prof = !arena;  // (event pairs are created on first use)
   const int D = L->D;
   const size_t es = esz(L);
-  const DistRange dr = context_distances(ctx, 0, T, T);
-  int row0, nrows, center;
-  if ((rc = plan_positions(pos_len, T, dr, row0, nrows, center))) return rc;
+  OfflineLayout o;
+  if (ready) o = *ready;
+  else if ((rc = offline_layout(L, B, T, pos_len, ctx, lens, s, arena, o))) return rc;
+  L->last_qkv = o.qkv;
+  L->last_pos = o.P;
 
-  const int64_t M = (int64_t)B * T;
-  const bool use_vt = L->dt == mhsa::kBF16;
-  auto key_bounds = [&](int b, int& lo, int& hi, int& qv) {
-    lo = 0;
-    hi = lens ? std::min(std::max(lens[b], 1), T) : T;  // attention.rs:281-285
-    qv = T;
-  };
+  {
+    LayerProf ps(L, "gemm_qkv", s, prof);
+    for (int r = prof ? L->prof.reps("gemm_qkv") : 1; r > 0; --r)
+      if ((rc = project_qkv(L, x, (int)o.M, o.qkv, 3 * D, s, o.use_vt ? &o.vt : nullptr))) return rc;
+  }
+  if (!ready) {
+    LayerProf ps(L, "gemm_pos", s, prof);
+    mhsa::GemmParams g;
+    if ((rc = pos_gemm(L, o, pos_emb, g))) return rc;
+    for (int r = prof ? L->prof.reps("gemm_pos") : 1; r > 0; --r) HIPCHK(mhsa::gemm(L->dt, L->dev[4].quantized, g, s));
+  }
+
   mhsa::AttnParams a;
   fill_attn_common(L, a);
   a.T = T;
   a.L = T;
   a.qoff = 0;
-  a.p_rows = nrows;
-  a.center = center;
+  a.p_rows = o.nrows;
+  a.center = o.center;
   set_ctx(a, ctx);
-  // bf16: position rows the kernel may read on either side of the table
-  // (they only meet masked pairs) and key rows past the last item, kept as
-  // finite slack in the workspace
-  int pad = 0;
-  const int kv_pad = use_vt ? 64 : 0;
-  if (use_vt)
-    for (int b0 = 0; b0 < B; b0 += mhsa::kMaxBatch) {
-      const int nb = std::min(mhsa::kMaxBatch, B - b0);
-      for (int i = 0; i < nb; ++i) key_bounds(b0 + i, a.key_lo[i], a.key_hi[i], a.q_valid[i]);
-      pad = std::max(pad, mhsa::bf16_pos_pad(a, nb));
-    }
-  pad = (int)align_up(pad, 8);
-  const int64_t prow_n = nrows + 2 * (int64_t)pad;
-  const size_t qkv_b = align_up((M + kv_pad) * 3 * D * es, 256), p_b = align_up(prow_n * D * es, 256),
-               ctx_b = align_up(M * D * es, 256);
-  // bf16: V also transposed per batch, [D][B * Tpad], for the MFMA PV operand.
-  // The QKV GEMM writes every column the attention kernel reads (whole tiles
-  // of tokens: projections of the next utterance's rows, or of zero rows past
-  // the last one), so it needs no clearing.
-  VtOut vt;
-  size_t vt_b = 0;
-  if (use_vt) {
-    vt.T = T;
-    vt.Tpad = (int)align_up(T, 256);  // whole GEMM tiles of tokens per utterance
-    vt.ld = (int64_t)B * vt.Tpad;
-    vt_b = align_up((int64_t)D * vt.ld * 2, 256);
-  }
-  char* qkv;
-  if (arena) {
-    if (qkv_b + p_b + ctx_b + vt_b > arena->cap)
-      return fail(MHSA_EINVAL, "batch %d x seq_len %d needs %zu bytes of workspace; the allocation-free forward "
-                  "has %zu", B, T, qkv_b + p_b + ctx_b + vt_b, arena->cap);
-    qkv = arena->base;
-    if (use_vt) vt.p = arena->base + qkv_b + p_b + ctx_b;
-    // the slack rows the bf16 kernel may read (key rows past the last item,
-    // position rows around the table) hold the previous call's values: clear them
-    if (kv_pad) HIPCHK(mhsa::fill_zero(qkv + (size_t)M * 3 * D * es, (size_t)kv_pad * 3 * D * es, s));
-    if (pad) {
-      HIPCHK(mhsa::fill_zero(qkv + qkv_b, (size_t)pad * D * es, s));
-      HIPCHK(mhsa::fill_zero(qkv + qkv_b + (size_t)(pad + nrows) * D * es, (size_t)pad * D * es, s));
-    }
-  } else {
-    const size_t ws_before = L->ws.n;
-    HIPCHK(L->ws.ensure(qkv_b + p_b + ctx_b));
-    if (L->ws.n != ws_before) HIPCHK(mhsa::fill_zero(L->ws.p, L->ws.n, s));  // slack rows start finite
-    qkv = static_cast<char*>(L->ws.p);
-    if (use_vt) {
-      const size_t before = L->vtbuf.n;
-      HIPCHK(L->vtbuf.ensure(vt_b));
-      if (L->vtbuf.n != before) HIPCHK(mhsa::fill_zero(L->vtbuf.p, L->vtbuf.n, s));
-      vt.p = L->vtbuf.p;
-    }
-  }
-  char* P = qkv + qkv_b + (size_t)pad * D * es;  // table rows [0, nrows) after `pad` slack rows
-  char* cx = qkv + qkv_b + p_b;
-  L->last_qkv = qkv;
-  L->last_pos = P;
-
-  {
-    LayerProf ps(L, "gemm_qkv", s, prof);
-    for (int r = prof ? L->prof.reps("gemm_qkv") : 1; r > 0; --r)
-      if ((rc = project_qkv(L, x, (int)M, qkv, 3 * D, s, use_vt ? &vt : nullptr))) return rc;
-  }
-  {
-    LayerProf ps(L, "gemm_pos", s, prof);
-    for (int r = prof ? L->prof.reps("gemm_pos") : 1; r > 0; --r)
-      if ((rc = run_gemm(L, L->dt, L->dev[4], D, static_cast<const char*>(pos_emb) + (size_t)row0 * D * es, D, nrows,
-                         P, D, nullptr, 0, s)))
-        return rc;
-  }
-
-  a.q = qkv;
-  a.k = qkv + (size_t)D * es;
-  a.v = qkv + (size_t)2 * D * es;
+  a.q = o.qkv;
+  a.k = o.qkv + (size_t)D * es;
+  a.v = o.qkv + (size_t)2 * D * es;
   a.q_bs = a.kv_bs = (int64_t)T * 3 * D;
   a.q_rs = a.kv_rs = 3 * D;
-  a.p = P;
+  a.p = o.P;
   a.p_rs = D;
-  a.p_pad = pad;
-  a.kv_pad = kv_pad;
-  a.o = cx;
+  a.p_pad = o.pad;
+  a.kv_pad = o.kv_pad;
+  a.o = o.cx;
   a.o_bs = (int64_t)T * D;
   a.o_rs = D;
   a.dbg_bd = dbg.bd;
   a.dbg_top = dbg.top;
   a.dbg_topv = dbg.topv;
-  if (use_vt) {
-    a.vt = vt.p;
-    a.vt_ld = vt.ld;
-    a.vt_bs = vt.Tpad;
+  if (o.use_vt) {
+    a.vt = o.vt.p;
+    a.vt_ld = o.vt.ld;
+    a.vt_bs = o.vt.Tpad;
   }
+  auto key_bounds = [&](int b, int& lo, int& hi, int& qv) { offline_key_bounds(lens, T, b, lo, hi, qv); };
   {
     LayerProf ps(L, "attention", s, prof);
-    for (int r = prof ? L->prof.reps("attention") : 1; r > 0 && !rc; --r)
-      rc = run_attention(L, L->dt, a, B, key_bounds, s);
+    for (int r = prof ? L->prof.reps("attention") : 1; r > 0 && !rc; --r) {
+      bool fused = false;
+      if (next && B <= mhsa::kMaxBatch) {
+        mhsa::AttnParams af = a;
+        af.b0 = 0;
+        for (int i = 0; i < B; ++i) key_bounds(i, af.key_lo[i], af.key_hi[i], af.q_valid[i]);
+        const hipError_t e = mhsa::attention_with_gemm(L->dt, L->dk, af, B, next->g, next->quant, s);
+        if (e != hipErrorNotSupported) {
+          HIPCHK(e);
+          fused = true;
+        }
+      }
+      if (!fused) {
+        rc = run_attention(L, L->dt, a, B, key_bounds, s);
+        if (!rc && next) HIPCHK(mhsa::gemm(next->dt, next->quant, next->g, s));
+      }
+    }
   }
   if (rc) return rc;
   if (!out) return MHSA_OK;
   LayerProf ps(L, "gemm_out", s, prof);
   for (int r = prof ? L->prof.reps("gemm_out") : 1; r > 0 && !rc; --r)
-    rc = run_gemm(L, L->dt, L->dev[3], D, cx, D, (int)M, out, D, residual, D, s);
+    rc = run_gemm(L, L->dt, L->dev[3], D, o.cx, D, (int)o.M, out, D, residual, D, s);
   return rc;
 }
 
@@ -587,6 +662,36 @@ int32_t prepare_stream(mhsa_layer* L) {
     }
   }
   L->stream_version = L->version;
+  return MHSA_OK;
+}
+
+// The sublayer's LayerNorm: its affine parameters on the device, uploaded
+// when they change (rounded like the reference's cast of the norm to the
+// layer dtype), and the output buffer for `rows` rows.
+int32_t sublayer_norm(mhsa_layer* L, const float* gamma, const float* beta, int64_t rows, const float** gd,
+                      const float** bd) {
+  const int D = L->D;
+  if (D > mhsa::kMaxLayerNormDim)
+    return fail(MHSA_ENOTSUP, "the sublayer's LayerNorm supports d_model <= %d (got %d)", mhsa::kMaxLayerNormDim, D);
+  *gd = *bd = nullptr;
+  if (gamma || beta) {
+    std::vector<float> tmp(2 * D);
+    const bool bf = L->dt == mhsa::kBF16;
+    for (int i = 0; i < D; ++i) {
+      const float gv = gamma ? gamma[i] : 1.f, bv = beta ? beta[i] : 0.f;
+      tmp[i] = bf ? round_bf16(gv) : gv;
+      tmp[D + i] = bf ? round_bf16(bv) : bv;
+    }
+    if (tmp != L->ln_host) {
+      if (L->ln_dev.p) HIPCHK(hipDeviceSynchronize());  // earlier LayerNorm launches may still read them
+      HIPCHK(L->ln_dev.ensure(tmp.size() * 4));
+      HIPCHK(hipMemcpy(L->ln_dev.p, tmp.data(), tmp.size() * 4, hipMemcpyHostToDevice));
+      L->ln_host = tmp;
+    }
+    *gd = static_cast<const float*>(L->ln_dev.p);
+    *bd = *gd + D;
+  }
+  HIPCHK(L->hbuf.ensure(align_up(rows * D * esz(L), 256)));
   return MHSA_OK;
 }
 
@@ -807,39 +912,72 @@ int32_t mhsa_sublayer_forward(mhsa_layer* L, void* x, int32_t batch, int32_t seq
   if (int32_t rc = check_layer(L)) return rc;
   if (!x || batch <= 0 || seq_len <= 0) return fail(MHSA_EINVAL, "bad sublayer arguments");
   if (!aligned16(x)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
-  if (L->D > mhsa::kMaxLayerNormDim)
-    return fail(MHSA_ENOTSUP, "the sublayer's LayerNorm supports d_model <= %d (got %d)", mhsa::kMaxLayerNormDim, L->D);
   hipStream_t s = static_cast<hipStream_t>(hs);
-  const int D = L->D;
-  const int64_t M = (int64_t)batch * seq_len;
-  // LayerNorm affine parameters, uploaded when they change (rounded like the
-  // reference's cast of the norm to the layer dtype)
   const float* gd = nullptr;
   const float* bd = nullptr;
-  if (gamma || beta) {
-    std::vector<float> tmp(2 * D);
-    const bool bf = L->dt == mhsa::kBF16;
-    for (int i = 0; i < D; ++i) {
-      const float gv = gamma ? gamma[i] : 1.f, bv = beta ? beta[i] : 0.f;
-      tmp[i] = bf ? round_bf16(gv) : gv;
-      tmp[D + i] = bf ? round_bf16(bv) : bv;
-    }
-    if (tmp != L->ln_host) {
-      if (L->ln_dev.p) HIPCHK(hipDeviceSynchronize());  // earlier LayerNorm launches may still read them
-      HIPCHK(L->ln_dev.ensure(tmp.size() * 4));
-      HIPCHK(hipMemcpy(L->ln_dev.p, tmp.data(), tmp.size() * 4, hipMemcpyHostToDevice));
-      L->ln_host = tmp;
-    }
-    gd = static_cast<const float*>(L->ln_dev.p);
-    bd = gd + D;
-  }
-  HIPCHK(L->hbuf.ensure(align_up(M * D * esz(L), 256)));
+  if (int32_t rc = sublayer_norm(L, gamma, beta, (int64_t)batch * seq_len, &gd, &bd)) return rc;
   {
     LayerProf ps(L, "layer_norm", s);
     for (int r = L->prof.reps("layer_norm"); r > 0; --r)
-      HIPCHK(mhsa::layer_norm(dtype_of(L), x, L->hbuf.p, gd, bd, eps, (int)M, D, s));
+      HIPCHK(mhsa::layer_norm(dtype_of(L), x, L->hbuf.p, gd, bd, eps, (int)((int64_t)batch * seq_len), L->D, s));
   }
   return forward_impl(L, L->hbuf.p, batch, seq_len, pos_emb, pos_len, ctx, lens, x, x, AttnDebug(), s);
+}
+
+int32_t mhsa_stack_sublayer_forward(mhsa_layer* const* layers, int32_t n_layers, void* x, int32_t batch,
+                                    int32_t seq_len, const float* gammas, const float* betas, float eps,
+                                    const void* pos_emb, int32_t pos_len, const mhsa_context* ctx,
+                                    const int32_t* lens, void* hs) {
+  if (!layers || n_layers <= 0) return fail(MHSA_EINVAL, "the stack needs at least one layer");
+  for (int l = 0; l < n_layers; ++l) {
+    if (int32_t rc = check_layer(layers[l])) return rc;
+    if (layers[l]->D != layers[0]->D || layers[l]->dt != layers[0]->dt)
+      return fail(MHSA_EINVAL, "layer %d has d_model %d / dtype %d, layer 0 has %d / %d", l, layers[l]->D,
+                  (int)layers[l]->dt, layers[0]->D, (int)layers[0]->dt);
+  }
+  if (!x || batch <= 0 || seq_len <= 0) return fail(MHSA_EINVAL, "bad sublayer arguments");
+  if (!pos_emb) return fail(MHSA_EINVAL, "null tensor pointer");
+  if (!aligned16(x) || !aligned16(pos_emb)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  const int64_t M = (int64_t)batch * seq_len;
+  // every layer's parameters, norm and workspace before the first launch:
+  // layer l + 1's position rows are projected while layer l runs
+  std::vector<OfflineLayout> lay(n_layers);
+  std::vector<const float*> gd(n_layers), bd(n_layers);
+  for (int l = 0; l < n_layers; ++l) {
+    mhsa_layer* L = layers[l];
+    if (int32_t rc = prepare(L)) return rc;
+    const size_t off = (size_t)l * L->D;
+    if (int32_t rc = sublayer_norm(L, gammas ? gammas + off : nullptr, betas ? betas + off : nullptr, M, &gd[l], &bd[l]))
+      return rc;
+    if (int32_t rc = offline_layout(L, batch, seq_len, pos_len, ctx, lens, s, nullptr, lay[l])) return rc;
+  }
+  {
+    mhsa_layer* L = layers[0];
+    LayerProf ps(L, "gemm_pos", s);
+    mhsa::GemmParams g;
+    if (int32_t rc = pos_gemm(L, lay[0], pos_emb, g)) return rc;
+    for (int r = L->prof.reps("gemm_pos"); r > 0; --r) HIPCHK(mhsa::gemm(L->dt, L->dev[4].quantized, g, s));
+  }
+  for (int l = 0; l < n_layers; ++l) {
+    mhsa_layer* L = layers[l];
+    {
+      LayerProf ps(L, "layer_norm", s);
+      for (int r = L->prof.reps("layer_norm"); r > 0; --r)
+        HIPCHK(mhsa::layer_norm(dtype_of(L), x, L->hbuf.p, gd[l], bd[l], eps, (int)M, L->D, s));
+    }
+    FusedNext nx;
+    if (l + 1 < n_layers) {
+      mhsa_layer* N = layers[l + 1];
+      if (int32_t rc = pos_gemm(N, lay[l + 1], pos_emb, nx.g)) return rc;
+      nx.quant = N->dev[4].quantized;
+      nx.dt = N->dt;
+    }
+    if (int32_t rc = forward_impl(L, L->hbuf.p, batch, seq_len, pos_emb, pos_len, ctx, lens, x, x, AttnDebug(), s,
+                                  nullptr, &lay[l], l + 1 < n_layers ? &nx : nullptr))
+      return rc;
+  }
+  return MHSA_OK;
 }
 
 int32_t mhsa_stream_create(mhsa_layer* L, int32_t batch, int32_t cache_size, int32_t chunk_len, mhsa_stream** out) {

@@ -35,7 +35,7 @@ EXPORTS = (
     "mhsa_load_linear_quantized", "mhsa_load_pos_bias", "mhsa_load_weights", "mhsa_checkpoint_open",
     "mhsa_checkpoint_close", "mhsa_checkpoint_quantization", "mhsa_checkpoint_count", "mhsa_checkpoint_tensor",
     "mhsa_checkpoint_metadata", "mhsa_load_weights_from_checkpoint", "mhsa_forward", "mhsa_forward_noalloc",
-    "mhsa_sublayer_forward", "mhsa_stream_create", "mhsa_stream_destroy", "mhsa_stream_load_cache",
+    "mhsa_sublayer_forward", "mhsa_stack_sublayer_forward", "mhsa_stream_create", "mhsa_stream_destroy", "mhsa_stream_load_cache",
     "mhsa_stream_read_cache", "mhsa_stream_fill", "mhsa_forward_with_cache", "mhsa_forward_uncached",
     "mhsa_stack_create", "mhsa_stack_destroy", "mhsa_stack_load_cache", "mhsa_stack_read_cache", "mhsa_stack_fill",
     "mhsa_stack_step", "mhsa_ffn_create", "mhsa_ffn_destroy", "mhsa_ffn_set_dtype", "mhsa_ffn_load_weights",
@@ -114,6 +114,8 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_forward_noalloc": (I, [VP, VP, I, I, VP, I, P(Context), PI, VP, VP]),
         "mhsa_sublayer_forward": (I, [VP, VP, I, I, P(ctypes.c_float), P(ctypes.c_float), F, VP, I, P(Context), PI,
                                       VP]),
+        "mhsa_stack_sublayer_forward": (I, [P(VP), I, VP, I, I, P(ctypes.c_float), P(ctypes.c_float), F, VP, I,
+                                            P(Context), PI, VP]),
         "mhsa_stream_create": (I, [VP, I, I, I, P(VP)]),
         "mhsa_stream_destroy": (None, [VP]),
         "mhsa_stream_load_cache": (I, [VP, VP, PI, VP]),
@@ -843,6 +845,31 @@ class StreamState:
                                                        ctypes.byref(m) if m is not None else None, _dptr(out),
                                                        _stream_ptr()))
         return out
+
+
+def stack_sublayer_forward_(layers: Sequence["RelPositionMultiHeadAttention"], x, pos_emb, context=None,
+                            key_mask=None, gamma=None, beta=None, eps=1e-5):
+    """The offline encoder's layer loop over the attention sublayers
+    (conformer.rs:542-550): in place x <- x + MHSA_l(LN_l(x)) for every layer,
+    with the results of calling `sublayer_forward_` layer by layer;
+    gamma/beta [layers, d_model] (None = 1 / 0)."""
+    layers = list(layers)
+    if not layers:
+        raise MhsaError(MHSA_EINVAL, "the stack needs at least one layer")
+    b, t, d = x.shape
+    pe = pos_emb.reshape(-1, d)
+    layers[0]._check_dev(x, pe)
+    ctx = context.c() if context is not None else None
+    g = None if gamma is None else _host_f32(gamma)
+    bb = None if beta is None else _host_f32(beta)
+    fp = ctypes.POINTER(ctypes.c_float)
+    arr = (ctypes.c_void_p * len(layers))(*[l._h.value for l in layers])
+    lib = layers[0]._lib
+    _check(lib.mhsa_stack_sublayer_forward(
+        arr, len(layers), _dptr(x), b, t, None if g is None else g.ctypes.data_as(fp),
+        None if bb is None else bb.ctypes.data_as(fp), float(eps), _dptr(pe), pe.shape[0],
+        ctypes.byref(ctx) if ctx is not None else None, _int_array(key_mask), _stream_ptr()))
+    return x
 
 
 class StreamingStack:

@@ -56,6 +56,21 @@ def test_layer_accessors_and_dtype(lib):
     assert layer.cache_drop_size == 3
 
 
+def test_stack_sublayer_forward_argument_checks(lib):
+    """The offline stack rejects an empty layer list and layers of different
+    d_model before touching any tensor."""
+    a = M.RelPositionMultiHeadAttention(512, 8, False)
+    b = M.RelPositionMultiHeadAttention(1024, 8, False)
+    arr = (ctypes.c_void_p * 2)(a._h.value, b._h.value)
+    assert lib.mhsa_stack_sublayer_forward(arr, 0, None, 1, 1, None, None, 1e-5, None, 1, None, None, None) == \
+        M.MHSA_EINVAL
+    assert lib.mhsa_stack_sublayer_forward(arr, 2, None, 1, 1, None, None, 1e-5, None, 1, None, None, None) == \
+        M.MHSA_EINVAL
+    assert b"layer 1 has d_model 1024" in lib.mhsa_last_error()
+    with pytest.raises(M.MhsaError):
+        M.stack_sublayer_forward_([], np.zeros((1, 1, 512), np.float32), np.zeros((1, 512), np.float32))
+
+
 def test_load_weights_strict_and_lenient():
     rng = np.random.default_rng(0)
     w = W.make_layer_weights(rng, 128, 2, True, False)

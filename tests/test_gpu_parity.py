@@ -948,6 +948,42 @@ def test_stack_u8_well_conditioned_against_oracle():
     assert err < 2e-2
 
 
+@pytest.mark.parametrize("kind", ["u8_8wave_fused", "bf16_4wave", "f32"])
+def test_stack_sublayer_forward_equals_layer_loop(kind):
+    """mhsa_stack_sublayer_forward gives the results of mhsa_sublayer_forward
+    called layer by layer, bit for bit: at the quantized stack's shape (B=4,
+    T=1500, key padding: each next layer's position projection runs in the
+    same launch as the attention), on a bf16 shape of the 4-wave form and in
+    fp32 (projections run apart), with per-layer LayerNorm parameters."""
+    if kind == "u8_8wave_fused":
+        cfg = W.CONFIGS["xl_stack_u8"]
+        D, H, T, B, n = cfg.d_model, cfg.n_heads, cfg.seq_len, cfg.batch, 3
+        rng = np.random.default_rng(47)
+        wts = [W.make_layer_weights(rng, D, H, False, True) for _ in range(n)]
+        lengths = [int(v) for v in rng.integers(1000, T + 1, size=B)]
+        dtype = O.BF16
+    else:
+        D, H, T, B, n = 256, 2, 300, 3, 3
+        rng = np.random.default_rng(48)
+        wts = [W.make_layer_weights(rng, D, H, True, False) for _ in range(n)]
+        lengths = [300, 211, 97]
+        dtype = O.BF16 if kind == "bf16_4wave" else O.F32
+    layers = [gpu_layer(w, D, H, kind != "u8_8wave_fused", dtype) for w in wts]
+    gamma = 1.0 + 0.1 * rng.standard_normal((n, D))
+    beta = 0.1 * rng.standard_normal((n, D))
+    x = rng.standard_normal((B, T, D))
+    pos = O.RelPositionalEncoding(D, 5000, True).get_encoding(T)
+    kmask = M.key_padding_mask(lengths, T)
+    xa, pd = dev(x, dtype), dev(pos, dtype)
+    xb = xa.clone()
+    for i, layer in enumerate(layers):
+        layer.sublayer_forward_(xa, pd, None, kmask, gamma[i], beta[i])
+    M.stack_sublayer_forward_(layers, xb, pd, None, kmask, gamma, beta)
+    torch.cuda.synchronize()
+    assert torch.isfinite(xb.float()).all()
+    assert torch.equal(xa, xb), f"{kind}: max difference {float((xa.float() - xb.float()).abs().max()):.3g}"
+
+
 def test_stack_u8_full_size_deterministic():
     cfg = W.CONFIGS["xl_stack_u8"]
     layers, x, ex = W.instantiate(cfg)
