@@ -906,8 +906,14 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
       p.dbg_topv[r] = top_v;
     }
   }
-  if (qi < p.T) {
-    bf16* orow = reinterpret_cast<bf16*>(p.o) + (int64_t)b * p.o_bs + (int64_t)qi * p.o_rs + h * DK;
+  // The output goes through LDS: the accumulators hold one query per lane
+  // (32 rows under a wave), the stores then write whole 16-byte runs of
+  // each row. The position ring is free: the loop's last barrier is behind
+  // every wave's last read of it.
+  {
+    constexpr int OP = DK * 2 + 16;  // staged row pitch (bytes)
+    static_assert(C::NT / 64 * 32 * OP <= C::RING * RB, "output staging fits the ring");
+    char* stg = smem + C::P_OFF + w * 32 * OP;
 #pragma unroll
     for (int d = 0; d < DK / 32; ++d)
 #pragma unroll
@@ -915,8 +921,19 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
         bf16x4 v4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) v4[e] = (bf16)(o[d][4 * a + e] * inv);
-        *reinterpret_cast<bf16x4*>(orow + 32 * d + 8 * a + 4 * hh) = v4;
+        *reinterpret_cast<bf16x4*>(stg + c * OP + (32 * d + 8 * a + 4 * hh) * 2) = v4;
       }
+    asm volatile("" ::: "memory");  // (LDS serves one wave's accesses in order)
+    constexpr int CPR = DK * 2 / 16, RPI = 64 / CPR;  // 16-byte chunks per row, rows per instruction
+    const int ch = lane % CPR;
+#pragma unroll
+    for (int i = 0; i < 32 / RPI; ++i) {
+      const int r = lane / CPR + RPI * i, q = iw + r;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(stg + r * OP + ch * 16);
+      if (q < p.T)
+        *reinterpret_cast<u32x4*>(reinterpret_cast<bf16*>(p.o) + (int64_t)b * p.o_bs + (int64_t)q * p.o_rs + h * DK +
+                                  ch * 8) = v;
+    }
   }
 }
 
