@@ -105,6 +105,9 @@ def kernel_work(cfg, tag, lengths, fills_seq):
         return None
     if tag == "gemm_qkv":
         return (2.0 * B * T * 3 * D * D, "TFLOP/s", "mfma")
+    if tag == "gemm_qkv_pos":  # the Q/K/V and position projections in one launch
+        rows = cfg.pos_band or (2 * T - 1)
+        return (2.0 * (B * T * 3 + rows) * D * D, "TFLOP/s", "mfma")
     if tag == "gemm_out":
         return (2.0 * B * T * D * D, "TFLOP/s", "mfma")
     if tag == "gemm_pos":

@@ -24,6 +24,7 @@
 // With seg_T > 0 the M tiles are laid out per utterance (rows b*seg_T ..
 // (b+1)*seg_T, never straddling two), so the V projection can be written
 // transposed ([D][B*Tpad], tokens contiguous) with 16-byte stores.
+#include <atomic>
 #include <type_traits>
 
 #include "common.hpp"
@@ -309,6 +310,19 @@ template <int BM, int BN, bool QUANT, int NS>
 __global__ __launch_bounds__(256, 1) void gemm_tile_kernel(const GemmParams p) {
   __shared__ __attribute__((aligned(1024))) char smem[TileCfg<BM, BN, QUANT, NS>::LDS];
   gemm_tile_body<BM, BN, QUANT, NS>(p, (int)blockIdx.x, smem);
+}
+
+// Two independent tile GEMMs in one launch: p1's tiles in workgroups [0, n1)
+// (n1 a multiple of 8), p2's in the workgroups after them. Workgroups are
+// dispatched in index order, so p2's tiles take the CUs p1's tiles free as
+// they end, instead of waiting for p1's last tile.
+template <int BM1, int BN1, int NS1, int BM2, int BN2, int NS2, bool QUANT>
+__global__ __launch_bounds__(256, 1) void gemm_pair_kernel(const GemmParams p1, int n1, const GemmParams p2) {
+  constexpr int L1 = TileCfg<BM1, BN1, QUANT, NS1>::LDS, L2 = TileCfg<BM2, BN2, QUANT, NS2>::LDS;
+  __shared__ __attribute__((aligned(1024))) char smem[L1 > L2 ? L1 : L2];
+  const int block = (int)blockIdx.x;
+  if (block < n1) gemm_tile_body<BM1, BN1, QUANT, NS1>(p1, block, smem);
+  else gemm_tile_body<BM2, BN2, QUANT, NS2>(p2, block - n1, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -628,14 +642,7 @@ int kpar_tile_rows(const GemmParams& p) {
 // Workgroups of the K-parallel kernel: as many tiles each as the tiles over
 // the CUs need, spread so that no workgroup has more.
 int kpar_grid(const GemmParams& p, int tr) {
-  static int cus = 0;
-  if (!cus) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
-                                                  hipSuccess || n <= 0)
-      n = 256;
-    cus = n;
-  }
+  const int cus = device_cus();
   const int ts = 16 * tr;
   const int T = (p.M + ts - 1) / ts * (p.N / ts);
   const int per = (T + cus - 1) / cus;
@@ -834,6 +841,59 @@ hipError_t gemm_check(DType dt, bool quantized, const GemmParams& p) {
 
 bool gemm_tile_form(DType dt, bool quantized, const GemmParams& p, TileForm& f) {
   return dt == kBF16 && p.M > 0 && !p.C2 && !p.acopy && gemm_check(dt, quantized, p) == hipSuccess && tile_form(p, f);
+}
+
+namespace {
+template <int BM1, int BN1, int NS1, bool QUANT>
+hipError_t launch_pair(const GemmParams& p1, const GemmParams& p2, hipStream_t s) {
+  const int64_t n1 = (m_tiles<BM1>(p1) * (p1.N / BN1) + 7) / 8 * 8, n2 = (m_tiles<64>(p2) * (p2.N / 64) + 7) / 8 * 8;
+  hipLaunchKernelGGL((gemm_pair_kernel<BM1, BN1, NS1, 64, 64, 4, QUANT>), dim3((unsigned)(n1 + n2)), dim3(256), 0, s,
+                     p1, (int)n1, p2);
+  return hipGetLastError();
+}
+
+template <bool QUANT>
+hipError_t dispatch_pair(const TileForm& f, const GemmParams& p1, const GemmParams& p2, hipStream_t s) {
+  if (f.bm == 256) return launch_pair<256, 256, 2, QUANT>(p1, p2, s);
+  if (f.bm == 192 && f.bn == 192) return launch_pair<192, 192, 3, QUANT>(p1, p2, s);
+  if (f.bm == 192) return launch_pair<192, 128, 3, QUANT>(p1, p2, s);
+  if (f.ns == 4) return launch_pair<128, 128, 4, QUANT>(p1, p2, s);
+  return launch_pair<128, 128, 2, QUANT>(p1, p2, s);
+}
+}  // namespace
+
+int device_cus() {
+  constexpr int kDevices = 64;
+  static std::atomic<int> cached[kDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev >= 0 && dev < kDevices)
+    if (const int n = cached[dev].load(std::memory_order_relaxed)) return n;
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  if (dev >= 0 && dev < kDevices) cached[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// Paired where p1's tiles take one round of CUs: the CUs its slowest tiles
+// leave idle then run p2's tiles (measured: 3000 x 3072 Q/K/V tiles with
+// 749 x 1024 position tiles, step 0.064 -> 0.061 ms). Past one round it
+// measured no gain (15000 x 3072 with 257 rows: step 0.2174 against
+// 0.2202 ms).
+bool gemm_pair_ok(DType dt, bool quantized, const GemmParams& p1, const GemmParams& p2) {
+  TileForm f1, f2;
+  return p1.M > 0 && p2.M > 0 && gemm_tile_form(dt, quantized, p1, f1) && f1.bm != 64 &&
+         gemm_tile_form(dt, quantized, p2, f2) && f2.bm == 64 &&
+         (p1.seg_T > 0 ? (int64_t)(p1.M / p1.seg_T) * ((p1.seg_T + f1.bm - 1) / f1.bm) : (p1.M + f1.bm - 1) / f1.bm) *
+                 (p1.N / f1.bn) <=
+             device_cus();
+}
+
+hipError_t gemm_pair(DType dt, bool quantized, const GemmParams& p1, const GemmParams& p2, hipStream_t s) {
+  if (!gemm_pair_ok(dt, quantized, p1, p2)) return hipErrorInvalidValue;
+  TileForm f;
+  tile_form(p1, f);
+  return quantized ? dispatch_pair<true>(f, p1, p2, s) : dispatch_pair<false>(f, p1, p2, s);
 }
 
 hipError_t gemm(DType dt, bool quantized, const GemmParams& p, hipStream_t s) {

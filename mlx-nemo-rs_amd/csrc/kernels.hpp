@@ -73,8 +73,18 @@ struct TileForm {
   int bm = 0, bn = 0, ns = 0;
 };
 bool gemm_tile_form(DType dt, bool quantized, const GemmParams& p, TileForm& f);
+// Two independent GEMMs of one dtype and weight form in one launch: p2's
+// tiles take the CUs p1's tiles free as they end. For a p1 that gemm() runs
+// in one round of tiles of a form larger than 64x64 and a p2 it runs in the
+// 64x64 form (gemm_pair_ok); the same results as gemm() on each. Otherwise
+// hipErrorInvalidValue and nothing is launched.
+bool gemm_pair_ok(DType dt, bool quantized, const GemmParams& p1, const GemmParams& p2);
+hipError_t gemm_pair(DType dt, bool quantized, const GemmParams& p1, const GemmParams& p2, hipStream_t s);
 // Whether gemm() takes this problem with C2 / acopy set (fp32, few rows).
 bool gemm_split_fused_ok(DType dt, const GemmParams& p);
+// Compute units of the current device (256 if the query fails), read once
+// per device.
+int device_cus();
 
 constexpr int kMaxBatch = 64;
 

@@ -503,16 +503,40 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   L->last_qkv = o.qkv;
   L->last_pos = o.P;
 
-  {
-    LayerProf ps(L, "gemm_qkv", s, prof);
-    for (int r = prof ? L->prof.reps("gemm_qkv") : 1; r > 0; --r)
-      if ((rc = project_qkv(L, x, (int)o.M, o.qkv, 3 * D, s, o.use_vt ? &o.vt : nullptr))) return rc;
+  // The Q/K/V and position projections in one launch where both take tile
+  // forms that pair (the position tiles take the CUs the Q/K/V tiles free as
+  // they end), else one after the other.
+  mhsa::GemmParams gq, gp;
+  bool paired = false;
+  if (!ready && L->qkv_fused && L->dev[0].quantized == L->dev[4].quantized) {
+    VtOut v;
+    if (o.use_vt) {
+      v = o.vt;
+      v.col0 = 2 * D;
+    }
+    if ((rc = make_gemm(L, L->dev[0], 3 * D, x, D, (int)o.M, o.qkv, 3 * D, nullptr, 0, gq, 0, 0, 0, 0,
+                        o.use_vt ? &v : nullptr)) ||
+        (rc = pos_gemm(L, o, pos_emb, gp)))
+      return rc;
+    paired = mhsa::gemm_pair_ok(L->dt, L->dev[0].quantized, gq, gp);
   }
-  if (!ready) {
-    LayerProf ps(L, "gemm_pos", s, prof);
-    mhsa::GemmParams g;
-    if ((rc = pos_gemm(L, o, pos_emb, g))) return rc;
-    for (int r = prof ? L->prof.reps("gemm_pos") : 1; r > 0; --r) HIPCHK(mhsa::gemm(L->dt, L->dev[4].quantized, g, s));
+  if (paired) {
+    LayerProf ps(L, "gemm_qkv_pos", s, prof);
+    for (int r = prof ? L->prof.reps("gemm_qkv_pos") : 1; r > 0; --r)
+      HIPCHK(mhsa::gemm_pair(L->dt, L->dev[0].quantized, gq, gp, s));
+  } else {
+    {
+      LayerProf ps(L, "gemm_qkv", s, prof);
+      for (int r = prof ? L->prof.reps("gemm_qkv") : 1; r > 0; --r)
+        if ((rc = project_qkv(L, x, (int)o.M, o.qkv, 3 * D, s, o.use_vt ? &o.vt : nullptr))) return rc;
+    }
+    if (!ready) {
+      LayerProf ps(L, "gemm_pos", s, prof);
+      mhsa::GemmParams g;
+      if ((rc = pos_gemm(L, o, pos_emb, g))) return rc;
+      for (int r = prof ? L->prof.reps("gemm_pos") : 1; r > 0; --r)
+        HIPCHK(mhsa::gemm(L->dt, L->dev[4].quantized, g, s));
+    }
   }
 
   mhsa::AttnParams a;

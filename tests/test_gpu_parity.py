@@ -189,6 +189,33 @@ def test_position_scores_bf16_match_rel_shift(d_model, n_heads, B, T):
                            f"at {np.argwhere(bad)[:3].tolist()}")
 
 
+@pytest.mark.parametrize("quantized", [False, True])
+def test_paired_projections_equal_separate_launches(quantized):
+    """At the xl_offline_bf16 shape (D=1024, B=8, T=375) the forward runs the
+    fused Q/K/V projection (3000 x 3072, 192x192 tiles) and the position
+    projection (749 rows, 64x64 tiles) in one launch, the position tiles
+    after the Q/K/V tiles. The q rows and position rows it leaves equal those
+    of the q and position linears run alone (`mhsa_debug_linear`, separate
+    launches and, for q, another tile form), bit for bit: every tile form
+    sums a dot product in the same 32x32x16 MFMA steps along K. For dense and
+    affine-u8 weights."""
+    cfg = W.CONFIGS["xl_offline_bf16"]
+    D, H, T, B = cfg.d_model, cfg.n_heads, cfg.seq_len, cfg.batch
+    rng = np.random.default_rng(61)
+    w = W.make_layer_weights(rng, D, H, not quantized, quantized)
+    layer = gpu_layer(w, D, H, not quantized, O.BF16)
+    xd = dev(rng.standard_normal((B, T, D)), O.BF16)
+    pd = dev(O.RelPositionalEncoding(D, 5000, True).get_encoding(T), O.BF16)
+    _, qd, Pd = layer.debug_position_scores(xd, pd, with_inputs=True)
+    q_alone = layer.debug_linear("linear_q", xd)
+    P_alone = layer.debug_linear("linear_pos", pd)
+    torch.cuda.synchronize()
+    assert torch.isfinite(qd.float()).all() and torch.isfinite(Pd.float()).all()
+    assert torch.equal(Pd.reshape(P_alone.shape), P_alone), \
+        f"position rows differ by up to {float((Pd.float() - P_alone.float()).abs().max()):.3g}"
+    assert torch.equal(qd, q_alone), f"q rows differ by up to {float((qd.float() - q_alone.float()).abs().max()):.3g}"
+
+
 # ---------------------------------------------------------------------------
 # offline forward
 # ---------------------------------------------------------------------------
