@@ -439,8 +439,10 @@ int32_t mhsa_pos_encoding(int32_t d_model, int32_t max_len, int32_t seq_len, flo
 /* No counterpart in the reference (it times whole calls with wall clocks,
  * examples/eval.rs:181-183, 289-295). When enabled, every kernel the layer
  * launches is bracketed by HIP events on the launch stream; totals accumulate
- * per kernel tag (gemm_qkv, gemm_pos, attention, gemm_out, layer_norm,
- * gemm_q, gemm_kv, ring_write). Reading waits for the recorded events. */
+ * per kernel tag (gemm_qkv, gemm_pos, gemm_qkv_pos where the offline Q/K/V
+ * and position projections run in one launch, attention, gemm_out,
+ * layer_norm, gemm_q, gemm_kv, ring_write). Reading waits for the recorded
+ * events. */
 int32_t mhsa_profile_enable(mhsa_layer* layer, int32_t enable);
 /* While profiling is enabled, issue every launch tagged `tag` n times inside
  * its event pair (it then counts as n launches), so the event overhead is
