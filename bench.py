@@ -151,7 +151,7 @@ def cpu_baseline(cfg, layers_w, x, ex, budget_s):
     bf = cfg.dtype == "bfloat16"
     D, T, B, H = cfg.d_model, cfg.seq_len, cfg.batch, cfg.n_heads
     dk = D // H
-    scale_bd = float(O.bf16_round(np.float32(O.f32_scale(dk)))[()]) if bf else None
+    scale_bd = float(np.asarray(O.bf16_round(np.float32(O.f32_scale(dk)))).reshape(-1)[0]) if bf else None
     rnd = (lambda a: O.bf16_round(a).astype(np.float32)) if bf else (lambda a: np.asarray(a, np.float32))
     ctx = None if cfg.context is None else (cfg.context[0], cfg.context[1], cfg.context[2] == "chunked_limited")
     # streaming layers run in f32 activations for either layer dtype
