@@ -493,7 +493,7 @@ typedef __bf16 bf16x8_a2 __attribute__((ext_vector_type(8), aligned(2)));
 
 // The kernel's work as workgroup `block` of `nblocks` (a multiple of 8), in
 // `smem` (C::LDS bytes, 16-byte aligned).
-template <int DK, int NW, bool DEBUG>
+template <int DK, int NW, bool DEBUG, bool SKIP = false>
 __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int block, int nblocks, char* smem) {
   using C = Cfg2<DK, NW>;
   constexpr int QB = C::QB, NK = C::NK, NU = C::NU, NS = C::NS, RB = C::RB;
@@ -696,6 +696,7 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
   if (jfirst < jend) carry = pack(band_tile(rrw));
 
   int buf = 0;
+  bool have_carry = true;  // carry holds band tile 0 of the current key tile
   for (int j0 = jfirst; j0 < jend; j0 += NK, buf ^= 1) {
     const bool more = j0 + NK < jend;
     // the next key tile and its 64 new ring rows (last read before the
@@ -704,6 +705,35 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
     // wave while the memory pipe takes them. The last tile reloads itself,
     // unused, so that every iteration issues the same loads.
     const int jn = more ? j0 + NK : j0, rr0n = rrw - 32 * (NW - 1 - w) + QB + NK;
+
+    // SKIP (8-wave form under a limited context): a wave none of whose
+    // queries sees a key of this tile only issues its share of the loads.
+    // The tile would add nothing (every probability 0; o, l and the
+    // reference unchanged), and the other wave of its SIMD then has the SIMD
+    // to itself. Under a window, a 256-query block's first and last tiles lie
+    // outside most of its waves' windows. (In the 4-wave form each SIMD holds
+    // one wave and the tile barrier waits for the slowest, so skipping there
+    // measured slower; without a window no tile is skipped, and the check
+    // alone measured 4% slower on 1500-frame items. The debug exports cover
+    // every tile.)
+    if constexpr (SKIP) {
+      if (__all(iv.x >= iv.y || iv.y <= j0 || iv.x >= j0 + NK)) {
+#pragma unroll
+        for (int g = 0; g < C::KDMA + C::VDMA; ++g) dma_kv(g, jn, buf ^ 1);
+#pragma unroll
+        for (int g = 0; g < C::PDMA; ++g) dma_ring(g, rr0n);
+        rrw += NK;
+        have_carry = false;
+        __syncthreads();
+        continue;
+      }
+    }
+    // after a skipped tile, band tile 0 from its ring rows (present since
+    // the last barrier)
+    if (!have_carry) {
+      carry = pack(band_tile(rrw));
+      have_carry = true;
+    }
 
     // Band tiles first, each stored to the remap strip as soon as it is
     // done (rel_shift: strip column n of query column c pairs with key
@@ -937,10 +967,10 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
   }
 }
 
-template <int DK, int NW, bool DEBUG>
+template <int DK, int NW, bool DEBUG, bool SKIP = false>
 __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, int nb) {
   __shared__ __attribute__((aligned(16))) char smem[Cfg2<DK, NW>::LDS];
-  attn_bf16_body<DK, NW, DEBUG>(p, nb, (int)blockIdx.x, (int)gridDim.x, smem);
+  attn_bf16_body<DK, NW, DEBUG, SKIP>(p, nb, (int)blockIdx.x, (int)gridDim.x, smem);
 }
 
 // The 8-wave attention of `p` in workgroups [0, nattn) and, in the
@@ -979,25 +1009,27 @@ int64_t order_items(AttnParams& p, int nb) {
   return (work + 7) / 8 * 8;
 }
 
-template <int DK, int NW, bool DEBUG>
+template <int DK, int NW, bool DEBUG, bool SKIP = false>
 hipError_t launch2(AttnParams p, int nb, hipStream_t s) {
   const int64_t grid = order_items<DK, NW>(p, nb);
   if (grid < 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((attn_bf16_kernel<DK, NW, DEBUG>), dim3((unsigned)grid), dim3(Cfg2<DK, NW>::NT), 0, s, p, nb);
+  hipLaunchKernelGGL((attn_bf16_kernel<DK, NW, DEBUG, SKIP>), dim3((unsigned)grid), dim3(Cfg2<DK, NW>::NT), 0, s,
+                     p, nb);
   return hipGetLastError();
 }
 
 // The 8-wave form (d_k = 128) where its 256-query blocks give at least
-// kWide8 workgroups and every query sees every key up to the padding;
-// otherwise the 4-wave form. (Under a limited context every wave of a block
-// computes the key tiles of all the block's windows: 512 keys per query on
-// +-128-frame windows against 384 with 128-query blocks, and the 8-wave form
-// measured 5% slower there, over 7500 frames.)
+// kWide8 workgroups; otherwise the 4-wave form. (Under a limited context a
+// 256-query block spans the key tiles of all its waves' windows, 512 keys
+// on +-128-frame windows against 384 for a 128-query block; its waves pass
+// over the tiles outside their own windows, and over 7500 frames the 8-wave
+// form measured 6% faster than the 4-wave form.)
 constexpr int kWide8 = 160;
+// a window or chunk limits the keys some queries see
+bool windowed(const AttnParams& p) { return p.has_ctx && (p.left >= 0 || p.right >= 0); }
 template <int DK>
 bool use_wide(const AttnParams& p, int nb) {
   if constexpr (DK != 128) return false;
-  if (p.has_ctx && (p.left >= 0 || p.right >= 0)) return false;
   return (int64_t)(p.T + Cfg2<128, 8>::QB - 1) / Cfg2<128, 8>::QB * p.H * nb >= kWide8;
 }
 
@@ -1005,7 +1037,10 @@ template <int DK>
 hipError_t dispatch_bf16(const AttnParams& p, int nb, hipStream_t s) {
   const bool dbg = p.dbg_bd || p.dbg_top;
   if constexpr (DK == 128) {
-    if (use_wide<DK>(p, nb)) return dbg ? launch2<DK, 8, true>(p, nb, s) : launch2<DK, 8, false>(p, nb, s);
+    if (use_wide<DK>(p, nb)) {
+      if (dbg) return launch2<DK, 8, true>(p, nb, s);
+      return windowed(p) ? launch2<DK, 8, false, true>(p, nb, s) : launch2<DK, 8, false>(p, nb, s);
+    }
   }
   return dbg ? launch2<DK, 4, true>(p, nb, s) : launch2<DK, 4, false>(p, nb, s);
 }
@@ -1366,7 +1401,7 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
 hipError_t attention_with_gemm(DType dt, int head_dim, const AttnParams& p, int nb, const GemmParams& g, bool gquant,
                                hipStream_t s) {
   if (nb <= 0 || p.T <= 0 || g.M <= 0) return hipErrorNotSupported;
-  if (dt != kBF16 || head_dim != 128 || !p.vt || p.dbg_bd || p.dbg_top || !use_wide<128>(p, nb))
+  if (dt != kBF16 || head_dim != 128 || !p.vt || p.dbg_bd || p.dbg_top || !use_wide<128>(p, nb) || windowed(p))
     return hipErrorNotSupported;
   if (check_attention(dt, head_dim, p, nb) != hipSuccess) return hipErrorNotSupported;
   TileForm f;

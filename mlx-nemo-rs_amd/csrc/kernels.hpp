@@ -136,8 +136,9 @@ struct AttnParams {
 hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nbatch, hipStream_t s);
 // attention() and, in the same launch, the tile GEMM `g`: a projection that
 // does not depend on the attention (nor the attention on it), whose tiles
-// take the CUs the attention leaves idle. Only for the bf16 8-wave form with
-// a GEMM of 128 x 128 tiles; otherwise hipErrorNotSupported and nothing is
+// take the CUs the attention leaves idle. Only for the bf16 8-wave form
+// without a window or chunk limit and a GEMM of 128 x 128 tiles; otherwise
+// hipErrorNotSupported and nothing is
 // launched (the caller launches the two apart). Same results as apart.
 hipError_t attention_with_gemm(DType dt, int head_dim, const AttnParams& p, int nbatch, const GemmParams& g,
                                bool gquant, hipStream_t s);

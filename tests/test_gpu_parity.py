@@ -493,6 +493,55 @@ def test_local_window_bf16_against_oracle():
     assert err < BF16_TOL
 
 
+@pytest.mark.parametrize("ctx", [((128, 128), "regular"), ((40, 7), "regular"), ((-1, 16), "regular"),
+                                 ((64, -1), "regular"), ((70, 13), "chunked_limited"), ((-1, 31), "chunked_limited")])
+def test_forward_bf16_contexts_against_oracle(ctx):
+    """The bf16 kernel under each kind of context (attention.rs:208-273): two-
+    and one-sided regular windows and chunked_limited chunks, with key
+    padding (lengths 600, 451, 257 of T = 600), on the full 2T-1 table, against
+    the oracle within the bf16 tolerance on the rows that see a key. Windows
+    leave a block's first or last key tiles outside some waves' queries, which
+    those waves pass over."""
+    D, H, T, lengths = 256, 2, 600, [600, 451, 257]
+    rng = np.random.default_rng(73)
+    w = random_weights(rng, D, H)
+    p = oracle_params(w, D, H)
+    x = O.bf16_round(rng.standard_normal((len(lengths), T, D)))
+    pos = O.bf16_round(O.RelPositionalEncoding(D, 5000, True).get_encoding(T))
+    octx = O.AttentionContext.new(*ctx)
+    ref = O.mhsa_forward(p, x, pos, octx, O.key_padding_mask(lengths, T), dtype=O.BF16)
+    layer = gpu_layer(w, D, H, True, O.BF16)
+    got = host(layer.forward(dev(x, O.BF16), dev(pos, O.BF16), M.AttentionContext.new(*ctx),
+                             M.key_padding_mask(lengths, T)))
+    rows = visible_rows(len(lengths), T, octx, lengths)
+    err = abs_err(got[rows], ref[rows])
+    print(f"bf16 context {ctx}: max abs error {err:.3e}")
+    assert err < BF16_TOL
+
+
+@pytest.mark.parametrize("ctx", [((70, 13), "chunked_limited"), ((64, -1), "regular")])
+def test_forward_bf16_contexts_eight_wave(ctx):
+    """The same at the 0.6B shape with B=4, T=1100 (lengths 1100, 987, 800,
+    1033): 5 blocks of 256 queries per item and head, 160 workgroups, so the
+    8-wave form runs, whose waves pass over the key tiles outside their
+    queries' windows or chunks."""
+    D, H, T, lengths = 1024, 8, 1100, [1100, 987, 800, 1033]
+    rng = np.random.default_rng(74)
+    w = random_weights(rng, D, H)
+    p = oracle_params(w, D, H)
+    x = O.bf16_round(rng.standard_normal((len(lengths), T, D)))
+    pos = O.bf16_round(O.RelPositionalEncoding(D, 5000, True).get_encoding(T))
+    octx = O.AttentionContext.new(*ctx)
+    ref = O.mhsa_forward(p, x, pos, octx, O.key_padding_mask(lengths, T), dtype=O.BF16)
+    layer = gpu_layer(w, D, H, True, O.BF16)
+    got = host(layer.forward(dev(x, O.BF16), dev(pos, O.BF16), M.AttentionContext.new(*ctx),
+                             M.key_padding_mask(lengths, T)))
+    rows = visible_rows(len(lengths), T, octx, lengths)
+    err = abs_err(got[rows], ref[rows])
+    print(f"bf16 context {ctx}, 8-wave form: max abs error {err:.3e}")
+    assert err < BF16_TOL
+
+
 def test_local_window_full_size_band_equals_full_table():
     """At B=2, T=7500 the banded table and the full 2T-1 table must give
     bit-identical outputs (the band holds every row the window reads)."""
