@@ -4,6 +4,8 @@
 // weight export used by the bit-exact checks.
 #include <algorithm>
 
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 #include "quant.hpp"
@@ -54,7 +56,7 @@ __global__ __launch_bounds__(256) void ln_kernel(const T* x, T* y, const float* 
 
 // The same with 16-byte accesses: lane l holds chunks l + 64 j of the row
 // (D a multiple of 64 chunks), gamma and beta read as float4.
-template <typename T, int NCH>
+template <typename T, int NCH, bool GAMMA, bool BETA>
 __global__ __launch_bounds__(256) void ln_vec_kernel(const T* x, T* y, const float* gamma, const float* beta,
                                                      float eps, int rows, int D, int act) {
   constexpr int E = 16 / sizeof(T);  // elements per chunk
@@ -62,12 +64,28 @@ __global__ __launch_bounds__(256) void ln_vec_kernel(const T* x, T* y, const flo
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
   const T* xr = x + (int64_t)row * D;
+  // The row's chunks, then gamma and beta of the same columns (they do not
+  // depend on the row), all issued before the first wait so that their
+  // latencies overlap; one instantiation per affine form keeps the loads
+  // free of branches, which would split them into separate waits.
+  u32x4 raw[NCH];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) raw[j] = *reinterpret_cast<const u32x4*>(xr + (lane + 64 * j) * E);
+  floatx4 g4[NCH][E / 4], b4[NCH][E / 4];
+#pragma unroll
+  for (int j = 0; j < NCH; ++j)
+#pragma unroll
+    for (int e4 = 0; e4 < E / 4; ++e4) {
+      const int c0 = (lane + 64 * j) * E + 4 * e4;
+      g4[j][e4] = GAMMA ? *reinterpret_cast<const floatx4*>(gamma + c0) : floatx4{1.f, 1.f, 1.f, 1.f};
+      b4[j][e4] = BETA ? *reinterpret_cast<const floatx4*>(beta + c0) : floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+  __builtin_amdgcn_sched_barrier(0);
   float v[NCH][E];
   float s = 0.f;
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
-    const u32x4 raw = *reinterpret_cast<const u32x4*>(xr + (lane + 64 * j) * E);
-    const T* t = reinterpret_cast<const T*>(&raw);
+    const T* t = reinterpret_cast<const T*>(&raw[j]);
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       v[j][e] = (float)t[e];
@@ -87,25 +105,39 @@ __global__ __launch_bounds__(256) void ln_vec_kernel(const T* x, T* y, const flo
   for (int o = 32; o > 0; o >>= 1) q += __shfl_xor(q, o, 64);
   const float rstd = rsqrtf(q / (float)D + eps);
   T* yr = y + (int64_t)row * D;
+  // (the activation test taken once, outside the element loops)
+  auto emit = [&](auto silu) {
 #pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    const int c0 = (lane + 64 * j) * E;
-    T out[E];
+    for (int j = 0; j < NCH; ++j) {
+      const int c0 = (lane + 64 * j) * E;
+      T out[E];
 #pragma unroll
-    for (int e4 = 0; e4 < E; e4 += 4) {
-      const floatx4 g = gamma ? *reinterpret_cast<const floatx4*>(gamma + c0 + e4) : floatx4{1.f, 1.f, 1.f, 1.f};
-      const floatx4 b = beta ? *reinterpret_cast<const floatx4*>(beta + c0 + e4) : floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int e4 = 0; e4 < E; e4 += 4) {
+        const floatx4 g = g4[j][e4 / 4], b = b4[j][e4 / 4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float t = (v[j][e4 + e] - mean) * rstd;
-        if (gamma) t *= g[e];
-        if (beta) t += b[e];
-        if (act == kActSilu) t = silu_value<T>(round_to<T>(t));
-        out[e4 + e] = from_float<T>(t);
+        for (int e = 0; e < 4; ++e) {
+          float t = (v[j][e4 + e] - mean) * rstd;
+          if (GAMMA) t *= g[e];
+          if (BETA) t += b[e];
+          if constexpr (decltype(silu)::value) t = silu_value<T>(round_to<T>(t));
+          out[e4 + e] = from_float<T>(t);
+        }
       }
+      *reinterpret_cast<u32x4*>(yr + c0) = *reinterpret_cast<const u32x4*>(out);
     }
-    *reinterpret_cast<u32x4*>(yr + c0) = *reinterpret_cast<const u32x4*>(out);
-  }
+  };
+  if (act == kActSilu) emit(std::true_type{});
+  else emit(std::false_type{});
+}
+
+template <typename T, int NCH>
+hipError_t ln_vec_launch(dim3 grid, const T* x, T* y, const float* g, const float* b, float eps, int rows, int D,
+                         int act, hipStream_t s) {
+  if (g && b) hipLaunchKernelGGL((ln_vec_kernel<T, NCH, true, true>), grid, dim3(256), 0, s, x, y, g, b, eps, rows, D, act);
+  else if (g) hipLaunchKernelGGL((ln_vec_kernel<T, NCH, true, false>), grid, dim3(256), 0, s, x, y, g, b, eps, rows, D, act);
+  else if (b) hipLaunchKernelGGL((ln_vec_kernel<T, NCH, false, true>), grid, dim3(256), 0, s, x, y, g, b, eps, rows, D, act);
+  else hipLaunchKernelGGL((ln_vec_kernel<T, NCH, false, false>), grid, dim3(256), 0, s, x, y, g, b, eps, rows, D, act);
+  return hipGetLastError();
 }
 
 template <typename T>
@@ -118,14 +150,11 @@ hipError_t ln_launch(const void* x, void* y, const float* g, const float* b, flo
   if (aligned && D % (64 * E) == 0) {
     switch (D / (64 * E)) {
       case 1:
-        hipLaunchKernelGGL((ln_vec_kernel<T, 1>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D, act);
-        return hipGetLastError();
+        return ln_vec_launch<T, 1>(grid, (const T*)x, (T*)y, g, b, eps, rows, D, act, s);
       case 2:
-        hipLaunchKernelGGL((ln_vec_kernel<T, 2>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D, act);
-        return hipGetLastError();
+        return ln_vec_launch<T, 2>(grid, (const T*)x, (T*)y, g, b, eps, rows, D, act, s);
       case 4:
-        hipLaunchKernelGGL((ln_vec_kernel<T, 4>), grid, dim3(256), 0, s, (const T*)x, (T*)y, g, b, eps, rows, D, act);
-        return hipGetLastError();
+        return ln_vec_launch<T, 4>(grid, (const T*)x, (T*)y, g, b, eps, rows, D, act, s);
       default:
         break;
     }
