@@ -359,13 +359,23 @@ int32_t mhsa_checkpoint_open(const char* path, mhsa_checkpoint** out) {
     mhsa_tensor mt{};
     mt.dtype = code;
     mt.ndim = (int32_t)sh->arr.size();
-    uint64_t numel = 1;
-    for (size_t i = 0; i < sh->arr.size(); ++i) {
-      mt.shape[i] = (int64_t)sh->arr[i].num;
-      numel *= (uint64_t)mt.shape[i];
+    // dimensions and offsets are whole numbers below 2^53 (exact in the
+    // JSON reader's doubles), and the byte size may not wrap: a shape whose
+    // product overflows could otherwise match a short data range
+    auto whole = [](const Json& j) {
+      return j.kind == Json::kNum && j.num >= 0 && j.num < 9.0e15 && j.num == (double)(int64_t)j.num;
+    };
+    uint64_t nbytes = esz;
+    bool ok = whole(off->arr[0]) && whole(off->arr[1]);
+    for (size_t i = 0; i < sh->arr.size() && ok; ++i) {
+      ok = whole(sh->arr[i]);
+      mt.shape[i] = ok ? (int64_t)sh->arr[i].num : 0;
+      if (ok && mt.shape[i] && nbytes > data_len / (uint64_t)mt.shape[i] + 1) ok = false;
+      nbytes *= (uint64_t)mt.shape[i];
     }
+    if (!ok) return ckfail(MHSA_EINVAL, "%s: `%s` has a bad shape or data offsets", weights.c_str(), kv.first.c_str());
     const uint64_t b0 = (uint64_t)off->arr[0].num, b1 = (uint64_t)off->arr[1].num;
-    if (b1 < b0 || b1 > data_len || b1 - b0 != numel * esz)
+    if (b1 < b0 || b1 > data_len || b1 - b0 != nbytes)
       return ckfail(MHSA_EINVAL, "%s: `%s` data offsets do not match its shape", weights.c_str(), kv.first.c_str());
     const unsigned char* src = data + b0;
     if (reinterpret_cast<uintptr_t>(src) % esz) {  // element reads must be aligned

@@ -130,7 +130,18 @@ def test_misaligned_tensor_and_malformed_files(tmp_path):
     # not JSON
     with open(tmp_path / "bad3.safetensors", "wb") as f:
         f.write(struct.pack("<Q", 5) + b"{nope" + data)
-    for n in ("bad1", "bad2", "bad3"):
+    # a shape whose byte size wraps 64 bits to the empty range it names
+    # (2^40 * 2^40 * 4 = 2^82 = 0 mod 2^64), a negative and a fractional
+    # dimension, a negative offset
+    wrap = dict(ents, b={"dtype": "F32", "shape": [2 ** 40, 2 ** 40], "data_offsets": [7, 7]})
+    _raw_file(tmp_path / "bad4.safetensors", wrap, data)
+    _raw_file(tmp_path / "bad5.safetensors", dict(ents, b={"dtype": "F32", "shape": [-5], "data_offsets": [7, 27]}),
+              data)
+    _raw_file(tmp_path / "bad6.safetensors", dict(ents, b={"dtype": "F32", "shape": [2.5, 2], "data_offsets": [7, 27]}),
+              data)
+    _raw_file(tmp_path / "bad7.safetensors", dict(ents, a={"dtype": "F16", "shape": [3], "data_offsets": [-6, 0]}),
+              data)
+    for n in ("bad1", "bad2", "bad3", "bad4", "bad5", "bad6", "bad7"):
         with pytest.raises(M.MhsaError) as e:
             M.Checkpoint(str(tmp_path / f"{n}.safetensors"))
         assert e.value.code == M.MHSA_EINVAL, n
