@@ -492,9 +492,11 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef __bf16 bf16x8_a2 __attribute__((ext_vector_type(8), aligned(2)));
 
 // The kernel's work as workgroup `block` of `nblocks` (a multiple of 8), in
-// `smem` (C::LDS bytes, 16-byte aligned).
+// `smem` (C::LDS bytes, 16-byte aligned), over the nb items p.order[ord0 ..
+// ord0 + nb).
 template <int DK, int NW, bool DEBUG, bool SKIP = false>
-__device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int block, int nblocks, char* smem) {
+__device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int block, int nblocks, char* smem,
+                                               int ord0 = 0) {
   using C = Cfg2<DK, NW>;
   constexpr int QB = C::QB, NK = C::NK, NU = C::NU, NS = C::NS, RB = C::RB;
   constexpr int PF = 3;  // MFMA steps an LDS operand read is issued ahead
@@ -508,7 +510,7 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
   if (W >= nqb * nb * p.H) return;
   const int tid = threadIdx.x, lane = tid & 63, hh = lane >> 5, c = lane & 31;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index (uniform)
-  const int bl = p.order[(W / nqb) % nb], b = p.b0 + bl, h = W / (nqb * nb);
+  const int bl = p.order[ord0 + (W / nqb) % nb], b = p.b0 + bl, h = W / (nqb * nb);
   const int i0 = (W % nqb) * QB;
   const int iw = i0 + 32 * w;  // first query of this wave
   const int qi = iw + c;       // this lane's query column
@@ -973,19 +975,29 @@ __global__ __launch_bounds__(64 * NW) void attn_bf16_kernel(const AttnParams p, 
   attn_bf16_body<DK, NW, DEBUG, SKIP>(p, nb, (int)blockIdx.x, (int)gridDim.x, smem);
 }
 
-// The 8-wave attention of `p` in workgroups [0, nattn) and, in the
-// workgroups after them, the tile GEMM `g`: a projection that does not
-// depend on the attention (the next layer's position rows). Workgroups are
-// dispatched in order, so the GEMM's tiles take the CUs the attention leaves
-// idle once every attention workgroup has one. Waves 4-7 of a GEMM
-// workgroup end at once (the tile body runs on 4 waves).
-template <int GBM, int GBN, bool GQ, int GNS>
-__global__ __launch_bounds__(512) void attn_bf16_gemm_kernel(const AttnParams p, int nb, int nattn, const GemmParams g) {
-  constexpr int LA = Cfg2<128, 8>::LDS, LG = TileCfg<GBM, GBN, GQ, GNS>::LDS;
+// The bf16 attention (d_k = 128) of p's items in both forms in one launch:
+// items p.order[0, nb4) in the 4-wave form in workgroups [0, n4) (waves 4-7
+// end at once), items p.order[nb4, nb) in the 8-wave form in workgroups
+// [n4, n4 + n8), and, with GEMM, the tile GEMM `g` in the workgroups after
+// them: a projection that does not depend on the attention (the next layer's
+// position rows). Workgroups are dispatched in index order, so every
+// attention workgroup has its CU before the first GEMM tile, and the tiles
+// take the CUs the attention leaves idle. A GEMM workgroup runs the tile body
+// on its first 4 waves.
+template <bool GEMM, int GBM, int GBN, bool GQ, int GNS>
+__global__ __launch_bounds__(512) void attn_bf16_mixed_kernel(const AttnParams p, int nb4, int n4, int nb, int n8,
+                                                              const GemmParams g) {
+  constexpr int L4 = Cfg2<128, 4>::LDS, L8 = Cfg2<128, 8>::LDS, LG = GEMM ? TileCfg<GBM, GBN, GQ, GNS>::LDS : 0;
+  constexpr int LA = L4 > L8 ? L4 : L8;
   __shared__ __attribute__((aligned(1024))) char smem[LA > LG ? LA : LG];
   const int block = (int)blockIdx.x;
-  if (block < nattn) attn_bf16_body<128, 8, false>(p, nb, block, nattn, smem);
-  else if (threadIdx.x < 256) gemm_tile_body<GBM, GBN, GQ, GNS>(g, block - nattn, smem);
+  if (block < n4) {
+    if (threadIdx.x < 256) attn_bf16_body<128, 4, false>(p, nb4, block, n4, smem, 0);
+  } else if (block < n4 + n8) {
+    attn_bf16_body<128, 8, false>(p, nb - nb4, block - n4, n8, smem, nb4);
+  } else if constexpr (GEMM) {
+    if (threadIdx.x < 256) gemm_tile_body<GBM, GBN, GQ, GNS>(g, block - n4 - n8, smem);
+  }
 }
 
 // Items in launch order, longest key range first, so that the work left for
@@ -1033,13 +1045,81 @@ bool use_wide(const AttnParams& p, int nb) {
   return (int64_t)(p.T + Cfg2<128, 8>::QB - 1) / Cfg2<128, 8>::QB * p.H * nb >= kWide8;
 }
 
+// Items of an 8-wave launch moved to the 4-wave form. The 8-wave form does
+// more work per CU (measured ~4400 cycles per 32-key tile of a 256-query
+// block against ~5450 per 64-key tile of a 128-query block); the 4-wave form
+// spreads an item over twice the workgroups. When the 8-wave blocks take one
+// round of workgroups with CUs left idle, the longest items, moved to the
+// 4-wave form while the busy blocks still fit the CUs, finish sooner, and
+// the launch ends with its slowest block.
+struct FormSplit {
+  int nb4 = 0;             // items p.order[0, nb4) in the 4-wave form
+  int64_t n4 = 0, n8 = 0;  // workgroups of each form (multiples of 8)
+};
+constexpr int64_t kTile8 = 4400, kTile4 = 5450, kBlockFixed = 11000;  // cycles
+FormSplit split_forms(AttnParams& p, int nb) {
+  using C4 = Cfg2<128, 4>;
+  using C8 = Cfg2<128, 8>;
+  FormSplit f;
+  int64_t c4[kMaxBatch], c8[kMaxBatch];
+  int busy4[kMaxBatch], busy8[kMaxBatch];
+  for (int bl = 0; bl < nb; ++bl) {
+    int jbeg, jend;
+    key_range(p, bl, 0, p.T, jbeg, jend);
+    const int rows = imin(p.q_valid[bl], p.T), keys = jend > jbeg && rows > 0 ? jend - jbeg : 0;
+    c8[bl] = keys ? kBlockFixed + kTile8 * ((keys + C8::NK - 1) / C8::NK) : 0;
+    c4[bl] = keys ? kBlockFixed + kTile4 * ((keys + C4::NK - 1) / C4::NK) : 0;
+    busy8[bl] = keys ? (rows + C8::QB - 1) / C8::QB * p.H : 0;
+    busy4[bl] = keys ? (rows + C4::QB - 1) / C4::QB * p.H : 0;
+    p.order[bl] = bl;
+  }
+  std::stable_sort(p.order, p.order + nb, [&](int a, int b) { return c8[a] > c8[b]; });
+  int64_t busy = 0;
+  for (int i = 0; i < nb; ++i) busy += busy8[p.order[i]];
+  const int cus = device_cus();
+  int best = 0;
+  int64_t best_t = nb ? c8[p.order[0]] : 0, head4 = 0;
+  for (int k = 1; k <= nb && busy <= cus; ++k) {
+    const int it = p.order[k - 1];
+    busy += busy4[it] - busy8[it];
+    head4 = std::max(head4, c4[it]);
+    const int64_t t = std::max(head4, k < nb ? c8[p.order[k]] : int64_t(0));
+    // switch forms only for a clear gain (3%) over the model's error
+    if (busy <= cus && t * 100 < best_t * 97) {
+      best = k;
+      best_t = t;
+    }
+  }
+  if (best == 0) return f;
+  f.nb4 = best;
+  f.n4 = ((int64_t)(p.T + C4::QB - 1) / C4::QB * p.H * best + 7) / 8 * 8;
+  f.n8 = ((int64_t)(p.T + C8::QB - 1) / C8::QB * p.H * (nb - best) + 7) / 8 * 8;
+  return f;
+}
+
+template <bool GEMM, int GBM, int GBN, bool GQ, int GNS>
+void launch_mixed(const AttnParams& p, int nb, const FormSplit& f, const GemmParams& g, int64_t gtiles,
+                  hipStream_t s) {
+  hipLaunchKernelGGL((attn_bf16_mixed_kernel<GEMM, GBM, GBN, GQ, GNS>), dim3((unsigned)(f.n4 + f.n8 + gtiles)),
+                     dim3(512), 0, s, p, f.nb4, (int)f.n4, nb, (int)f.n8, g);
+}
+
 template <int DK>
 hipError_t dispatch_bf16(const AttnParams& p, int nb, hipStream_t s) {
   const bool dbg = p.dbg_bd || p.dbg_top;
   if constexpr (DK == 128) {
     if (use_wide<DK>(p, nb)) {
       if (dbg) return launch2<DK, 8, true>(p, nb, s);
-      return windowed(p) ? launch2<DK, 8, false, true>(p, nb, s) : launch2<DK, 8, false>(p, nb, s);
+      if (windowed(p)) return launch2<DK, 8, false, true>(p, nb, s);
+      if ((int64_t)p.T * p.H * nb <= (1 << 28)) {
+        AttnParams a = p;
+        const FormSplit f = split_forms(a, nb);
+        if (f.nb4) {
+          launch_mixed<false, 128, 128, false, 4>(a, nb, f, GemmParams(), 0, s);
+          return hipGetLastError();
+        }
+      }
+      return launch2<DK, 8, false>(p, nb, s);
     }
   }
   return dbg ? launch2<DK, 4, true>(p, nb, s) : launch2<DK, 4, false>(p, nb, s);
@@ -1404,17 +1484,19 @@ hipError_t attention_with_gemm(DType dt, int head_dim, const AttnParams& p, int 
   if (dt != kBF16 || head_dim != 128 || !p.vt || p.dbg_bd || p.dbg_top || !use_wide<128>(p, nb) || windowed(p))
     return hipErrorNotSupported;
   if (check_attention(dt, head_dim, p, nb) != hipSuccess) return hipErrorNotSupported;
-  TileForm f;
-  if (!gemm_tile_form(dt, gquant, g, f) || f.bm != 128 || f.bn != 128 || f.ns != 4) return hipErrorNotSupported;
+  TileForm tf;
+  if (!gemm_tile_form(dt, gquant, g, tf) || tf.bm != 128 || tf.bn != 128 || tf.ns != 4) return hipErrorNotSupported;
   AttnParams a = p;
-  const int64_t nattn = order_items<128, 8>(a, nb);
-  const int64_t tiles = m_tiles<128>(g) * (g.N / 128);
-  if (nattn < 0 || nattn + (tiles + 7) / 8 * 8 > (1 << 30)) return hipErrorNotSupported;
-  const dim3 grid((unsigned)(nattn + (tiles + 7) / 8 * 8));
-  if (gquant)
-    hipLaunchKernelGGL((attn_bf16_gemm_kernel<128, 128, true, 4>), grid, dim3(512), 0, s, a, nb, (int)nattn, g);
-  else
-    hipLaunchKernelGGL((attn_bf16_gemm_kernel<128, 128, false, 4>), grid, dim3(512), 0, s, a, nb, (int)nattn, g);
+  FormSplit f;
+  if ((int64_t)p.T * p.H * nb <= (1 << 28)) f = split_forms(a, nb);
+  if (!f.nb4) {
+    f.n8 = order_items<128, 8>(a, nb);
+    if (f.n8 < 0) return hipErrorNotSupported;
+  }
+  const int64_t tiles = (m_tiles<128>(g) * (g.N / 128) + 7) / 8 * 8;
+  if (f.n4 + f.n8 + tiles > (1 << 30)) return hipErrorNotSupported;
+  if (gquant) launch_mixed<true, 128, 128, true, 4>(a, nb, f, g, tiles, s);
+  else launch_mixed<true, 128, 128, false, 4>(a, nb, f, g, tiles, s);
   return hipGetLastError();
 }
 

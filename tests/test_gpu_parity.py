@@ -412,24 +412,31 @@ def test_forward_bf16_4000_rows():
     assert err < BF16_TOL
 
 
-def test_forward_bf16_eight_wave_blocks():
+@pytest.mark.parametrize("padded", [False, True], ids=["eight_wave", "mixed_forms"])
+def test_forward_bf16_eight_wave_blocks(padded):
     """The 0.6B-shape offline bf16 layer at B=5, T=1100: 5 blocks of 256
     queries per (item, head), 200 workgroups, so the attention takes the
-    8-wave form with 32-key tiles; the last block is ragged (76 queries) and
-    the items' key padding ends inside key tiles. Against the oracle within
-    the bf16 tolerance."""
+    8-wave form with 32-key tiles; the last block is ragged (76 queries).
+    Unpadded, every item takes that form. With key padding (lengths 921,
+    1015, 1100, 989, 1028, ending inside key tiles) the longest item takes
+    the 4-wave form in the same launch: 72 workgroups of 128 queries with 18
+    tiles of 64 keys, beside 160 8-wave workgroups whose longest has 33 tiles
+    of 32 keys (35 for the moved item). Against the oracle within the bf16
+    tolerance."""
     D, H, T, B = 1024, 8, 1100, 5
     w, rng = _biased_weights(85, D, H, 0.1)
     x = rng.normal(size=(B, T, D))
     lengths = [int(v) for v in rng.integers(600, T + 1, size=B)]
     lengths[2] = T
+    mask = O.key_padding_mask(lengths, T) if padded else None
     p = oracle_params(w, D, H)
     pos = O.RelPositionalEncoding(D, 5000, True).get_encoding(T)
-    ref = O.mhsa_forward(p, O.bf16_round(x), O.bf16_round(pos), None, O.key_padding_mask(lengths, T), dtype=O.BF16)
+    ref = O.mhsa_forward(p, O.bf16_round(x), O.bf16_round(pos), None, mask, dtype=O.BF16)
     layer = gpu_layer(w, D, H, True, O.BF16)
-    got = host(layer.forward(dev(x, O.BF16), dev(pos, O.BF16), None, M.key_padding_mask(lengths, T)))
+    got = host(layer.forward(dev(x, O.BF16), dev(pos, O.BF16), None,
+                             M.key_padding_mask(lengths, T) if padded else None))
     err = abs_err(got, ref)
-    print(f"bf16 eight-wave blocks: max abs error {err:.3e} (max |ref| {np.max(np.abs(ref)):.2f})")
+    print(f"bf16 eight-wave blocks (padded {padded}): max abs error {err:.3e} (max |ref| {np.max(np.abs(ref)):.2f})")
     assert err < BF16_TOL
 
 
@@ -1024,19 +1031,24 @@ def test_stack_u8_well_conditioned_against_oracle():
     assert err < 2e-2
 
 
-@pytest.mark.parametrize("kind", ["u8_8wave_fused", "bf16_4wave", "f32"])
+@pytest.mark.parametrize("kind", ["u8_8wave_fused", "u8_mixed_fused", "bf16_4wave", "f32"])
 def test_stack_sublayer_forward_equals_layer_loop(kind):
     """mhsa_stack_sublayer_forward gives the results of mhsa_sublayer_forward
     called layer by layer, bit for bit: at the quantized stack's shape (B=4,
     T=1500, key padding: each next layer's position projection runs in the
     same launch as the attention), on a bf16 shape of the 4-wave form and in
-    fp32 (projections run apart), with per-layer LayerNorm parameters."""
-    if kind == "u8_8wave_fused":
+    fp32 (projections run apart), with per-layer LayerNorm parameters. At the
+    stack's shape, lengths 1014, 1438, 1303, 1396 keep every item in the
+    8-wave form; with lengths 1000, 1364, 1295, 1227 (the stack workload's)
+    the longest item takes the 4-wave form in the same launch."""
+    if kind.startswith("u8_"):
         cfg = W.CONFIGS["xl_stack_u8"]
         D, H, T, B, n = cfg.d_model, cfg.n_heads, cfg.seq_len, cfg.batch, 3
         rng = np.random.default_rng(47)
         wts = [W.make_layer_weights(rng, D, H, False, True) for _ in range(n)]
         lengths = [int(v) for v in rng.integers(1000, T + 1, size=B)]
+        if kind == "u8_mixed_fused":
+            lengths = [1000, 1364, 1295, 1227]
         dtype = O.BF16
     else:
         D, H, T, B, n = 256, 2, 300, 3, 3
@@ -1044,7 +1056,7 @@ def test_stack_sublayer_forward_equals_layer_loop(kind):
         wts = [W.make_layer_weights(rng, D, H, True, False) for _ in range(n)]
         lengths = [300, 211, 97]
         dtype = O.BF16 if kind == "bf16_4wave" else O.F32
-    layers = [gpu_layer(w, D, H, kind != "u8_8wave_fused", dtype) for w in wts]
+    layers = [gpu_layer(w, D, H, not kind.startswith("u8_"), dtype) for w in wts]
     gamma = 1.0 + 0.1 * rng.standard_normal((n, D))
     beta = 0.1 * rng.standard_normal((n, D))
     x = rng.standard_normal((B, T, D))
