@@ -319,6 +319,13 @@ int32_t mhsa_ffn_sublayer_forward(mhsa_ffn* ffn, void* x_inout, int32_t rows, co
 int32_t mhsa_ffn_forward_f32(mhsa_ffn* ffn, const float* x, int32_t rows, float* out, void* hip_stream);
 int32_t mhsa_ffn_sublayer_forward_f32(mhsa_ffn* ffn, float* x_inout, int32_t rows, const float* ln_gamma_host,
                                       const float* ln_beta_host, float eps, void* hip_stream);
+/* Debug: linear `which` (0 = linear1, 1 = linear2) alone, as the plain
+ * LinearLayer::forward (quantization.rs:126-162) through the GEMM kernels the
+ * module runs, without its SiLU or residual epilogue: out [rows, out_dim] =
+ * x [rows, in_dim] W^T + b, device; in the module dtype, or f32 (the
+ * promoted streaming form) when f32_act. */
+int32_t mhsa_ffn_debug_linear(mhsa_ffn* ffn, int32_t which, int32_t f32_act, const void* x, int32_t rows, void* out,
+                              void* hip_stream);
 
 /* ---- ConvolutionModule (the Conformer block's convolution sublayer) ------- */
 
@@ -359,6 +366,11 @@ int32_t mhsa_conv_cache_size(const mhsa_conv* conv);
 /* The dtype mhsa_conv_forward writes: the module dtype for a symmetric
  * module, MHSA_F32 for a causal one. */
 int32_t mhsa_conv_output_dtype(const mhsa_conv* conv);
+/* Debug: pointwise_conv{1,2} (which 0, 1) alone, as LinearLayer::forward
+ * through the module's GEMM kernels: out [rows, 2D or D] = x [rows, D] W^T +
+ * b, device, in the module dtype or f32 when f32_act. */
+int32_t mhsa_conv_debug_linear(mhsa_conv* conv, int32_t which, int32_t f32_act, const void* x, int32_t rows,
+                               void* out, void* hip_stream);
 /* forward (conformer.rs:2197-2291): x [batch, seq_len, d_model] device, in
  * the module dtype; lengths [batch] host (frames >= lengths[b] are padding,
  * zeroed after the GLU; NULL = none); out [batch, seq_len, d_model] device
@@ -465,6 +477,24 @@ int32_t mhsa_debug_dequantize(mhsa_layer* layer, int32_t which, float* out_dev, 
  * through the same GEMM kernels the forward pass uses. */
 int32_t mhsa_debug_linear(mhsa_layer* layer, int32_t which, const void* x, int32_t rows, void* out_dev,
                           void* hip_stream);
+/* The same projection as the streaming path runs it: f32 activations x,
+ * out_dev [rows, d_model], fp32 kernels; a bf16 layer's parameters keep
+ * their bf16 values (MLX promotes the op to f32, conformer.rs:845-849). */
+int32_t mhsa_debug_linear_f32(mhsa_layer* layer, int32_t which, const float* x, int32_t rows, float* out_dev,
+                              void* hip_stream);
+/* Launches of each attention kernel form since the library was loaded
+ * (process-wide; no reference counterpart): counts[f] for f < n, in the
+ * order 0 bf16 4-wave, 1 bf16 8-wave, 2 bf16 8-wave with tile skipping,
+ * 3 both bf16 forms in one launch, 4 both bf16 forms with a projection GEMM
+ * in the launch, 5 fp32 streaming chunk, 6 generic, 7 generic key split.
+ * Returns the number of forms (8). */
+int32_t mhsa_debug_attention_forms(int64_t* counts, int32_t n);
+/* The sublayer's LayerNorm alone (nn::LayerNorm, conformer.rs:1749), as
+ * mhsa_sublayer_forward and mhsa_stack_sublayer_forward run it: out_dev
+ * [rows, d_model] = LayerNorm(x) in the layer dtype (device); gamma/beta
+ * host fp32 or NULL. */
+int32_t mhsa_debug_layer_norm(mhsa_layer* layer, const void* x, int32_t rows, const float* ln_gamma_host,
+                              const float* ln_beta_host, float eps, void* out_dev, void* hip_stream);
 /* Visibility map [batch, seq_len, seq_len] (1 = visible) the offline kernel
  * applies for (ctx, key lengths) (device output). */
 int32_t mhsa_debug_offline_mask(int32_t batch, int32_t seq_len, const mhsa_context* ctx,

@@ -21,6 +21,7 @@
 // dtype for the PV MFMA. Key tiles that no query of the block can see are
 // skipped, so a +-w local window costs O(T w) instead of O(T^2).
 #include <algorithm>
+#include <atomic>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -32,6 +33,9 @@ namespace {
 #include "gemm_tile.hpp"
 
 constexpr float kLog2e = 1.4426950408889634f;
+
+std::atomic<int64_t> g_form_launches[kAttnForms];
+void count_form(AttnForm f) { g_form_launches[f].fetch_add(1, std::memory_order_relaxed); }
 
 // Every mask of the path hides keys outside one interval per query (i at
 // absolute frame ia = qoff + i): the padding / unfilled-cache range
@@ -94,11 +98,11 @@ __host__ __device__ inline void key_range(const AttnParams& p, int bl, int i0, i
   }
 }
 
-template <typename T, int DK, int NW>
+template <typename T, int DK, int NW, int NKO = 0>
 struct Cfg {
   static constexpr int NT = 64 * NW;
   static constexpr int QB = 16 * NW;
-  static constexpr int NK = sizeof(T) == 2 ? 64 : 32;
+  static constexpr int NK = NKO ? NKO : sizeof(T) == 2 ? 64 : 32;
   static constexpr int RB = DK * (int)sizeof(T);           // bytes per K/P row
   static constexpr int KP = RB + 16;                       // LDS pitch of K and P rows
   static constexpr int VP = NK * (int)sizeof(T) + 16;      // LDS pitch of V^T rows
@@ -118,9 +122,21 @@ struct Cfg {
 // waves of a workgroup share its 16 queries and take the key tiles w,
 // w + NW, ... each with LDS tiles of its own and no workgroup barrier in the
 // loop; their softmax states (running maximum, sum, O) are merged at the end.
+// In the split form each wave prefetches a whole key tile into registers
+// (K, V and position rows: 16 KB per 16 keys at d_k = 128 in fp32), so fp32
+// d_k = 128 takes 16-key tiles: with 32-key tiles the prefetch alone held 224
+// of the 256 VGPRs and the kernel spilled to AGPRs and scratch.
+template <typename T, int DK, bool KS>
+constexpr int gen_tile_keys() { return KS && sizeof(T) == 4 && DK == 128 ? 16 : 0; }
+
 template <typename T, int DK, int NW, bool DEBUG, bool KS = false>
 __global__ __launch_bounds__(64 * NW) void attn_kernel(const AttnParams p) {
-  using C = Cfg<T, DK, KS ? 1 : NW>;  // (split: one wave's tile geometry, 16 queries)
+  // Forms: NW >= 4 waves of 16 queries sharing each key tile, or the key
+  // split. A one-wave shared-tile form (16 queries, no split) is not built:
+  // it gave wrong outputs whenever its per-key mask ran while spilling at
+  // 256 VGPRs + 256 AGPRs, and the split form covers short query blocks.
+  static_assert(KS || NW >= 4, "the shared-tile form needs at least 4 waves");
+  using C = Cfg<T, DK, KS ? 1 : NW, gen_tile_keys<T, DK, KS>()>;  // (split: one wave's tile geometry, 16 queries)
   using F = Frag<T>;
   using frag_t = typename F::type;
   constexpr int NT = C::NT, QB = C::QB, NK = C::NK, EPL = F::EPL;
@@ -1027,6 +1043,7 @@ hipError_t launch2(AttnParams p, int nb, hipStream_t s) {
   if (grid < 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL((attn_bf16_kernel<DK, NW, DEBUG, SKIP>), dim3((unsigned)grid), dim3(Cfg2<DK, NW>::NT), 0, s,
                      p, nb);
+  count_form(NW == 4 ? kFormBf16Wave4 : SKIP ? kFormBf16Wave8Skip : kFormBf16Wave8);
   return hipGetLastError();
 }
 
@@ -1102,6 +1119,7 @@ void launch_mixed(const AttnParams& p, int nb, const FormSplit& f, const GemmPar
                   hipStream_t s) {
   hipLaunchKernelGGL((attn_bf16_mixed_kernel<GEMM, GBM, GBN, GQ, GNS>), dim3((unsigned)(f.n4 + f.n8 + gtiles)),
                      dim3(512), 0, s, p, f.nb4, (int)f.n4, nb, (int)f.n8, g);
+  count_form(GEMM ? kFormBf16MixedGemm : kFormBf16Mixed);
 }
 
 template <int DK>
@@ -1349,6 +1367,7 @@ hipError_t launch(const AttnParams& p, int nb, hipStream_t s) {
   using C = Cfg<T, DK, NW>;
   dim3 grid((p.T + C::QB - 1) / C::QB, p.H, nb);
   hipLaunchKernelGGL((attn_kernel<T, DK, NW, DEBUG>), grid, dim3(C::NT), 0, s, p);
+  count_form(kFormGeneric);
   return hipGetLastError();
 }
 
@@ -1357,6 +1376,7 @@ template <typename T, int DK, int NW>
 hipError_t launch_ks(const AttnParams& p, int nb, hipStream_t s) {
   dim3 grid((p.T + 15) / 16, p.H, nb);
   hipLaunchKernelGGL((attn_kernel<T, DK, NW, false, true>), grid, dim3(64 * NW), 0, s, p);
+  count_form(kFormKeySplit);
   return hipGetLastError();
 }
 
@@ -1372,7 +1392,7 @@ hipError_t dispatch_nw(const AttnParams& p, int nb, hipStream_t s) {
   // shapes, so there is no one-wave form.
   if constexpr (sizeof(T) == 4) {
     if (!dbg && (p.T <= 16 || (int64_t)nb * p.H * ((p.T + 63) / 64) < 128))
-      return launch_ks<T, DK, DK == 64 ? 4 : 2>(p, nb, s);  // (per-wave tiles: 34 / 64 KB of LDS)
+      return launch_ks<T, DK, 4>(p, nb, s);  // (per-wave tiles: 34 / 37 KB of LDS)
   }
   return dbg ? launch<T, DK, 4, true>(p, nb, s) : launch<T, DK, 4, false>(p, nb, s);
 }
@@ -1467,6 +1487,7 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
       if (head_dim == 64) hipLaunchKernelGGL(attn_chunk_f32_kernel<64>, grid, dim3(CfgS<64>::NT), 0, s, p);
       else if (head_dim == 128) hipLaunchKernelGGL(attn_chunk_f32_kernel<128>, grid, dim3(CfgS<128>::NT), 0, s, p);
       else return hipErrorInvalidValue;
+      count_form(kFormChunkF32);
       return hipGetLastError();
     }
     if (head_dim == 64) return dispatch_nw<float, 64>(p, nb, s);
@@ -1476,6 +1497,10 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nb, hipStr
     if (head_dim == 128) return dispatch_nw<bf16, 128>(p, nb, s);
   }
   return hipErrorInvalidValue;
+}
+
+int64_t attention_form_count(int form) {
+  return form >= 0 && form < kAttnForms ? g_form_launches[form].load(std::memory_order_relaxed) : -1;
 }
 
 hipError_t attention_with_gemm(DType dt, int head_dim, const AttnParams& p, int nb, const GemmParams& g, bool gquant,

@@ -98,6 +98,29 @@ int32_t prepare_ffn(mhsa_ffn* f) {
   return MHSA_OK;
 }
 
+// Linear i of the FeedForward as a plain GEMM C[rows, out] = A[rows, in] W^T
+// + b on activations of dtype `act` (prepare_ffn and the partial buffer
+// come first).
+mhsa::GemmParams ffn_gemm(mhsa_ffn* f, int i, DType act, const void* A, int rows, void* C) {
+  const DevLinear& d = act == f->dt ? f->dev[i] : f->dev32[i];
+  mhsa::GemmParams p;
+  p.A = A;
+  p.lda = ffn_in(f, i);
+  p.W = d.w;
+  p.sb = d.sb;
+  p.bias = d.bias;
+  p.C = C;
+  p.ldc = ffn_out(f, i);
+  p.M = rows;
+  p.N = ffn_out(f, i);
+  p.K = ffn_in(f, i);
+  p.seg_rows = rows;
+  p.ring_len = rows;
+  p.partial = static_cast<float*>(f->partial.p);
+  p.partial_elems = mhsa::kGemmPartialElems;
+  return p;
+}
+
 // FeedForward on activations of dtype `act`: the module dtype, or f32 on the
 // streaming path, where a bf16 module's ops meet f32 activations and MLX
 // promotes them (its parameters keep their bf16 values).
@@ -112,29 +135,14 @@ int32_t ffn_impl(mhsa_ffn* f, const void* x, int rows, void* out, const void* re
   HIPCHK(f->act.ensure(align_up((int64_t)rows * f->F * es, 256)));
   HIPCHK(f->partial.ensure((size_t)mhsa::kGemmPartialElems * 4));
   for (int i = 0; i < 2; ++i) {
-    const DevLinear& d = act == f->dt ? f->dev[i] : f->dev32[i];
-    mhsa::GemmParams p;
-    p.A = i == 0 ? x : f->act.p;
-    p.lda = ffn_in(f, i);
-    p.W = d.w;
-    p.sb = d.sb;
-    p.bias = d.bias;
-    p.C = i == 0 ? f->act.p : out;
-    p.ldc = ffn_out(f, i);
-    p.M = rows;
-    p.N = ffn_out(f, i);
-    p.K = ffn_in(f, i);
-    p.seg_rows = rows;
-    p.ring_len = rows;
-    p.partial = static_cast<float*>(f->partial.p);
-    p.partial_elems = mhsa::kGemmPartialElems;
+    mhsa::GemmParams p = ffn_gemm(f, i, act, i == 0 ? x : f->act.p, rows, i == 0 ? f->act.p : out);
     if (i == 0) p.act = mhsa::kActSilu;
     if (i == 1 && residual) {
       p.R = residual;
       p.ldr = f->D;
       p.res_scale = res_scale;
     }
-    HIPCHK(mhsa::gemm(act, d.quantized, p, s));
+    HIPCHK(mhsa::gemm(act, f->lin[i].quantized, p, s));
   }
   return MHSA_OK;
 }
@@ -244,6 +252,21 @@ int32_t mhsa_ffn_sublayer_forward_f32(mhsa_ffn* f, float* x, int32_t rows, const
                                       float eps, void* hs) {
   if (!f) return fail(MHSA_EINVAL, "null handle");
   return ffn_sublayer(f, x, rows, gamma, beta, eps, mhsa::kF32, static_cast<hipStream_t>(hs));
+}
+
+int32_t mhsa_ffn_debug_linear(mhsa_ffn* f, int32_t which, int32_t f32_act, const void* x, int32_t rows, void* out,
+                              void* hs) {
+  if (!f) return fail(MHSA_EINVAL, "null handle");
+  if (which < 0 || which > 1 || !x || !out || rows <= 0) return fail(MHSA_EINVAL, "bad arguments");
+  if (!aligned16(x) || !aligned16(out)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  if (int32_t rc = prepare_ffn(f)) return rc;
+  HIPCHK(f->partial.ensure((size_t)mhsa::kGemmPartialElems * 4));
+  const DType act = f32_act ? mhsa::kF32 : f->dt;
+  const mhsa::GemmParams p = ffn_gemm(f, which, act, x, rows, out);
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  HIPCHK(mhsa::gemm(act, f->lin[which].quantized, p, s));
+  HIPCHK(hipStreamSynchronize(s));
+  return MHSA_OK;
 }
 
 }  // extern "C"
@@ -565,6 +588,19 @@ int32_t mhsa_conv_profile_entry(mhsa_conv* m, int32_t idx, const char** name, do
 int32_t mhsa_conv_output_dtype(const mhsa_conv* m) {
   if (!m) return -1;
   return conv_dtype(m, m->dt, false) == mhsa::kF32 ? MHSA_F32 : MHSA_BF16;
+}
+
+int32_t mhsa_conv_debug_linear(mhsa_conv* m, int32_t which, int32_t f32_act, const void* x, int32_t rows, void* out,
+                               void* hs) {
+  if (int32_t rc = check_conv(m)) return rc;
+  if (which < 0 || which > 1 || !x || !out || rows <= 0) return fail(MHSA_EINVAL, "bad arguments");
+  if (!aligned16(x) || !aligned16(out)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  if (int32_t rc = prepare_conv(m)) return rc;
+  HIPCHK(m->partial.ensure((size_t)mhsa::kGemmPartialElems * 4));
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  if (int32_t rc = conv_pointwise(m, which, f32_act ? mhsa::kF32 : m->dt, x, rows, out, nullptr, s)) return rc;
+  HIPCHK(hipStreamSynchronize(s));
+  return MHSA_OK;
 }
 
 int32_t mhsa_conv_load_weights(mhsa_conv* m, const mhsa_tensor* tensors, int32_t n, const char* prefix, int32_t strict,

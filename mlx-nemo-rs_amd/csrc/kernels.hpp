@@ -142,6 +142,20 @@ hipError_t attention(DType dt, int head_dim, const AttnParams& p, int nbatch, hi
 // launched (the caller launches the two apart). Same results as apart.
 hipError_t attention_with_gemm(DType dt, int head_dim, const AttnParams& p, int nbatch, const GemmParams& g,
                                bool gquant, hipStream_t s);
+// Attention kernel forms, counted per launch (process-wide) so that tests
+// can tell which form a dispatch took.
+enum AttnForm {
+  kFormBf16Wave4 = 0,  // bf16, 4 waves of 32 queries, 64-key tiles
+  kFormBf16Wave8,      // bf16, 8 waves of 32 queries, 32-key tiles
+  kFormBf16Wave8Skip,  // the 8-wave form with per-wave tile skipping (windows)
+  kFormBf16Mixed,      // both bf16 forms in one launch
+  kFormBf16MixedGemm,  // both bf16 forms and a projection GEMM in one launch
+  kFormChunkF32,       // fp32 streaming chunk kernel
+  kFormGeneric,        // generic kernel (fp32, or bf16 without V^T)
+  kFormKeySplit,       // generic kernel, keys split over the waves
+  kAttnForms
+};
+int64_t attention_form_count(int form);
 // Position rows the bf16 kernel reads beyond the table on either side for
 // these items' key ranges (key_lo / key_hi / q_valid, context, T, center).
 int bf16_pos_pad(const AttnParams& p, int nbatch);

@@ -1418,6 +1418,38 @@ int32_t mhsa_debug_linear(mhsa_layer* L, int32_t which, const void* x, int32_t r
   return MHSA_OK;
 }
 
+int32_t mhsa_debug_attention_forms(int64_t* counts, int32_t n) {
+  if (!counts || n < 0) return fail(MHSA_EINVAL, "bad arguments");
+  for (int f = 0; f < n && f < mhsa::kAttnForms; ++f) counts[f] = mhsa::attention_form_count(f);
+  return mhsa::kAttnForms;
+}
+
+int32_t mhsa_debug_layer_norm(mhsa_layer* L, const void* x, int32_t rows, const float* gamma, const float* beta,
+                              float eps, void* out, void* hs) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (!x || !out || rows <= 0) return fail(MHSA_EINVAL, "bad arguments");
+  if (!aligned16(x) || !aligned16(out)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  const float* gd = nullptr;
+  const float* bd = nullptr;
+  if (int32_t rc = sublayer_norm(L, gamma, beta, rows, &gd, &bd)) return rc;
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  HIPCHK(mhsa::layer_norm(dtype_of(L), x, out, gd, bd, eps, rows, L->D, s));
+  HIPCHK(hipStreamSynchronize(s));
+  return MHSA_OK;
+}
+
+int32_t mhsa_debug_linear_f32(mhsa_layer* L, int32_t which, const float* x, int32_t rows, float* out, void* hs) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (which < 0 || which > 4 || !x || !out || rows < 0) return fail(MHSA_EINVAL, "bad arguments");
+  if (!aligned16(x) || !aligned16(out)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  int32_t rc = prepare_stream(L);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  if ((rc = run_gemm(L, mhsa::kF32, L->sdev[which], L->D, x, L->D, rows, out, L->D, nullptr, 0, s))) return rc;
+  HIPCHK(hipStreamSynchronize(s));
+  return MHSA_OK;
+}
+
 int32_t mhsa_debug_offline_mask(int32_t B, int32_t T, const mhsa_context* ctx, const int32_t* lens, uint8_t* out,
                                 void* hs) {
   if (B <= 0 || T <= 0 || !out) return fail(MHSA_EINVAL, "bad arguments");

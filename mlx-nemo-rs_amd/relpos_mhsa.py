@@ -45,7 +45,9 @@ EXPORTS = (
     "mhsa_conv_forward_with_cache", "mhsa_conv_sublayer_forward", "mhsa_conv_profile_enable",
     "mhsa_conv_profile_repeat", "mhsa_conv_profile_reset", "mhsa_conv_profile_count", "mhsa_conv_profile_entry",
     "mhsa_pos_encoding",
-    "mhsa_debug_dequantize", "mhsa_debug_linear", "mhsa_debug_offline_mask", "mhsa_debug_stream_mask", "mhsa_debug_rel_shift_index",
+    "mhsa_ffn_debug_linear", "mhsa_conv_debug_linear",
+    "mhsa_debug_dequantize", "mhsa_debug_linear", "mhsa_debug_linear_f32", "mhsa_debug_layer_norm",
+    "mhsa_debug_attention_forms", "mhsa_debug_offline_mask", "mhsa_debug_stream_mask", "mhsa_debug_rel_shift_index",
     "mhsa_debug_position_scores", "mhsa_debug_top_keys", "mhsa_profile_enable", "mhsa_profile_repeat",
     "mhsa_profile_reset", "mhsa_profile_count",
     "mhsa_profile_entry",
@@ -154,6 +156,11 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_pos_encoding": (I, [I, I, I, P(ctypes.c_float)]),
         "mhsa_debug_dequantize": (I, [VP, I, VP, VP]),
         "mhsa_debug_linear": (I, [VP, I, VP, I, VP, VP]),
+        "mhsa_debug_linear_f32": (I, [VP, I, VP, I, VP, VP]),
+        "mhsa_debug_attention_forms": (I, [P(ctypes.c_int64), I]),
+        "mhsa_debug_layer_norm": (I, [VP, VP, I, P(ctypes.c_float), P(ctypes.c_float), F, VP, VP]),
+        "mhsa_ffn_debug_linear": (I, [VP, I, I, VP, I, VP, VP]),
+        "mhsa_conv_debug_linear": (I, [VP, I, I, VP, I, VP, VP]),
         "mhsa_debug_offline_mask": (I, [I, I, P(Context), PI, VP, VP]),
         "mhsa_debug_stream_mask": (I, [I, I, I, P(StreamMask), VP, VP]),
         "mhsa_debug_rel_shift_index": (I, [I, I, VP, VP]),
@@ -424,6 +431,23 @@ class FeedForward:
                   None if b is None else b.ctypes.data_as(fp), float(eps), _stream_ptr()))
         return x
 
+    def debug_linear(self, which: int, x):
+        """linear1 (0) or linear2 (1) alone, without its epilogue, through the
+        module's GEMM kernels; an f32 x in a bf16 module runs the promoted form."""
+        import torch
+        promoted = self._check(x) if which == 0 else None
+        if which == 1:
+            want = _torch_dtype(self._dtype)
+            if not x.is_cuda or x.dtype not in (want, torch.float32) or x.shape[-1] != self.ff_dim:
+                raise MhsaError(MHSA_EINVAL, f"expected a {want} or float32 GPU tensor [..., {self.ff_dim}]")
+            promoted = x.dtype == torch.float32 and want != torch.float32
+        rows = x.numel() // x.shape[-1]
+        n = self.ff_dim if which == 0 else self.d_model
+        out = torch.empty((rows, n), dtype=x.dtype, device=x.device)
+        _check(self._lib.mhsa_ffn_debug_linear(self._h, which, 1 if promoted else 0, _dptr(x.contiguous()), rows,
+                                               _dptr(out), _stream_ptr()))
+        return out
+
 
 CONV_BATCH_NORM, CONV_LAYER_NORM = 0, 1
 
@@ -490,6 +514,20 @@ class ConvolutionModule(_Profiled):
         if (not cache.is_cuda or cache.dtype != torch.float32 or not cache.is_contiguous()
                 or tuple(cache.shape) != want or cache.device != x.device):
             raise MhsaError(MHSA_EINVAL, f"cache must be a contiguous float32 GPU tensor {list(want)} on x's device")
+
+    def debug_linear(self, which: int, x, f32_act: bool = False):
+        """pointwise_conv1 (0) or pointwise_conv2 (1) alone through the
+        module's GEMM kernels: x [rows, D] in the module dtype, or f32 with
+        `f32_act` (the promoted form)."""
+        import torch
+        want = torch.float32 if f32_act else _torch_dtype(self._dtype)
+        if not x.is_cuda or x.dtype != want or not x.is_contiguous() or x.shape[-1] != self.d_model:
+            raise MhsaError(MHSA_EINVAL, f"expected a contiguous {want} GPU tensor [..., {self.d_model}]")
+        rows = x.numel() // self.d_model
+        out = torch.empty((rows, (2 if which == 0 else 1) * self.d_model), dtype=want, device=x.device)
+        _check(self._lib.mhsa_conv_debug_linear(self._h, which, 1 if f32_act else 0, _dptr(x), rows, _dptr(out),
+                                                _stream_ptr()))
+        return out
 
     def forward(self, x, lengths=None):
         """forward (conformer.rs:2197-2291); lengths [B] (frames past them are padding)."""
@@ -743,6 +781,32 @@ class RelPositionMultiHeadAttention(_Profiled):
                                            _stream_ptr()))
         return out
 
+    def debug_linear_f32(self, name: str, x):
+        """The projection as the streaming path runs it: f32 x and output,
+        fp32 kernels (a bf16 layer's parameters keep their bf16 values)."""
+        import torch
+        if not x.is_cuda or x.dtype != torch.float32 or not x.is_contiguous():
+            raise MhsaError(MHSA_EINVAL, "expected a contiguous float32 GPU tensor")
+        rows = x.numel() // self.d_model
+        out = torch.empty_like(x)
+        _check(self._lib.mhsa_debug_linear_f32(self._h, LINEARS.index(name), _dptr(x), rows, _dptr(out),
+                                               _stream_ptr()))
+        return out
+
+    def debug_layer_norm(self, x, gamma=None, beta=None, eps=1e-5):
+        """The sublayer's LayerNorm alone, as the (stack) sublayer forward runs it."""
+        import torch
+        self._check_dev(x)
+        out = torch.empty_like(x)
+        g = None if gamma is None else _host_f32(gamma)
+        b = None if beta is None else _host_f32(beta)
+        fp = ctypes.POINTER(ctypes.c_float)
+        _check(self._lib.mhsa_debug_layer_norm(self._h, _dptr(x), x.numel() // self.d_model,
+                                               None if g is None else g.ctypes.data_as(fp),
+                                               None if b is None else b.ctypes.data_as(fp), float(eps), _dptr(out),
+                                               _stream_ptr()))
+        return out
+
     def debug_position_scores(self, x, pos_emb, with_inputs: bool = False):
         """Scaled rel-shifted position scores [B, H, T, T] (fp32); with
         `with_inputs`, also the projected q [B, T, D] and position rows the
@@ -929,6 +993,20 @@ class StreamingStack:
 # ---------------------------------------------------------------------------
 # debug exports
 # ---------------------------------------------------------------------------
+
+ATTENTION_FORMS = ("bf16_wave4", "bf16_wave8", "bf16_wave8_skip", "bf16_mixed", "bf16_mixed_gemm", "chunk_f32",
+                   "generic", "generic_key_split")
+
+
+def debug_attention_forms() -> Dict[str, int]:
+    """Launches of each attention kernel form since the library was loaded."""
+    lib = library()
+    arr = (ctypes.c_int64 * len(ATTENTION_FORMS))()
+    n = lib.mhsa_debug_attention_forms(arr, len(ATTENTION_FORMS))
+    if n < 0:
+        _check(n)
+    return {name: int(arr[i]) for i, name in enumerate(ATTENTION_FORMS)}
+
 
 def debug_offline_mask(batch: int, seq_len: int, context: Optional[AttentionContext],
                        key_lengths: Optional[Sequence[int]]):

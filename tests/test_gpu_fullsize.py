@@ -150,83 +150,176 @@ def _decided(logits, bound):
     return top, finite & (np.max(up, axis=-1) < lt - bt)
 
 
-def test_stack_u8_specified_distribution_top_keys():
-    """Two layers of the specified quantized stack at B=4, T=1500 with key
-    padding. Layer l's input is the GPU's output of layer l-1 on both sides,
-    and h = LayerNorm(x) is formed on the host, so both sides attend over the
-    same h.
+def _bf16_ulp(v):
+    """One bf16 ulp at |v| (2^(e-8) for |v| in [2^(e-1), 2^e))."""
+    _, e = np.frexp(np.abs(np.asarray(v, dtype=np.float64)))
+    return np.ldexp(1.0, e - 8)
 
-    Bounds, per (row, key j), in logit units:
+
+@pytest.mark.timeout(1200)
+def test_stack_u8_specified_distribution_through_the_stack():
+    """Four layers of the specified quantized stack at B=4, T=1500 with key
+    padding, run through mhsa_stack_sublayer_forward (the benchmarked path:
+    the next layer's position projection inside the attention launch, both
+    attention forms in one launch). Prefix stacks of 1..4 layers give every
+    layer's output; the 4-layer stack must equal the layer loop bit for bit.
+
+    Per layer l, on the GPU's output x of layer l-1, with h = the library's
+    LayerNorm of x (the same kernel the stack runs; within one bf16 ulp of
+    the oracle's):
+
+    Bounds per (row, key j), in logit units:
       eps_j  = 2^-22 s sum|q_u||k_j| + 2^-6 |t_j|: what separates the kernel's
                logit from the float64 logit of its own bf16 operands (fp32
                accumulation of q_u.k; the band's fp32 sum may round bd to the
                other bf16 neighbour, moving t = bf16(bd cast(s)) by <= 2 ulp);
       delta_j = |logit(GPU operands) - logit(oracle operands)|, exact, from
-               the projections each side computed (they differ by at most one
-               bf16 ulp per element, pinned elsewhere).
-    Every row whose winner is decided under eps (kernel check) or under
-    eps + delta (end to end) must have the same top key. The fraction of
-    decided rows and each layer's error are reported."""
+               the projections each side computed.
+    1. Every row whose winner is decided under eps (kernel check) or under
+       eps + delta (end to end) has the same top key (production kernel's
+       debug instantiation), in at least 65% of the rows (about 70% are).
+    2. Where the winner leads every other key by more than 40 beyond
+       eps + delta, both softmaxes put less than e^-40 on any other key, so the
+       head's attention output is that key's value row on both sides: the
+       GPU's (read through an identity linear_out) must then equal the
+       oracle's within 2^-8 relative (its bf16 probability over the fp32 sum
+       and the output rounding) + one bf16 ulp + 2^-14 sum|h||W_v| (the V
+       projections' fp32 accumulation, (K - 1) 2^-24 per term).
+    3. Rows where all 8 heads are so decided: the stack's sublayer output must
+       equal the oracle's within sum_k bound_k |W_out| (the bounds of 2.) +
+       2^-14 sum|ctx||W_out| plus one bf16 ulp of the projection and one of
+       the residual sum, element by element.
+    The undecided rows are where MLX internals (SDPA softmax precision, score
+    rounding, quantized_matmul accumulation) pick the key: parity unpinned.
+    """
     cfg = W.CONFIGS["xl_stack_u8"]
     D, H, T, B = cfg.d_model, cfg.n_heads, cfg.seq_len, cfg.batch
     dk = D // H
+    n_layers = 4
     rng = np.random.default_rng(cfg.seed)
-    layers_w = [W.make_layer_weights(rng, D, H, False, True) for _ in range(2)]
+    layers_w = [W.make_layer_weights(rng, D, H, False, True) for _ in range(n_layers)]
     lengths = [int(v) for v in rng.integers(1000, 1501, size=B)]
-    x = O.bf16_round(rng.standard_normal((B, T, D)))
+    x0 = O.bf16_round(rng.standard_normal((B, T, D)))
     pos = O.bf16_round(O.RelPositionalEncoding(D, 5000, True).get_encoding(T))
     s = O.f32_scale(dk)
     kmask = M.key_padding_mask(lengths, T)
+    layers = [gpu_layer(w, D, H, False, O.BF16) for w in layers_w]
+    # the production path: every layer's output from a prefix stack
+    outs = []
+    for n in range(1, n_layers + 1):
+        xd = dev(x0)
+        M.stack_sublayer_forward_(layers[:n], xd, dev(pos), None, kmask)
+        outs.append(host(xd))
+    xd = dev(x0)
+    for layer in layers:
+        layer.sublayer_forward_(xd, dev(pos), None, kmask)
+    assert np.array_equal(host(xd), outs[-1]), "stack differs from the layer loop"
+    x = x0
     for li, w in enumerate(layers_w):
         p = oracle_params(w, D, H)
-        layer = gpu_layer(w, D, H, False, O.BF16)
-        h = O.layer_norm(x, dtype=O.BF16)
-        top_g, val_g, q_g, k_g, P_g = layer.debug_top_keys(dev(h), dev(pos), None, kmask, with_inputs=True)
+        layer = layers[li]
+        h_d = layer.debug_layer_norm(dev(x))
+        h = host(h_d)
+        h_o = O.layer_norm(x, dtype=O.BF16)
+        # one bf16 ulp, plus the fp32 rounding of x - mean where they cancel
+        ln_ratio = float(np.max(np.abs(h - h_o) / (_bf16_ulp(h_o) + 2.0 ** -20)))
+        assert ln_ratio <= 1.0, f"layer {li}: LayerNorm off by {ln_ratio:.3f} x (one bf16 ulp + 2^-20)"
+        top_g, val_g, q_g, k_g, P_g = layer.debug_top_keys(h_d, dev(pos), None, kmask, with_inputs=True)
         top_g, val_g = top_g.cpu().numpy(), val_g.cpu().numpy()
         q_g, k_g, P_g = host(q_g), host(k_g), host(P_g)
-        n_rows = n_dec_k = n_dec_e = 0
+        # the attention output itself: the same weights with an identity linear_out
+        w_id = dict(w)
+        for key in ("linear_out.scales", "linear_out.biases"):
+            w_id.pop(key)
+        w_id["linear_out.weight"] = np.eye(D, dtype=np.float32)
+        ctx_g = host(gpu_layer(w_id, D, H, False, O.BF16).forward(h_d, dev(pos), None, kmask))
+        ctx_o = np.zeros((B, T, D))
+        ectx = np.zeros((B, T, D))
+        wv = p.linear_v.dense_weight(O.BF16)
+        onehot_rows = np.ones((B, T), dtype=bool)
+        n_rows = n_dec_k = n_dec_e = n_one = 0
+        worst_ctx = 0.0
         for b in range(B):
             km = O.key_padding_mask([lengths[b]], T)
             qg, kg, Pg = _heads(q_g[b], T, H, dk), _heads(k_g[b], T, H, dk), _heads(P_g, 2 * T - 1, H, dk)
             lg = O.attention_logits(p, qg, kg, Pg, None, km, O.BF16)[0]
-            q_o, k_o, _, pp_o = O.project(p, h[b:b + 1], pos, O.BF16)
+            q_o, k_o, v_o, pp_o = O.project(p, h[b:b + 1], pos, O.BF16)
             lo = O.attention_logits(p, q_o, k_o, pp_o, None, km, O.BF16)[0]
             qu_g, _ = O.biased_queries(p, qg, O.BF16)
             content = s * np.matmul(qu_g, np.swapaxes(kg, -1, -2))[0]
             absqk = s * np.matmul(np.abs(qu_g), np.abs(np.swapaxes(kg, -1, -2)))[0]
             eps = 2.0 ** -22 * absqk + 2.0 ** -6 * np.abs(np.where(np.isfinite(lg), lg - content, 0.0))
             del content, absqk
-            # kernel: GPU top key against the float64 logits of its own operands
+            # 1. kernel: GPU top key against the float64 logits of its own operands
             tk, dec_k = _decided(lg, eps)
             gt = top_g[b]
             assert np.all(gt[dec_k] == tk[dec_k]), \
                 f"layer {li} item {b}: {int(np.sum(gt[dec_k] != tk[dec_k]))} decided rows pick another key"
-            # its reported logit for that key
             lv = np.take_along_axis(lg, np.maximum(gt, 0)[..., None], -1)[..., 0]
             ev = np.take_along_axis(eps, np.maximum(gt, 0)[..., None], -1)[..., 0]
             vis = gt >= 0
-            assert np.all(np.abs(val_g[b][vis] - lv[vis]) <= ev[vis] + 2.0 ** -22 * np.abs(lv[vis]))
+            vr = np.abs(val_g[b][vis] - lv[vis]) / (ev[vis] + 2.0 ** -22 * np.abs(lv[vis]) + 1e-30)
+            assert vr.size == 0 or float(np.max(vr)) <= 1.0, \
+                f"layer {li} item {b}: reported top logit off by {float(np.max(vr)):.3f} x its bound"
             # end to end: against the oracle's own projections
             with np.errstate(invalid="ignore"):  # -inf - -inf where both hide a key
                 delta = np.abs(np.where(np.isfinite(lo), lg - lo, 0.0))
-            to, dec_e = _decided(lo, eps + delta)
+            bound = eps + delta
+            del lg, eps, delta
+            to, dec_e = _decided(lo, bound)
             assert np.all(gt[dec_e] == to[dec_e]), \
                 f"layer {li} item {b}: {int(np.sum(gt[dec_e] != to[dec_e]))} decided rows disagree with the oracle"
+            # 2. one-hot heads: the winner leads by > 40 beyond the bounds
+            lt = np.take_along_axis(lo, to[..., None], -1)[..., 0]
+            bt = np.take_along_axis(bound, to[..., None], -1)[..., 0]
+            up = lo + bound
+            np.put_along_axis(up, to[..., None], -np.inf, -1)
+            onehot = np.isfinite(lt) & (lt - bt - np.max(up, axis=-1) > 40.0)
+            del up, bound
+            c_o = O.bf16_round(np.matmul(O._softmax(lo), v_o[0]))  # [H, T, dk]
+            del lo
+            c_g = ctx_g[b].reshape(T, H, dk).transpose(1, 0, 2)
+            # a one-hot head's output is its winner's V row: the V projections
+            # of both sides differ by the fp32 accumulation (recursive-sum
+            # bound (K - 1) 2^-24 sum|h||w| <= 2^-14 sum|h||w|) and one bf16
+            # ulp; the GPU then scales it by its bf16 probability over the
+            # fp32 sum and rounds (2^-8 relative)
+            acc = np.matmul(np.abs(h[b]), np.abs(wv).T).reshape(T, H, dk).transpose(1, 0, 2)  # [H, T(key), dk]
+            acc_top = np.take_along_axis(acc, to[..., None], 1)  # [H, T(query), dk]
+            lim = 2.0 ** -8 * np.abs(c_o) + _bf16_ulp(c_o) + 2.0 ** -14 * acc_top
+            err = np.abs(c_g - c_o)
+            ratio = (err / lim)[onehot]
+            assert np.all(ratio <= 1.0), f"layer {li} item {b}: one-hot heads' attention output off by " \
+                                         f"{float(np.max(ratio)):.3f} x the bound"
+            if ratio.size:
+                worst_ctx = max(worst_ctx, float(np.max(ratio)))
+            ectx[b] = np.where(onehot[..., None], lim, 0.0).transpose(1, 0, 2).reshape(T, D)
+            ctx_o[b] = c_o.transpose(1, 0, 2).reshape(T, D)
+            onehot_rows[b] = onehot.all(axis=0)
             n_rows += gt.size
             n_dec_k += int(dec_k.sum())
             n_dec_e += int(dec_e.sum())
-            del lg, lo, eps, delta
-        # the layer's output (GPU sublayer) against the oracle sublayer on the same x
-        xd = dev(x)
-        layer.sublayer_forward_(xd, dev(pos), None, kmask)
-        out = host(xd)
-        ref = O.mhsa_sublayer(p, x, pos, None, O.key_padding_mask(lengths, T), dtype=O.BF16)
-        close = np.mean(np.abs(out - ref) <= 1e-2 * np.max(np.abs(ref)))
+            n_one += int(onehot.sum())
+        # 3. the stack's output on rows whose 8 heads are all one-hot
+        wout = p.linear_out.dense_weight(O.BF16)
+        a_o = p.linear_out.forward(ctx_o, O.BF16)
+        ref = O.bf16_round(x + a_o)
+        out = outs[li]
+        lim = (np.matmul(ectx, np.abs(wout).T) + 2.0 ** -14 * np.matmul(np.abs(ctx_o), np.abs(wout).T)
+               + _bf16_ulp(a_o) + _bf16_ulp(ref))
+        sel = onehot_rows
+        excess = float(np.max((np.abs(out - ref) / lim)[sel])) if sel.any() else 0.0
         print(f"specified u8 layer {li}: top key decided (kernel) in {n_dec_k / n_rows:.4f} of {n_rows} rows, "
-              f"end to end in {n_dec_e / n_rows:.4f}; all decided rows agree. Output: max|ref| "
-              f"{np.max(np.abs(ref)):.3e}, max error / max|ref| {rel_err(out, ref):.3e}, "
-              f"{close:.4f} of outputs within 1% of max|ref|")
-        assert n_dec_k > 0.5 * n_rows and n_dec_e > 0.1 * n_rows
+              f"end to end in {n_dec_e / n_rows:.4f}, one-hot in {n_one / n_rows:.4f} (attention output within "
+              f"{worst_ctx:.3f} of its bound); {int(sel.sum())} of {B * T} rows one-hot in every head, stack output "
+              f"there within {excess:.3f} of its bound. Whole output: max error / max|ref| "
+              f"{rel_err(out, ref):.3e}", flush=True)
+        # (measured on the four layers: decided 0.688-0.692, one-hot 0.637-0.644,
+        # 167-202 rows one-hot in all 8 heads)
+        assert n_dec_k > 0.65 * n_rows and n_dec_e > 0.65 * n_rows
+        assert n_one > 0.6 * n_rows
+        assert int(sel.sum()) >= 100
+        assert excess <= 1.0
         x = out
 
 

@@ -433,8 +433,12 @@ def test_forward_bf16_eight_wave_blocks(padded):
     pos = O.RelPositionalEncoding(D, 5000, True).get_encoding(T)
     ref = O.mhsa_forward(p, O.bf16_round(x), O.bf16_round(pos), None, mask, dtype=O.BF16)
     layer = gpu_layer(w, D, H, True, O.BF16)
+    before = M.debug_attention_forms()
     got = host(layer.forward(dev(x, O.BF16), dev(pos, O.BF16), None,
                              M.key_padding_mask(lengths, T) if padded else None))
+    after = M.debug_attention_forms()
+    ran = {k for k in after if after[k] > before[k]}
+    assert ran == ({"bf16_mixed"} if padded else {"bf16_wave8"}), ran
     err = abs_err(got, ref)
     print(f"bf16 eight-wave blocks (padded {padded}): max abs error {err:.3e} (max |ref| {np.max(np.abs(ref)):.2f})")
     assert err < BF16_TOL
@@ -686,6 +690,41 @@ def test_streaming_long_context_ring_wraps(B, C, T, ctx):
             fills[b] = O.next_fill(fills[b], T, 0, C)
         assert st.fill() == fills
     assert np.array_equal(st.read_cache().cpu().numpy(), np.concatenate(caches, 0).astype(np.float32))
+
+
+@pytest.mark.parametrize("keys", [97, 98, 112, 114, 129])
+@pytest.mark.parametrize("d,h", [(512, 4), (512, 8)], ids=["dk128", "dk64"])
+def test_streaming_key_split_partial_tiles(keys, d, h):
+    """14-frame chunks against caches of keys - 14 rows, key counts that end
+    inside a key tile (past the chunk kernel's 96 keys, so the generic fp32
+    kernel's key-split form runs, with its per-key mask on the last tile and on
+    the unfilled-cache offset). Per-session fills, with and without a chunked
+    context; one step against the oracle."""
+    rng = np.random.default_rng(keys + h)
+    T = 14
+    C = keys - T
+    B = 3
+    w = random_weights(rng, d, h, use_bias=True, scale=0.04)
+    p = oracle_params(w, d, h)
+    pos = O.RelPositionalEncoding(d, 5000, False).get_encoding(C + T)
+    layer = gpu_layer(w, d, h, True, O.F32)
+    for ctx in (None, ((C, T - 1), "chunked_limited")):
+        st = layer.stream(B, C, T)
+        cache = rng.standard_normal((B, C, d)).astype(np.float32)
+        fills = [C, C // 2, 3]
+        for b in range(B):
+            cache[b, :C - fills[b]] = 0.0
+        st.load_cache(dev(cache, O.F32), fills)
+        x = rng.standard_normal((B, T, d)).astype(np.float32)
+        before = M.debug_attention_forms()
+        mask = M.StreamingMask(*ctx, fills, [T] * B) if ctx else None
+        got = host(st.step(dev(x, O.F32), dev(pos, O.F32), mask))
+        after = M.debug_attention_forms()
+        assert {k for k in after if after[k] > before[k]} == {"generic_key_split"}
+        for b in range(B):
+            m = O.streaming_mask(ctx[0], ctx[1], C, fills[b], T, T) if ctx else None
+            ref, _ = O.mhsa_forward_with_cache(p, x[b:b + 1], pos, cache[b:b + 1].astype(np.float64), m)
+            assert row_rel_err(got[b:b + 1], ref) < F32_TOL, (ctx, b)
 
 
 def test_streaming_bf16_layer_xl_shape():
@@ -1066,8 +1105,15 @@ def test_stack_sublayer_forward_equals_layer_loop(kind):
     xb = xa.clone()
     for i, layer in enumerate(layers):
         layer.sublayer_forward_(xa, pd, None, kmask, gamma[i], beta[i])
+    before = M.debug_attention_forms()
     M.stack_sublayer_forward_(layers, xb, pd, None, kmask, gamma, beta)
     torch.cuda.synchronize()
+    after = M.debug_attention_forms()
+    ran = {k: after[k] - before[k] for k in after if after[k] > before[k]}
+    want = {"u8_8wave_fused": {"bf16_mixed_gemm": n - 1, "bf16_wave8": 1},
+            "u8_mixed_fused": {"bf16_mixed_gemm": n - 1, "bf16_mixed": 1},
+            "bf16_4wave": {"bf16_wave4": n}, "f32": {"generic_key_split": n}}[kind]
+    assert ran == want, ran
     assert torch.isfinite(xb.float()).all()
     assert torch.equal(xa, xb), f"{kind}: max difference {float((xa.float() - xb.float()).abs().max()):.3g}"
 
