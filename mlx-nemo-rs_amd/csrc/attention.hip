@@ -501,6 +501,39 @@ struct Cfg2 {
   static_assert(LDS <= 160 * 1024, "LDS");
 };
 
+// bf16(v) (round to nearest even) as an fp32 value from one packed
+// conversion: with 0 as its low input, the high half holds bf16(v) and the
+// word is that value in fp32. (Written as the instruction: from the
+// equivalent vector expression the compiler converts into the low half and
+// then moves it up, two instructions.) v comes from a vector ALU result.
+__device__ __forceinline__ float bf16_as_f32(float v) {
+  bf16x2 r;
+  asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(v));
+  return __builtin_bit_cast(float, r);
+}
+
+// max and sum of v over lanes l and l ^ 32, with the halves of the wave
+// exchanged by v_permlane32_swap (a vector ALU op; the equivalent shuffle is
+// an LDS permute with its own address arithmetic). After the swap a holds
+// v of lanes 0-31 in both halves and b v of lanes 32-63. (The compiler's
+// builtin for the instruction returned one value for both operands here,
+// so it is written as the instruction, with the wait states around it.)
+__device__ __forceinline__ void halves(float v, float& a, float& b) {
+  a = v;
+  b = v;
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  float a, b;
+  halves(v, a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  float a, b;
+  halves(v, a, b);
+  return a + b;
+}
+
 // Tile-local key held by LDS K row m (an involution on [0, 32) and [0, 64)).
 __device__ __forceinline__ constexpr int swap23(int m) { return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1); }
 
@@ -843,13 +876,11 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
         const bf16x8 q8 = __builtin_bit_cast(bf16x8, al);
 #pragma unroll
         for (int e = 0; e < 8; e += 2) {
-          // the position term as the reference materialises it:
-          // bf16(bf16(bd) * bf16(s)) (attention.rs:308-311), two per conversion
-          const floatx2 prod = {(float)q8[e] * p.scale_bd, (float)q8[e + 1] * p.scale_bd};
-          const bf16x2 tb2 = __builtin_convertvector(prod, bf16x2);
 #pragma unroll
           for (int k = 0; k < 2; ++k) {
-            const float tb = (float)tb2[k];
+            // the position term as the reference materialises it:
+            // bf16(bf16(bd) * bf16(s)) (attention.rs:308-311)
+            const float tb = bf16_as_f32((float)q8[e + k] * p.scale_bd);
             if (DEBUG && p.dbg_bd) {
               const int j = j0 + 32 * u + 16 * g + 8 * hh + e + k;
               if (qi < p.T && j < p.L) p.dbg_bd[(((int64_t)b * p.H + h) * p.T + qi) * p.L + j] = tb;
@@ -887,7 +918,7 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
     for (int u = 0; u < NU; ++u)
 #pragma unroll
       for (int r = 0; r < 16; ++r) tmax = fmaxf(tmax, s[u][r]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+    tmax = max_xor32(tmax);
     if (m_ref == -INFINITY) m_ref = tmax;
     if (__any(tmax > m_ref + lim)) {
       // (o holds only this lane's query: its column of O^T)
@@ -938,7 +969,7 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
     __syncthreads();  // waits for this wave's loads of the next tile first
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  const float l_tot = sum_xor32(l_run);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (DEBUG && p.dbg_top) {
     // merge with the lane holding the other 8-key halves of this query
