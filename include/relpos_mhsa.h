@@ -406,6 +406,75 @@ int32_t mhsa_conv_profile_count(mhsa_conv* conv);
 int32_t mhsa_conv_profile_entry(mhsa_conv* conv, int32_t idx, const char** name, double* total_ms,
                                 int32_t* launches);
 
+/* ---- the whole Conformer block and the encoder's layer loops ---------------- */
+
+/* ConformerBlock (conformer.rs:1613-2028): the half-step FeedForward, the
+ * MHSA sublayer, the convolution sublayer, the second half-step FeedForward
+ * and norm_out, each sublayer pre-LayerNorm + residual. The block owns one
+ * handle of each module (mhsa_block_attention etc. give them out for
+ * profiling; their lifetime is the block's). */
+typedef struct mhsa_block mhsa_block;
+/* ConformerBlock::new (conformer.rs:1662-1690): two FeedForward(d_model,
+ * ff_dim), RelPositionMultiHeadAttention(d_model, n_heads, use_bias),
+ * ConvolutionModule(d_model, conv_kernel, conv_norm, causal, use_bias) and
+ * five LayerNorms at their init (weight 1, bias 0). */
+int32_t mhsa_block_create(int32_t d_model, int32_t n_heads, int32_t ff_dim, int32_t conv_kernel, int32_t conv_norm,
+                          int32_t causal, int32_t use_bias, mhsa_block** out);
+void mhsa_block_destroy(mhsa_block* block);
+/* set_dtype (conformer.rs:1643-1660): every module and norm. */
+int32_t mhsa_block_set_dtype(mhsa_block* block, int32_t dtype);
+/* load_weights (conformer.rs:1977-2028): {prefix}.feed_forward1,
+ * .self_attn, .conv, .feed_forward2 as the modules' loaders take them, and
+ * the optional LayerNorm tensors {prefix}.norm_feed_forward1, .norm_self_att,
+ * .norm_conv, .norm_feed_forward2, .norm_out (.weight, .bias)
+ * (prefix e.g. "encoder.layers.0"). */
+int32_t mhsa_block_load_weights(mhsa_block* block, const mhsa_tensor* tensors, int32_t n_tensors, const char* prefix,
+                                int32_t strict, int32_t quant_bits, int32_t quant_group);
+mhsa_layer* mhsa_block_attention(mhsa_block* block);
+mhsa_ffn* mhsa_block_feed_forward(mhsa_block* block, int32_t which /* 1 or 2 */);
+mhsa_conv* mhsa_block_conv(mhsa_block* block);
+/* forward (conformer.rs:1693-1875) in place: x_inout [batch, seq_len,
+ * d_model] device in the block dtype; pos_emb, pos_len, ctx as for
+ * mhsa_forward; lengths [batch] host or NULL (PaddingMask,
+ * conformer.rs:1594-1615: keys past a length hidden from the attention,
+ * clamped to >= 1; frames past it zeroed in the conv). MHSA_ENOTSUP for a
+ * causal conv in a bf16 block (its f32 result promotes the rest of the
+ * block). */
+int32_t mhsa_block_forward(mhsa_block* block, void* x_inout, int32_t batch, int32_t seq_len, const void* pos_emb,
+                           int32_t pos_len, const mhsa_context* ctx, const int32_t* lengths, void* hip_stream);
+/* The offline encoder's layer loop (conformer.rs:542-550): every block in
+ * order on x_inout with one pos_emb, context and padding. */
+int32_t mhsa_encoder_forward(mhsa_block* const* blocks, int32_t n_layers, void* x_inout, int32_t batch,
+                             int32_t seq_len, const void* pos_emb, int32_t pos_len, const mhsa_context* ctx,
+                             const int32_t* lengths, void* hip_stream);
+
+/* The streaming encoder's per-chunk loop over n_layers blocks
+ * (ConformerEncoder::forward_streaming, conformer.rs:840-1047, with
+ * ConformerBlock::forward_with_cache, conformer.rs:1893-1971): per layer an
+ * HBM ring of cache_size attention frames and the conv cache [batch,
+ * d_model, K - 1] (cache_last_time, zeros at creation), one fill per
+ * session. Blocks need causal convs of one kernel size >= 2; they are not
+ * owned and must not serve another encoder at the same time. */
+typedef struct mhsa_encoder mhsa_encoder;
+int32_t mhsa_encoder_create(mhsa_block* const* blocks, int32_t n_layers, int32_t batch, int32_t cache_size,
+                            int32_t chunk_len, mhsa_encoder** out);
+void mhsa_encoder_destroy(mhsa_encoder* enc);
+/* channel [n_layers, batch, cache_size, d_model] and time [n_layers, batch,
+ * d_model, K - 1] device fp32 (time NULL = zeros); filled_host [batch] (NULL
+ * = 0). */
+int32_t mhsa_encoder_load_cache(mhsa_encoder* enc, const float* channel_cache, const float* time_cache,
+                                const int32_t* filled_host, void* hip_stream);
+int32_t mhsa_encoder_read_cache(const mhsa_encoder* enc, float* channel_cache_out, float* time_cache_out,
+                                void* hip_stream);
+int32_t mhsa_encoder_fill(const mhsa_encoder* enc, int32_t* filled_out_host);
+/* One chunk through every block: x_inout [batch, chunk_len, d_model] device
+ * fp32 (the streaming activations stay f32, conformer.rs:845-849), updated in
+ * place; pos_emb [2*(cache_size+chunk_len)-1, d_model] device in the block
+ * dtype; mask as for mhsa_stack_step; valid_host [batch] or NULL: the conv's
+ * pad_mask (frames past valid zeroed after the GLU, conformer.rs:929-941). */
+int32_t mhsa_encoder_step(mhsa_encoder* enc, float* x_inout, const void* pos_emb, int32_t pos_len,
+                          const mhsa_stream_mask* mask, const int32_t* valid_host, void* hip_stream);
+
 /* ---- encoder-level streaming ---------------------------------------------- */
 
 /* The per-chunk layer loop of ConformerEncoder::forward_streaming

@@ -26,7 +26,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libmhsa_hip.so")
-SOURCES = ["gemm.hip", "attention.hip", "misc.hip", "mhsa_api.hip", "block_api.hip", "conv.hip", "checkpoint.cpp"]
+SOURCES = ["gemm.hip", "attention.hip", "misc.hip", "mhsa_api.hip", "block_api.hip", "encoder_api.hip", "conv.hip",
+           "checkpoint.cpp"]
 ARCH = "gfx950"
 
 

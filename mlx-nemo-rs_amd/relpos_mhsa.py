@@ -45,6 +45,10 @@ EXPORTS = (
     "mhsa_conv_forward_with_cache", "mhsa_conv_sublayer_forward", "mhsa_conv_profile_enable",
     "mhsa_conv_profile_repeat", "mhsa_conv_profile_reset", "mhsa_conv_profile_count", "mhsa_conv_profile_entry",
     "mhsa_pos_encoding",
+    "mhsa_block_create", "mhsa_block_destroy", "mhsa_block_set_dtype", "mhsa_block_load_weights",
+    "mhsa_block_attention", "mhsa_block_feed_forward", "mhsa_block_conv", "mhsa_block_forward",
+    "mhsa_encoder_forward", "mhsa_encoder_create", "mhsa_encoder_destroy", "mhsa_encoder_load_cache",
+    "mhsa_encoder_read_cache", "mhsa_encoder_fill", "mhsa_encoder_step",
     "mhsa_ffn_debug_linear", "mhsa_conv_debug_linear",
     "mhsa_debug_dequantize", "mhsa_debug_linear", "mhsa_debug_linear_f32", "mhsa_debug_layer_norm",
     "mhsa_debug_attention_forms", "mhsa_debug_offline_mask", "mhsa_debug_stream_mask", "mhsa_debug_rel_shift_index",
@@ -154,6 +158,21 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_conv_profile_count": (I, [VP]),
         "mhsa_conv_profile_entry": (I, [VP, I, P(ctypes.c_char_p), P(ctypes.c_double), PI]),
         "mhsa_pos_encoding": (I, [I, I, I, P(ctypes.c_float)]),
+        "mhsa_block_create": (I, [I, I, I, I, I, I, I, P(VP)]),
+        "mhsa_block_destroy": (None, [VP]),
+        "mhsa_block_set_dtype": (I, [VP, I]),
+        "mhsa_block_load_weights": (I, [VP, P(Tensor), I, ctypes.c_char_p, I, I, I]),
+        "mhsa_block_attention": (VP, [VP]),
+        "mhsa_block_feed_forward": (VP, [VP, I]),
+        "mhsa_block_conv": (VP, [VP]),
+        "mhsa_block_forward": (I, [VP, VP, I, I, VP, I, P(Context), PI, VP]),
+        "mhsa_encoder_forward": (I, [P(VP), I, VP, I, I, VP, I, P(Context), PI, VP]),
+        "mhsa_encoder_create": (I, [P(VP), I, I, I, I, P(VP)]),
+        "mhsa_encoder_destroy": (None, [VP]),
+        "mhsa_encoder_load_cache": (I, [VP, VP, VP, PI, VP]),
+        "mhsa_encoder_read_cache": (I, [VP, VP, VP, VP]),
+        "mhsa_encoder_fill": (I, [VP, PI]),
+        "mhsa_encoder_step": (I, [VP, VP, VP, I, P(StreamMask), PI, VP]),
         "mhsa_debug_dequantize": (I, [VP, I, VP, VP]),
         "mhsa_debug_linear": (I, [VP, I, VP, I, VP, VP]),
         "mhsa_debug_linear_f32": (I, [VP, I, VP, I, VP, VP]),
@@ -1032,3 +1051,125 @@ def debug_rel_shift_index(rows: int, total_len: int):
     out = torch.empty((rows, total_len), dtype=torch.int32, device="cuda")
     _check(library().mhsa_debug_rel_shift_index(rows, total_len, _dptr(out), _stream_ptr()))
     return out
+
+
+class ConformerBlock:
+    """ConformerBlock (conformer.rs:1613-2028) backed by the HIP library:
+    FF1 half-step, MHSA, convolution, FF2 half-step, norm_out."""
+
+    def __init__(self, d_model: int, n_heads: int, ff_dim: int, conv_kernel: int, conv_norm: str = "batch_norm",
+                 causal: bool = False, use_bias: bool = True):
+        lib = library()
+        h = ctypes.c_void_p()
+        norm = CONV_BATCH_NORM if conv_norm == "batch_norm" else CONV_LAYER_NORM
+        _check(lib.mhsa_block_create(d_model, n_heads, ff_dim, conv_kernel, norm, 1 if causal else 0,
+                                     1 if use_bias else 0, ctypes.byref(h)))
+        self._h, self._lib = h, lib
+        self.d_model, self.n_heads, self.ff_dim, self.conv_kernel = d_model, n_heads, ff_dim, conv_kernel
+        self.causal = causal
+        self._dtype = F32
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            self._lib.mhsa_block_destroy(h)
+            self._h = None
+
+    def set_dtype(self, dtype) -> None:
+        self._dtype = _dtype_code(dtype)
+        _check(self._lib.mhsa_block_set_dtype(self._h, self._dtype))
+
+    @property
+    def dtype(self):
+        return _torch_dtype(self._dtype)
+
+    def load_weights(self, weights: Dict[str, np.ndarray], prefix: str,
+                     quant: Optional[QuantizationConfig] = None, strict: bool = True) -> None:
+        arr_t, n, keep = _tensor_list(weights)
+        bits, group = (quant.bits, quant.group_size) if quant else (0, 0)
+        _check(self._lib.mhsa_block_load_weights(self._h, arr_t, n, prefix.encode(), 1 if strict else 0, bits, group))
+
+    def forward_(self, x, pos_emb, context: Optional[AttentionContext] = None, lengths: Optional[Sequence[int]] = None):
+        """In place x <- block(x) (conformer.rs:1693-1875); lengths [B] build the
+        padding masks (PaddingMask, conformer.rs:1594-1615)."""
+        b, t, d = x.shape
+        pe = pos_emb.reshape(-1, d)
+        want = _torch_dtype(self._dtype)
+        for a in (x, pe):
+            if not a.is_cuda or a.dtype != want or not a.is_contiguous():
+                raise MhsaError(MHSA_EINVAL, f"expected contiguous {want} GPU tensors")
+        ctx = context.c() if context is not None else None
+        if lengths is not None and len(lengths) != b:
+            raise MhsaError(MHSA_EINVAL, f"lengths must have {b} entries")
+        _check(self._lib.mhsa_block_forward(self._h, _dptr(x), b, t, _dptr(pe), pe.shape[0],
+                                            ctypes.byref(ctx) if ctx is not None else None, _int_array(lengths),
+                                            _stream_ptr()))
+        return x
+
+
+def encoder_forward_(blocks: Sequence[ConformerBlock], x, pos_emb, context=None, lengths=None):
+    """The offline encoder's layer loop over blocks (conformer.rs:542-550), in place."""
+    blocks = list(blocks)
+    if not blocks:
+        raise MhsaError(MHSA_EINVAL, "the encoder needs at least one block")
+    b, t, d = x.shape
+    pe = pos_emb.reshape(-1, d)
+    ctx = context.c() if context is not None else None
+    arr = (ctypes.c_void_p * len(blocks))(*[k._h.value for k in blocks])
+    _check(blocks[0]._lib.mhsa_encoder_forward(arr, len(blocks), _dptr(x), b, t, _dptr(pe), pe.shape[0],
+                                               ctypes.byref(ctx) if ctx is not None else None,
+                                               _int_array(lengths), _stream_ptr()))
+    return x
+
+
+class StreamingEncoder:
+    """The streaming encoder's per-chunk loop over blocks with causal convs
+    (ConformerEncoder::forward_streaming, conformer.rs:840-1047): per layer an
+    attention ring and the conv cache; one fill per session."""
+
+    def __init__(self, blocks: Sequence[ConformerBlock], batch: int, cache_size: int, chunk_len: int):
+        self.blocks = list(blocks)
+        lib = self.blocks[0]._lib
+        arr = (ctypes.c_void_p * len(self.blocks))(*[k._h.value for k in self.blocks])
+        h = ctypes.c_void_p()
+        _check(lib.mhsa_encoder_create(arr, len(self.blocks), batch, cache_size, chunk_len, ctypes.byref(h)))
+        self._h, self._lib = h, lib
+        self.batch, self.cache_size, self.chunk_len = batch, cache_size, chunk_len
+        self.d_model = self.blocks[0].d_model
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h:
+            self._lib.mhsa_encoder_destroy(h)
+            self._h = None
+
+    def load_cache(self, channel, time=None, filled: Optional[Sequence[int]] = None) -> None:
+        _check(self._lib.mhsa_encoder_load_cache(self._h, _dptr(channel), _dptr(time) if time is not None else None,
+                                                 _int_array(filled), _stream_ptr()))
+
+    def read_cache(self):
+        import torch
+        n = len(self.blocks)
+        ch = torch.empty((n, self.batch, self.cache_size, self.d_model), dtype=torch.float32, device="cuda")
+        tm = torch.empty((n, self.batch, self.d_model, self.blocks[0].conv_kernel - 1), dtype=torch.float32,
+                         device="cuda")
+        _check(self._lib.mhsa_encoder_read_cache(self._h, _dptr(ch), _dptr(tm), _stream_ptr()))
+        return ch, tm
+
+    def fill(self):
+        arr = (ctypes.c_int32 * self.batch)()
+        _check(self._lib.mhsa_encoder_fill(self._h, arr))
+        return list(arr)
+
+    def step_(self, x, pos_emb, mask: Optional[StreamingMask] = None, valid: Optional[Sequence[int]] = None):
+        """One chunk through every block, in place (x fp32 [B, T, D])."""
+        import torch
+        d = self.d_model
+        if not x.is_cuda or x.dtype != torch.float32 or not x.is_contiguous():
+            raise MhsaError(MHSA_EINVAL, "streaming activations are contiguous float32 GPU tensors")
+        pe = pos_emb.reshape(-1, d)
+        m, keep = (mask.c() if mask is not None else (None, []))
+        _check(self._lib.mhsa_encoder_step(self._h, _dptr(x), _dptr(pe), pe.shape[0],
+                                           ctypes.byref(m) if m is not None else None, _int_array(valid),
+                                           _stream_ptr()))
+        return x

@@ -811,6 +811,76 @@ def conv_sublayer(p: ConvModuleParams, x, gamma=None, beta=None, dtype: str = F3
 
 
 # ---------------------------------------------------------------------------
+# ConformerBlock (conformer.rs:1613-2028): FF1 half-step, MHSA, conv, FF2
+# half-step, norm_out
+# ---------------------------------------------------------------------------
+
+@dataclass
+class ConformerBlockParams:
+    """One ConformerBlock (conformer.rs:1613-1641, new 1662-1690): each norm a
+    (weight, bias) pair, None meaning the identity init (load_layer_norm
+    leaves a missing tensor at its init, loading.rs:203-214)."""
+
+    ff1: FeedForwardParams
+    ff1_norm: Tuple
+    attn: MhsaParams
+    attn_norm: Tuple
+    conv: ConvModuleParams
+    conv_norm: Tuple
+    ff2: FeedForwardParams
+    ff2_norm: Tuple
+    out_norm: Tuple
+
+
+def conformer_block(p: ConformerBlockParams, x, pos_emb, context: Optional[AttentionContext] = None,
+                    lengths=None, dtype: str = F32):
+    """ConformerBlock::forward (conformer.rs:1693-1875) on x [B, T, D] in
+    `dtype`: x + 0.5 FF1(LN(x)) (1703-1729), x + MHSA(LN(x)) with the key
+    padding mask of `lengths` (1747-1780), x + conv(LN(x)) with frames past
+    `lengths` zeroed (1790-1814), x + 0.5 FF2(LN(x)) (1827-1851), then
+    norm_out (1862). `lengths` builds PaddingMask (conformer.rs:1594-1615):
+    None when no frame is padding. A causal conv in a bf16 block promotes
+    the rest of the block to f32 (the conv's f32 padding), as MLX does."""
+    x = np.asarray(x, dtype=np.float64)
+    t_ = x.shape[1]
+    if lengths is not None and all(int(v) >= t_ for v in lengths):
+        lengths = None  # PaddingMask::new gives None
+    key_mask = key_padding_mask(lengths, t_) if lengths is not None else None
+    x = feed_forward_sublayer(p.ff1, x, *p.ff1_norm, dtype=dtype)
+    x = mhsa_sublayer(p.attn, x, pos_emb, context, key_mask, *p.attn_norm, dtype=dtype)
+    x, _ = conv_sublayer(p.conv, x, *p.conv_norm, dtype=dtype, lengths=lengths)
+    act = F32 if p.conv.causal else dtype
+    x = feed_forward_sublayer(p.ff2, x, *p.ff2_norm, dtype=dtype, act=act)
+    g, b = p.out_norm
+    return layer_norm(x, None if g is None else to_dtype(g, dtype), None if b is None else to_dtype(b, dtype),
+                      1e-5, act)
+
+
+def conformer_block_with_cache(p: ConformerBlockParams, x, pos_emb, att_cache, conv_cache, att_mask=None,
+                               pad_lengths=None, dtype: str = F32):
+    """ConformerBlock::forward_with_cache (conformer.rs:1893-1971) on the
+    streaming path's f32 activations x [B, T, D]: every op that meets them is
+    f32 (the parameters hold their `dtype` values). The attention caches
+    its LayerNorm output h (attention.rs:579-586); `att_mask` as
+    mhsa_forward_with_cache takes it; `pad_lengths` [B] zero the conv's
+    frames past them (pad_mask, conformer.rs:929-941). Returns (x,
+    new_att_cache, new_conv_cache)."""
+    x = np.asarray(x, dtype=np.float64)
+    x = feed_forward_sublayer(p.ff1, x, *p.ff1_norm, dtype=dtype, act=F32)  # 1914-1919
+    g, b = p.attn_norm
+    h = layer_norm(x, None if g is None else to_dtype(g, dtype), None if b is None else to_dtype(b, dtype), 1e-5, F32)
+    a, new_att = mhsa_forward_with_cache(p.attn, h, pos_emb, att_cache, att_mask, dtype)  # 1924-1933
+    x = x + a
+    x, new_conv = conv_sublayer(p.conv, x, *p.conv_norm, dtype=dtype, act=F32, lengths=pad_lengths,
+                                cache=conv_cache)  # 1936-1941
+    x = feed_forward_sublayer(p.ff2, x, *p.ff2_norm, dtype=dtype, act=F32)  # 1950-1955
+    g, b = p.out_norm
+    x = layer_norm(x, None if g is None else to_dtype(g, dtype), None if b is None else to_dtype(b, dtype), 1e-5,
+                   F32)  # 1960
+    return x, new_att, new_conv
+
+
+# ---------------------------------------------------------------------------
 # Index maps exported for bit-exact checks
 # ---------------------------------------------------------------------------
 

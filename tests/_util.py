@@ -100,3 +100,77 @@ def conv_oracle(w, norm="batch_norm", causal=False, prefix="conv") -> O.ConvModu
     return O.ConvModuleParams(lin[0], np.asarray(g("depthwise_conv.weight"), np.float64), g("depthwise_conv.bias"),
                               lin[1], norm, g("batch_norm.weight"), g("batch_norm.bias"),
                               g("batch_norm.running_mean"), g("batch_norm.running_var"), causal)
+
+
+def ffn_weights(rng, d, f, quant, prefix="ff", use_bias=True):
+    """FeedForward linear1 [f, d], linear2 [d, f] keyed like a checkpoint:
+    dense Xavier, or affine u8 with zero-mean weights (scales U(1e-4, 1e-3))
+    so activations stay O(1); biases N(0, 0.1)."""
+    import workloads as W
+    w = {}
+    for name, (o, i) in (("linear1", (f, d)), ("linear2", (d, f))):
+        if quant:
+            codes = rng.integers(0, 256, size=(o, i))
+            sc = rng.uniform(1e-4, 1e-3, size=(o, i // 64)).astype(np.float16)
+            w[f"{prefix}.{name}.weight"] = W.pack_u8(codes)
+            w[f"{prefix}.{name}.scales"] = sc
+            w[f"{prefix}.{name}.biases"] = (-128.0 * sc.astype(np.float64)
+                                            + rng.normal(0, 1e-3, sc.shape)).astype(np.float16)
+            if use_bias:
+                w[f"{prefix}.{name}.bias"] = rng.normal(0, 0.1, o).astype(np.float16)
+        else:
+            w[f"{prefix}.{name}.weight"] = W.xavier(rng, o, i)
+            if use_bias:
+                w[f"{prefix}.{name}.bias"] = rng.normal(0, 0.1, o).astype(np.float32)
+    return w
+
+
+def ffn_oracle(w, prefix="ff"):
+    lin = []
+    for name in ("linear1", "linear2"):
+        k = f"{prefix}.{name}"
+        if f"{k}.scales" in w:
+            lin.append(O.LinearLayer(w[f"{k}.weight"], w.get(f"{k}.bias"), w[f"{k}.scales"], w[f"{k}.biases"]))
+        else:
+            lin.append(O.LinearLayer(np.asarray(w[f"{k}.weight"], np.float64), w.get(f"{k}.bias")))
+    return O.FeedForwardParams(*lin)
+
+
+BLOCK_NORMS = ("norm_feed_forward1", "norm_self_att", "norm_conv", "norm_feed_forward2", "norm_out")
+
+
+def block_weights(rng, d, h, f, k, norm="batch_norm", quant=False, prefix="blk"):
+    """One ConformerBlock's tensors keyed like a checkpoint
+    (conformer.rs:1977-2028): feed_forward1/2, self_attn (quantized ones
+    zero-mean, so the attention stays well conditioned), conv and the five
+    LayerNorms (weight 1 + N(0, 0.1), bias N(0, 0.1))."""
+    import workloads as W
+    w = {}
+    w.update(ffn_weights(rng, d, f, quant, f"{prefix}.feed_forward1"))
+    att = W.make_layer_weights(rng, d, h, True, quant)
+    if quant:  # zero-mean codes: scales U(1e-4, 1e-3), biases -128 s + N(0, 1e-3)
+        for name in LINEARS:
+            sc = rng.uniform(1e-4, 1e-3, size=att[f"{name}.scales"].shape).astype(np.float16)
+            att[f"{name}.scales"] = sc
+            att[f"{name}.biases"] = (-128.0 * sc.astype(np.float64) + rng.normal(0, 1e-3, sc.shape)).astype(np.float16)
+    else:
+        for name in LINEARS[:4]:
+            att[f"{name}.bias"] = (rng.standard_normal(d) * 0.1).astype(np.float32)
+    w.update(W.prefixed(att, f"{prefix}.self_attn"))
+    w.update(conv_weights(rng, d, k, norm, quant, True, f"{prefix}.conv"))
+    w.update(ffn_weights(rng, d, f, quant, f"{prefix}.feed_forward2"))
+    for n in BLOCK_NORMS:
+        w[f"{prefix}.{n}.weight"] = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+        w[f"{prefix}.{n}.bias"] = (0.1 * rng.standard_normal(d)).astype(np.float32)
+    return w
+
+
+def block_oracle(w, d, h, norm="batch_norm", causal=False, prefix="blk") -> O.ConformerBlockParams:
+    """Oracle view of `block_weights` tensors."""
+    att = {k[len(prefix) + len(".self_attn."):]: v for k, v in w.items() if k.startswith(f"{prefix}.self_attn.")}
+    nrm = lambda n: (np.asarray(w[f"{prefix}.{n}.weight"], np.float64), np.asarray(w[f"{prefix}.{n}.bias"], np.float64))
+    return O.ConformerBlockParams(ffn_oracle(w, f"{prefix}.feed_forward1"), nrm(BLOCK_NORMS[0]), oracle_params(att, d, h),
+                                  nrm(BLOCK_NORMS[1]), conv_oracle(w, norm, causal, f"{prefix}.conv"),
+                                  nrm(BLOCK_NORMS[2]), ffn_oracle(w, f"{prefix}.feed_forward2"), nrm(BLOCK_NORMS[3]),
+                                  nrm(BLOCK_NORMS[4]))
+

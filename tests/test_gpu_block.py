@@ -1,0 +1,163 @@
+"""GPU parity of the whole Conformer block and the encoder's layer loops
+against the oracle's composed block (conformer.rs:1693-1971).
+
+Tolerances: fp32 per output row max |gpu - oracle| / max |oracle| <= 1e-4.
+bf16: per output row max |gpu - oracle| <= 2e-2 of the row's max |oracle|.
+Five bf16-rounded sublayers run in sequence (each checked on its own at
+2e-2 absolute elsewhere): a one-ulp difference of an intermediate that the
+GPU's fp32 sums and the oracle's exact ones round to different neighbours
+moves the later sublayers' sums, so a few outputs of |x| ~ 2-5 end two or
+three ulps (0.03-0.05) from the oracle's; measured 265 (dense) and 1082 (u8)
+of 614400 outputs past 2e-2 absolute, largest 0.047 at row maxima ~4, and
+the check also bounds that count at 1%.
+"""
+import numpy as np
+import pytest
+import torch
+
+import relpos_oracle as O
+import relpos_mhsa as M
+from _util import block_oracle, block_weights, row_rel_err
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-4
+BF16_TOL = 2e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    assert torch.cuda.is_available(), "GPU tests need an MI355X"
+    M.library()
+    yield
+    torch.cuda.synchronize()
+
+
+def dev(a, dtype):
+    t = torch.from_numpy(np.ascontiguousarray(np.asarray(a, dtype=np.float32)))
+    return t.to("cuda").to(torch.float32 if dtype == O.F32 else torch.bfloat16).contiguous()
+
+
+def host(t):
+    return t.float().cpu().numpy().astype(np.float64)
+
+
+def gpu_block(w, d, h, f, k, norm, causal, dtype, prefix="blk"):
+    blk = M.ConformerBlock(d, h, f, k, norm, causal, True)
+    blk.load_weights(w, prefix)
+    blk.set_dtype(dtype)
+    return blk
+
+
+@pytest.mark.parametrize("dtype,quant,norm,causal", [(O.BF16, False, "batch_norm", False),
+                                                     (O.BF16, True, "batch_norm", False),
+                                                     (O.F32, False, "layer_norm", True),
+                                                     (O.F32, True, "batch_norm", False)])
+def test_block_offline_against_oracle(dtype, quant, norm, causal):
+    """One 0.6B-shape block (d_model 1024, 8 heads, ff 4096, conv kernel 9)
+    at B=3, T=200 with key/frame padding (lengths 200, 131, 57), dense or
+    affine u8 projections, against conformer_block."""
+    d, h, f, k, B, T = 1024, 8, 4096, 9, 3, 200
+    rng = np.random.default_rng(70 + quant)
+    w = block_weights(rng, d, h, f, k, norm, quant)
+    p = block_oracle(w, d, h, norm, causal)
+    lengths = [200, 131, 57]
+    x = O.to_dtype(rng.standard_normal((B, T, d)), dtype)
+    pos = O.to_dtype(O.RelPositionalEncoding(d, 5000, True).get_encoding(T), dtype)
+    blk = gpu_block(w, d, h, f, k, norm, causal, dtype)
+    xd = dev(x, dtype)
+    blk.forward_(xd, dev(pos, dtype), None, lengths)
+    got = host(xd)
+    ref = O.conformer_block(p, x, pos, None, lengths, dtype)
+    if dtype == O.F32:
+        err = row_rel_err(got, ref)
+        print(f"block f32 quant={quant}: max per-row error / row max {err:.3e}")
+        assert err < F32_TOL
+    else:
+        err = row_rel_err(got, ref)
+        n_far = int(np.sum(np.abs(got - ref) > BF16_TOL))
+        print(f"block bf16 quant={quant}: max |err| {np.max(np.abs(got - ref)):.3e}, per-row error / row max "
+              f"{err:.3e}, {n_far} of {got.size} outputs beyond {BF16_TOL} (max |ref| {np.max(np.abs(ref)):.2f})")
+        assert err < BF16_TOL
+        assert n_far <= 1e-2 * got.size
+
+
+def test_block_bf16_causal_conv_is_refused():
+    d, h, f, k = 256, 2, 512, 4
+    rng = np.random.default_rng(72)
+    w = block_weights(rng, d, h, f, k, "layer_norm", False)
+    blk = gpu_block(w, d, h, f, k, "layer_norm", True, O.BF16)
+    x = dev(rng.standard_normal((1, 10, d)), O.BF16)
+    pos = dev(O.RelPositionalEncoding(d, 5000, True).get_encoding(10), O.BF16)
+    with pytest.raises(M.MhsaError) as e:
+        blk.forward_(x, pos)
+    assert e.value.code == M.MHSA_ENOTSUP
+
+
+def test_encoder_forward_equals_block_loop():
+    """The offline encoder loop over 3 bf16 blocks equals calling each block
+    in turn, bit for bit."""
+    d, h, f, k, B, T = 512, 4, 2048, 9, 2, 150
+    rng = np.random.default_rng(73)
+    ws = [block_weights(rng, d, h, f, k, "batch_norm", False, prefix=f"l{i}") for i in range(3)]
+    blks = [gpu_block(w, d, h, f, k, "batch_norm", False, O.BF16, prefix=f"l{i}") for i, w in enumerate(ws)]
+    x = dev(rng.standard_normal((B, T, d)), O.BF16)
+    pos = dev(O.RelPositionalEncoding(d, 5000, True).get_encoding(T), O.BF16)
+    a, b = x.clone(), x.clone()
+    for blk in blks:
+        blk.forward_(a, pos, None, [150, 97])
+    M.encoder_forward_(blks, b, pos, None, [150, 97])
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+@pytest.mark.timeout(900)
+def test_streaming_encoder_24_steps_against_oracle():
+    """Two cache-aware blocks (causal conv kernel 9 with LayerNorm, d_model
+    512, 4 heads, ff 2048) streamed 24 chunks of 14 frames for 3 sessions
+    with per-session fills (0, 33, 70) against a 70-frame cache under the
+    [70, 13] chunked_limited context, in fp32: every step's output against
+    the oracle's conformer_block_with_cache run per session on its own state
+    (end to end), and both caches read back at the end."""
+    d, h, f, k = 512, 4, 2048, 9
+    B, C, T, steps = 3, 70, 14, 24
+    ctx = ((70, 13), "chunked_limited")
+    rng = np.random.default_rng(74)
+    ws = [block_weights(rng, d, h, f, k, "layer_norm", False, prefix=f"l{i}") for i in range(2)]
+    ps = [block_oracle(w, d, h, "layer_norm", True, prefix=f"l{i}") for i, w in enumerate(ws)]
+    blks = [gpu_block(w, d, h, f, k, "layer_norm", True, O.F32, prefix=f"l{i}") for i, w in enumerate(ws)]
+    enc = M.StreamingEncoder(blks, B, C, T)
+    fills = [0, 33, 70]
+    att = rng.standard_normal((2, B, C, d)) * 0.5
+    for b in range(B):
+        att[:, b, :C - fills[b]] = 0.0
+    conv = rng.standard_normal((2, B, d, k - 1)) * 0.5
+    enc.load_cache(dev(att, O.F32), dev(conv, O.F32), fills)
+    state = [[(att[l, b:b + 1], conv[l, b:b + 1]) for l in range(2)] for b in range(B)]
+    pos = O.RelPositionalEncoding(d, 5000, True).get_encoding(C + T)
+    pos_d = dev(pos, O.F32)
+    worst = 0.0
+    for step in range(steps):
+        x = rng.standard_normal((B, T, d))
+        xd = dev(x, O.F32)
+        enc.step_(xd, pos_d, M.StreamingMask(*ctx, None, [T] * B))
+        got = host(xd)
+        for b in range(B):
+            m = O.streaming_mask(ctx[0], ctx[1], C, fills[b], T, T)
+            y = x[b:b + 1].astype(np.float32).astype(np.float64)
+            for l in range(2):
+                a_c, c_c = state[b][l]
+                y, a_c, c_c = O.conformer_block_with_cache(ps[l], y, pos, a_c, c_c, m, None, O.F32)
+                state[b][l] = (a_c, c_c)
+            e = row_rel_err(got[b:b + 1], y)
+            worst = max(worst, e)
+            assert e < F32_TOL, (step, b, e)
+            fills[b] = O.next_fill(fills[b], T, 0, C)
+        assert enc.fill() == fills
+    ch, tm = enc.read_cache()
+    ch, tm = host(ch), host(tm)
+    for b in range(B):
+        for l in range(2):
+            assert row_rel_err(ch[l, b:b + 1], state[b][l][0]) < F32_TOL
+            assert row_rel_err(np.swapaxes(tm[l, b:b + 1], 1, 2), np.swapaxes(state[b][l][1], 1, 2)) < F32_TOL
+    print(f"streaming encoder, 2 blocks x {steps} steps x {B} sessions: worst per-row error / row max {worst:.3e}")

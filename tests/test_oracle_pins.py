@@ -829,3 +829,124 @@ def test_feed_forward_promoted_matches_torch_promotion():
     got = O.feed_forward(p, x, O.BF16, act=O.F32)
     assert np.max(np.abs(got - y)) / np.max(np.abs(y)) < 1e-6
     assert np.max(np.abs(O.feed_forward(p, O.bf16_round(x), O.BF16) - got)) / np.max(np.abs(y)) > 1e-3
+
+
+# ---------------------------------------------------------------------------
+# ConformerBlock (conformer.rs:1693-1971)
+# ---------------------------------------------------------------------------
+
+def _block_params(d, h, f, k, seed, causal=True, zero=()):
+    """A block with random modules and norms; modules named in `zero` output
+    exactly 0 (FeedForward: linear2 zero; attention: linear_out zero;
+    conv: pointwise_conv2 zero)."""
+    rng = np.random.default_rng(seed)
+    ff1, ff2 = _ffn_params(d, f, seed + 1, 0.3), _ffn_params(d, f, seed + 2, 0.3)
+    attn = random_params(d, h, seed + 3, scale=0.3)
+    conv = _conv_params(d, k, "layer_norm", causal, seed + 4)
+    zl = lambda lin: O.LinearLayer(np.zeros_like(lin.weight), None if lin.bias is None else np.zeros_like(lin.bias))
+    if "ff1" in zero:
+        ff1 = O.FeedForwardParams(ff1.linear1, zl(ff1.linear2))
+    if "ff2" in zero:
+        ff2 = O.FeedForwardParams(ff2.linear1, zl(ff2.linear2))
+    if "attn" in zero:
+        attn.linear_out = zl(attn.linear_out)
+    if "conv" in zero:
+        conv.pointwise_conv2 = zl(conv.pointwise_conv2)
+    norm = lambda: (1.0 + 0.2 * rng.standard_normal(d), 0.2 * rng.standard_normal(d))
+    return O.ConformerBlockParams(ff1, norm(), attn, norm(), conv, norm(), ff2, norm(), norm())
+
+
+def _torch_ln(x, nw):
+    F = torch.nn.functional
+    return F.layer_norm(torch.tensor(x), (x.shape[-1],), torch.tensor(nw[0]), torch.tensor(nw[1]), eps=1e-5).numpy()
+
+
+def _torch_ffn(p, x):
+    F = torch.nn.functional
+    xt = torch.tensor(x)
+    hh = F.silu(F.linear(xt, torch.tensor(p.linear1.weight), torch.tensor(p.linear1.bias)))
+    return F.linear(hh, torch.tensor(p.linear2.weight), torch.tensor(p.linear2.bias)).numpy()
+
+
+@pytest.mark.parametrize("live", [("ff1",), ("attn",), ("conv",), ("ff2",), ("ff1", "attn"), ("attn", "conv"),
+                                  ("conv", "ff2"), ("ff1", "attn", "conv", "ff2")])
+def test_conformer_block_sublayer_order(live):
+    """The block from library routines and the definition-based attention
+    (torch layer_norm / linear / silu / conv1d, `direct_attention`), in the
+    order conformer.rs:1693-1875 runs them: x += 0.5 FF1(LN1 x); x +=
+    MHSA(LN2 x); x += conv(LN3 x); x += 0.5 FF2(LN4 x); norm_out. Modules not
+    in `live` output zero; with two or more live, a swapped order changes the
+    result (checked), so the comparison pins the order, the half steps and
+    each residual."""
+    d, h, f, k, T = 16, 2, 32, 5, 9
+    p = _block_params(d, h, f, k, 50, zero=tuple(m for m in ("ff1", "attn", "conv", "ff2") if m not in live))
+    x = np.random.default_rng(51).standard_normal((2, T, d))
+    pos = O.RelPositionalEncoding(d, 64, False).get_encoding(T)
+    vis = np.ones((2, T, T), dtype=bool)
+    steps = {
+        "ff1": lambda y: y + 0.5 * _torch_ffn(p.ff1, _torch_ln(y, p.ff1_norm)),
+        "attn": lambda y: y + direct_attention(p.attn, _torch_ln(y, p.attn_norm), _torch_ln(y, p.attn_norm), pos, 0,
+                                               vis),
+        "conv": lambda y: y + _torch_conv_module(p.conv, _torch_ln(y, p.conv_norm)),
+        "ff2": lambda y: y + 0.5 * _torch_ffn(p.ff2, _torch_ln(y, p.ff2_norm)),
+    }
+    order = ["ff1", "attn", "conv", "ff2"]
+    y = x
+    for m in order:
+        y = steps[m](y)
+    ref = _torch_ln(y, p.out_norm)
+    got = O.conformer_block(p, x, pos, None, None, O.F32)
+    assert np.max(np.abs(got - ref)) < 1e-10
+    if len(live) > 1:
+        y = x
+        for m in reversed(order):
+            y = steps[m](y)
+        assert np.max(np.abs(_torch_ln(y, p.out_norm) - ref)) > 1e-3
+
+
+def test_conformer_block_key_padding_and_conv_padding():
+    """Padding from lengths (PaddingMask, conformer.rs:1594-1615): keys past
+    each length are hidden from attention (length 0 keeps key 0, the
+    reference's clamp) and the conv zeroes those frames after its GLU; with
+    every length >= T there is no mask at all."""
+    d, h, f, k, T = 16, 2, 32, 5, 9
+    p = _block_params(d, h, f, k, 52, causal=False)
+    x = np.random.default_rng(53).standard_normal((3, T, d))
+    pos = O.RelPositionalEncoding(d, 64, False).get_encoding(T)
+    lengths = [T, 4, 0]
+    got = O.conformer_block(p, x, pos, None, lengths, O.F32)
+    vis = np.zeros((3, T, T), dtype=bool)
+    for b, ln in enumerate(lengths):
+        vis[b, :, :max(ln, 1)] = True
+    y = x + 0.5 * _torch_ffn(p.ff1, _torch_ln(x, p.ff1_norm))
+    hn = _torch_ln(y, p.attn_norm)
+    y = y + direct_attention(p.attn, hn, hn, pos, 0, vis)
+    y = y + _torch_conv_module(p.conv, _torch_ln(y, p.conv_norm), lengths)
+    y = y + 0.5 * _torch_ffn(p.ff2, _torch_ln(y, p.ff2_norm))
+    assert np.max(np.abs(got - _torch_ln(y, p.out_norm))) < 1e-10
+    assert np.array_equal(O.conformer_block(p, x, pos, None, [T, T + 3, T], O.F32),
+                          O.conformer_block(p, x, pos, None, None, O.F32))
+
+
+def test_conformer_block_streaming_equals_offline_chunked():
+    """The cache-aware block over consecutive chunks, from empty caches
+    (attention fill 0, conv cache zeros), equals the offline block over the
+    whole sequence under the same chunked_limited context with a causal
+    conv: rows are row-wise through FF / LayerNorm, the attention cache holds
+    the normalised inputs h that offline attention reads as keys, the
+    streaming mask hides exactly the keys outside the chunk window, and the
+    conv cache is the causal left context."""
+    d, h, f, k = 16, 2, 32, 5
+    C, T, n = 8, 4, 4
+    p = _block_params(d, h, f, k, 54, causal=True)
+    seq = np.random.default_rng(55).standard_normal((1, n * T, d))
+    ctx = ((C, T - 1), "chunked_limited")
+    whole = O.conformer_block(p, seq, O.RelPositionalEncoding(d, 64, False).get_encoding(n * T),
+                              O.AttentionContext.new(*ctx), None, O.F32)
+    att, conv, fill = np.zeros((1, C, d)), np.zeros((1, d, k - 1)), 0
+    pos = O.RelPositionalEncoding(d, 64, False).get_encoding(C + T)
+    for c in range(n):
+        m = O.streaming_mask(ctx[0], ctx[1], C, fill, T, T)
+        y, att, conv = O.conformer_block_with_cache(p, seq[:, c * T:(c + 1) * T], pos, att, conv, m, None, O.F32)
+        assert np.max(np.abs(y - whole[:, c * T:(c + 1) * T])) < 1e-10, c
+        fill = O.next_fill(fill, T, 0, C)
