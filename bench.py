@@ -242,6 +242,14 @@ def profile_kernels(handles, step, nsteps, rep_tag, repeat):
     return kernels
 
 
+def launch_repeat(base, base_steps, rep, rep_steps, tag):
+    """How many back-to-back launches each event pair of the repeat pass held:
+    its launches per step over the plain pass's (the library issues in-place
+    forms once whatever the repeat request)."""
+    per_step = base[tag][1] / base_steps
+    return max(1, round(rep[tag][1] / rep_steps / per_step)) if per_step else 1
+
+
 def roofline(cfg, kernel, work, avg_ms, dtag, repeat):
     """The roofline object of one kernel from its algorithmic work per launch
     and its average launch time."""
@@ -255,7 +263,8 @@ def roofline(cfg, kernel, work, avg_ms, dtag, repeat):
     return {"bound": bound, "kernel": kernel, "achieved": round(ach, 2), "peak": peak, "unit": unit,
             "frac": round(ach / peak, 4), "traffic": measured_traffic(cfg.name, kernel),
             "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_per_launch": amount,
-            "timing": f"HIP events around {repeat} back-to-back launches on the launch stream"}
+            "timing": (f"HIP events around {repeat} back-to-back launches on the launch stream" if repeat > 1
+                       else "HIP events around each launch on the launch stream")}
 
 
 def bench_conv(args, cfg):
@@ -294,18 +303,18 @@ def bench_conv(args, cfg):
 
     wall, gpu_ms = time_steps(step, args)
     ms_per_step = wall * 1e3 / args.steps
-    kernels = profile_kernels([m], step, max(1, min(args.steps, 50)), None, 1)
+    n_base, n_rep = max(1, min(args.steps, 50)), max(1, min(args.steps, 10))
+    kernels = profile_kernels([m], step, n_base, None, 1)
     dom = max(kernels, key=lambda k: kernels[k][0])
-    rep = profile_kernels([m], step, max(1, min(args.steps, 10)), dom, args.repeat)
+    rep = profile_kernels([m], step, n_rep, dom, args.repeat)
     dtag = "bf16" if cfg.dtype == "bfloat16" else "f32"
     roof = roofline(cfg, dom, W.conv_work(cfg, dom), rep[dom][0] / rep[dom][1], dtag,
-                    1 if (cfg.steps and dom == "conv") else args.repeat)
+                    launch_repeat(kernels, n_base, rep, n_rep, dom))
     # every kernel against its own roofline (the fused conv kernel is HBM-bound)
     per_kernel = {}
     for tag in kernels:
-        r = rep if tag == dom else profile_kernels([m], step, max(1, min(args.steps, 10)), tag, args.repeat)
-        # the library does not repeat the in-place cache update
-        reps = 1 if (cfg.steps and tag == "conv") else args.repeat
+        r = rep if tag == dom else profile_kernels([m], step, n_rep, tag, args.repeat)
+        reps = launch_repeat(kernels, n_base, r, n_rep, tag)
         ro = roofline(cfg, tag, W.conv_work(cfg, tag), r[tag][0] / r[tag][1], dtag, reps)
         if ro:
             per_kernel[tag] = {k: ro[k] for k in ("bound", "achieved", "unit", "frac", "avg_launch_us")}
@@ -325,6 +334,133 @@ def bench_conv(args, cfg):
     }
     result["cpu_baseline"] = None if args.no_cpu else cpu_baseline_conv(cfg, ws[0], x, ex, args.cpu_seconds)
     print(json.dumps(result))
+
+
+def block_kernel_work(cfg, tag, lengths, fills_seq):
+    """Algorithmic work of one launch of a ConformerBlock kernel: the
+    FeedForward GEMMs (2 rows D F each), the conv module's kernels as
+    conv_work counts them and the attention sublayer's as kernel_work does."""
+    import workloads as W
+    rows = cfg.batch * cfg.seq_len
+    if tag in ("linear1", "linear2"):
+        return (2.0 * rows * cfg.d_model * cfg.ff_dim, "TFLOP/s", "mfma")
+    if tag in ("pointwise_conv1", "pointwise_conv2", "conv"):
+        return W.conv_work(cfg, tag)
+    return kernel_work(cfg, tag, lengths, fills_seq)
+
+
+def bench_block(args, cfg):
+    """The whole-ConformerBlock workloads: one block pass per step, in place
+    on the previous step's output (offline), or one chunk per session through
+    forward_with_cache with the attention ring and the conv cache
+    (streaming, in place on the step's chunk)."""
+    import torch
+    import relpos_mhsa as M
+    import workloads as W
+
+    ws, x, ex = W.instantiate(cfg)
+    D, T, B, H = cfg.d_model, cfg.seq_len, cfg.batch, cfg.n_heads
+    dt = torch.bfloat16 if cfg.dtype == "bfloat16" else torch.float32
+    blk = M.ConformerBlock(D, H, cfg.ff_dim, cfg.conv_kernel, cfg.conv_norm, cfg.causal, cfg.use_bias)
+    blk.load_weights(ws[0], "blk")
+    blk.set_dtype(dt)
+    pe = M.RelPositionalEncoding(D, 5000, True)
+    lengths = ex.get("lengths")
+    fills_log = []
+    if cfg.cache_size:
+        C = cfg.cache_size
+        pos = pe.get_encoding(C + T).cuda().to(dt).contiguous()
+        enc = M.StreamingEncoder([blk], B, C, T)
+        enc.load_cache(torch.from_numpy(ex["cache"]).cuda().contiguous(),
+                       torch.from_numpy(ex["conv_cache"]).cuda().contiguous(), ex["fills"])
+        chunks = torch.from_numpy(ex["chunks"]).cuda().contiguous()
+        mask = M.StreamingMask((cfg.context[0], cfg.context[1]), cfg.context[2])
+        state = {"i": 0}
+
+        def step():
+            fills_log.append(enc.fill())  # host-side counts, no sync
+            enc.step_(chunks[state["i"] % cfg.steps], pos, mask)
+            state["i"] += 1
+    else:
+        pos = pe.get_encoding(T).cuda().to(dt).contiguous()
+        xs = torch.from_numpy(x).cuda().to(dt).contiguous()
+
+        def step():
+            blk.forward_(xs, pos, None, lengths)
+
+    n_before = len(fills_log)
+    wall, gpu_ms = time_steps(step, args)
+    ms_per_step = wall * 1e3 / args.steps
+    timed_fills = fills_log[n_before:]
+    parts = blk.parts()
+    n_base, n_rep = max(1, min(args.steps, 20)), max(1, min(args.steps, 10))
+    kernels = profile_kernels(parts, step, n_base, None, 1)
+    dom = max(kernels, key=lambda k: kernels[k][0])
+    n0 = len(fills_log)
+    rep = profile_kernels(parts, step, n_rep, dom, args.repeat)
+    dtag = "bf16" if cfg.dtype == "bfloat16" else "f32"
+    work = block_kernel_work(cfg, dom, lengths, fills_log[n0:] or [ex.get("fills")])
+    roof = roofline(cfg, dom, work, rep[dom][0] / rep[dom][1], dtag, launch_repeat(kernels, n_base, rep, n_rep, dom))
+    if cfg.cache_size:
+        total = float(np.mean([W.block_flops(cfg, None, f) for f in timed_fills]))
+    else:
+        total = W.block_flops(cfg, lengths)
+    result = {
+        "metric": METRIC, "value": round(B * T * args.steps / wall, 1), "unit": "frames/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": dtag,
+        "data": "synthetic (seeded numpy PCG64; Xavier-uniform weights)",
+        "config": {"workload": cfg.name, "module": "ConformerBlock", "d_model": D, "n_heads": H, "ff_dim": cfg.ff_dim,
+                   "conv_kernel": cfg.conv_kernel, "conv_norm": cfg.conv_norm, "causal": cfg.causal, "batch": B,
+                   "seq_len": T, "key_padding": bool(lengths), "context": cfg.context,
+                   "cache_size": cfg.cache_size or None},
+        "gpu_ms_per_step": round(gpu_ms / args.steps, 4),
+        "step_tflops": round(total / (ms_per_step * 1e-3) / 1e12, 2),
+        "roofline": roof,
+        "kernels_avg_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in sorted(kernels.items())},
+    }
+    result["cpu_baseline"] = None if args.no_cpu else cpu_baseline_block(cfg, ws[0], x, ex, args.cpu_seconds)
+    print(json.dumps(result))
+
+
+def cpu_baseline_block(cfg, w, x, ex, budget_s):
+    """The float32 BLAS restatement of the ConformerBlock (oracle/cpu_blas.py)
+    timed on the host over a bounded sample."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import cpu_blas
+    import relpos_oracle as O
+    P = cpu_blas.block_params(w, "blk", cfg.dtype == "bfloat16")
+    D, T, B, H = cfg.d_model, cfg.seq_len, cfg.batch, cfg.n_heads
+    ctx = None if cfg.context is None else (cfg.context[0], cfg.context[1], cfg.context[2] == "chunked_limited")
+    pe = O.RelPositionalEncoding(D, 5000, True)
+    if cfg.cache_size:
+        C = cfg.cache_size
+        st = cpu_blas.BlockStreamer(P, H, ex["cache"][0], ex["conv_cache"][0], pe.get_encoding(C + T)[0], ctx)
+        state = {"i": 0, "fill": ex["fills"][0]}  # one mask per step from session 0 (conformer.rs:883-887)
+
+        def one():
+            st.step(ex["chunks"][state["i"] % cfg.steps], state["fill"])
+            state["fill"] = min(state["fill"] + T, C)
+            state["i"] += 1
+        frames, what = B * T, f"{B} sessions x {T}-frame chunk through the block's caches"
+    else:
+        pos = pe.get_encoding(T)[0].astype(np.float32)
+        lens = ex.get("lengths")
+
+        def one():
+            cpu_blas.block(P, H, x, pos, ctx, lens, cfg.causal)
+        frames, what = B * T, f"{B} utterances x {T} frames"
+    passes, t0 = 0, time.perf_counter()
+    while True:
+        one()
+        passes += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    el = time.perf_counter() - t0
+    return {"value": round(passes * frames / el, 2), "unit": "frames/s", "cores": cpu_blas.threads(), "kind": "port",
+            "sample": f"{passes} pass(es) of {what} in {el:.1f} s; float32 numpy restatement of the ConformerBlock "
+                      f"(FeedForwards and projections as OpenBLAS sgemm, the attention as the reference writes it, "
+                      f"streaming K/V re-projected over cache + chunk)"}
 
 
 def cpu_baseline_conv(cfg, w, x, ex, budget_s):
@@ -380,6 +516,9 @@ def main():
     cfg = W.CONFIGS[args.config]
     if cfg.module == "conv":
         bench_conv(args, cfg)
+        return
+    if cfg.module == "block":
+        bench_block(args, cfg)
         return
     layers_w, x, ex = W.instantiate(cfg)
     dt = torch.bfloat16 if cfg.dtype == "bfloat16" else torch.float32
@@ -459,10 +598,12 @@ def main():
     prof_steps = max(1, min(args.steps, 50 if cfg.layers == 1 else 3))
     kernels, _ = profile_pass(prof_steps)
     dom = "attention" if cfg.cache_size else max(kernels, key=lambda k: kernels[k][0])
-    rep, rep_fills = profile_pass(max(1, min(args.steps, 10 if cfg.layers == 1 else 2)), dom)
+    rep_steps = max(1, min(args.steps, 10 if cfg.layers == 1 else 2))
+    rep, rep_fills = profile_pass(rep_steps, dom)
     avg_ms = rep[dom][0] / rep[dom][1]
     dtag = "bf16" if cfg.dtype == "bfloat16" else "f32"
-    roof = roofline(cfg, dom, kernel_work(cfg, dom, lengths, rep_fills), avg_ms, dtag, args.repeat)
+    roof = roofline(cfg, dom, kernel_work(cfg, dom, lengths, rep_fills), avg_ms, dtag,
+                    launch_repeat(kernels, prof_steps, rep, rep_steps, dom))
 
     if cfg.cache_size:
         total_flops = float(np.mean([W.algorithmic_flops(cfg, None, f) for f in timed_fills]))

@@ -319,6 +319,14 @@ int32_t mhsa_ffn_sublayer_forward(mhsa_ffn* ffn, void* x_inout, int32_t rows, co
 int32_t mhsa_ffn_forward_f32(mhsa_ffn* ffn, const float* x, int32_t rows, float* out, void* hip_stream);
 int32_t mhsa_ffn_sublayer_forward_f32(mhsa_ffn* ffn, float* x_inout, int32_t rows, const float* ln_gamma_host,
                                       const float* ln_beta_host, float eps, void* hip_stream);
+/* Per-kernel HIP-event timing of the module's launches, as mhsa_profile_*
+ * does for a layer (tags linear1, linear2, layer_norm; the residual form of
+ * linear2 is not repeated). No reference counterpart. */
+int32_t mhsa_ffn_profile_enable(mhsa_ffn* ffn, int32_t enable);
+int32_t mhsa_ffn_profile_repeat(mhsa_ffn* ffn, const char* tag, int32_t n);
+int32_t mhsa_ffn_profile_reset(mhsa_ffn* ffn);
+int32_t mhsa_ffn_profile_count(mhsa_ffn* ffn);
+int32_t mhsa_ffn_profile_entry(mhsa_ffn* ffn, int32_t idx, const char** name, double* total_ms, int32_t* launches);
 /* Debug: linear `which` (0 = linear1, 1 = linear2) alone, as the plain
  * LinearLayer::forward (quantization.rs:126-162) through the GEMM kernels the
  * module runs, without its SiLU or residual epilogue: out [rows, out_dim] =

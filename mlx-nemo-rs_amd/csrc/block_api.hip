@@ -35,6 +35,7 @@ struct mhsa_ffn {
   DevBuf ln_dev;
   std::vector<float> ln_host;
   DevBuf partial;  // split-K partials of small problems
+  Profiler prof;
 };
 
 namespace {
@@ -142,7 +143,11 @@ int32_t ffn_impl(mhsa_ffn* f, const void* x, int rows, void* out, const void* re
       p.ldr = f->D;
       p.res_scale = res_scale;
     }
-    HIPCHK(mhsa::gemm(act, f->lin[i].quantized, p, s));
+    const char* tag = i == 0 ? "linear1" : "linear2";
+    // (an in-place residual form is not repeated: each pass would add again)
+    ProfScope ps(f->prof, tag, s, true, !(i == 1 && residual == out));
+    for (int r = ps.reps(); r > 0; --r)
+      HIPCHK(mhsa::gemm(act, f->lin[i].quantized, p, s));
   }
   return MHSA_OK;
 }
@@ -174,7 +179,11 @@ int32_t ffn_sublayer(mhsa_ffn* f, void* x, int32_t rows, const float* gamma, con
     bd = gd + D;
   }
   HIPCHK(f->hbuf.ensure(align_up((int64_t)rows * D * mhsa::dtype_size(act), 256)));
-  HIPCHK(mhsa::layer_norm(act, x, f->hbuf.p, gd, bd, eps, rows, D, s));
+  {
+    ProfScope ps(f->prof, "layer_norm", s);
+    for (int r = ps.reps(); r > 0; --r)
+      HIPCHK(mhsa::layer_norm(act, x, f->hbuf.p, gd, bd, eps, rows, D, s));
+  }
   // x + 0.5 * FF(LN(x)): the half step scales exactly (conformer.rs:1727-1729)
   return ffn_impl(f, f->hbuf.p, rows, x, x, 0.5f, act, s);
 }
@@ -252,6 +261,24 @@ int32_t mhsa_ffn_sublayer_forward_f32(mhsa_ffn* f, float* x, int32_t rows, const
                                       float eps, void* hs) {
   if (!f) return fail(MHSA_EINVAL, "null handle");
   return ffn_sublayer(f, x, rows, gamma, beta, eps, mhsa::kF32, static_cast<hipStream_t>(hs));
+}
+
+int32_t mhsa_ffn_profile_enable(mhsa_ffn* f, int32_t enable) {
+  if (!f) return fail(MHSA_EINVAL, "null handle");
+  return f->prof.enable(enable);
+}
+int32_t mhsa_ffn_profile_repeat(mhsa_ffn* f, const char* tag, int32_t n) {
+  if (!f) return fail(MHSA_EINVAL, "null handle");
+  return f->prof.set_repeat(tag, n);
+}
+int32_t mhsa_ffn_profile_reset(mhsa_ffn* f) {
+  if (!f) return fail(MHSA_EINVAL, "null handle");
+  return f->prof.reset();
+}
+int32_t mhsa_ffn_profile_count(mhsa_ffn* f) { return f ? f->prof.entries() : -1; }
+int32_t mhsa_ffn_profile_entry(mhsa_ffn* f, int32_t idx, const char** name, double* total_ms, int32_t* launches) {
+  if (!f) return fail(MHSA_EINVAL, "null handle");
+  return f->prof.entry(idx, name, total_ms, launches);
 }
 
 int32_t mhsa_ffn_debug_linear(mhsa_ffn* f, int32_t which, int32_t f32_act, const void* x, int32_t rows, void* out,
@@ -463,7 +490,7 @@ int32_t conv_impl(mhsa_conv* m, const void* x, int B, int T, DType act, const in
   HIPCHK(m->partial.ensure((size_t)mhsa::kGemmPartialElems * 4));
   {
     ProfScope ps(m->prof, "pointwise_conv1", s);
-    for (int r = m->prof.reps("pointwise_conv1"); r > 0; --r)
+    for (int r = ps.reps(); r > 0; --r)
       if (int32_t rc = conv_pointwise(m, 0, act, x, (int)rows, m->gbuf.p, nullptr, s)) return rc;
   }
   // several frame tiles of one item would read the cache while the last one
@@ -476,7 +503,7 @@ int32_t conv_impl(mhsa_conv* m, const void* x, int B, int T, DType act, const in
     cache_in = static_cast<const float*>(m->cache_prev.p);
   }
   // (a cache updated in place is not repeated: each pass would advance it)
-  ProfScope ps(m->prof, "conv", s);
+  ProfScope ps(m->prof, "conv", s, true, !cache);
   for (int b0 = 0; b0 < B; b0 += mhsa::kMaxBatch) {
     const int nb = std::min(mhsa::kMaxBatch, B - b0);
     mhsa::ConvParams p;
@@ -494,16 +521,16 @@ int32_t conv_impl(mhsa_conv* m, const void* x, int B, int T, DType act, const in
     p.K = K;
     p.left = m->causal ? C : C / 2;
     for (int b = 0; b < nb; ++b) p.len[b] = lens ? std::max(0, std::min(lens[b0 + b], T)) : T;
-    for (int r = cache ? 1 : m->prof.reps("conv"); r > 0; --r) HIPCHK(mhsa::conv_glu_depthwise(act, cdt, p, nb, s));
+    for (int r = ps.reps(); r > 0; --r) HIPCHK(mhsa::conv_glu_depthwise(act, cdt, p, nb, s));
   }
   if (m->norm == MHSA_CONV_LAYER_NORM) {  // nn::LayerNorm (eps 1e-5) then SiLU, in place
-    ps.next("layer_norm");
+    ps.next("layer_norm", false);  // in place
     HIPCHK(mhsa::layer_norm(cdt, m->ybuf.p, m->ybuf.p, m->norm_pack, m->norm_pack + D, 1e-5f, (int)rows, D, s,
                             mhsa::kActSilu));
   }
-  ps.next("pointwise_conv2");
-  // (the residual form is not repeated: out aliases the residual)
-  for (int r = residual ? 1 : m->prof.reps("pointwise_conv2"); r > 0; --r)
+  // (an in-place residual form is not repeated: each pass would add again)
+  ps.next("pointwise_conv2", residual != out);
+  for (int r = ps.reps(); r > 0; --r)
     if (int32_t rc = conv_pointwise(m, 1, cdt, m->ybuf.p, (int)rows, out, residual, s)) return rc;
   return MHSA_OK;
 }

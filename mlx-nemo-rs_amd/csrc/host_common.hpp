@@ -202,7 +202,9 @@ struct Profiler {
       if (p.b) (void)hipEventDestroy(p.b);
     }
   }
-  int begin(const char* tag, hipStream_t s) {
+  // `repeatable` false: the launches are issued once whatever the repeat tag
+  // (in-place forms, whose second pass would read their own output).
+  int begin(const char* tag, hipStream_t s, bool repeatable = true) {
     if (!on) return -1;
     if (used == pool.size()) {
       Pair p;
@@ -211,7 +213,7 @@ struct Profiler {
     }
     Pair& p = pool[used];
     p.tag = tag;
-    p.n = reps(tag);
+    p.n = repeatable ? reps(tag) : 1;
     if (hipEventRecord(p.a, s) != hipSuccess) return -1;
     return (int)used++;
   }
@@ -276,13 +278,16 @@ struct ProfScope {
   Profiler& p;
   hipStream_t s;
   int idx;
-  ProfScope(Profiler& prof, const char* tag, hipStream_t s_, bool enabled = true)
-      : p(prof), s(s_), idx(enabled ? prof.begin(tag, s_) : -1) {}
+  ProfScope(Profiler& prof, const char* tag, hipStream_t s_, bool enabled = true, bool repeatable = true)
+      : p(prof), s(s_), idx(enabled ? prof.begin(tag, s_, repeatable) : -1) {}
   ~ProfScope() { p.end(idx, s); }
+  // How many times the scope's launches are to be issued: the count its span
+  // is credited with, so the per-launch average stays right.
+  int reps() const { return idx >= 0 ? p.pool[idx].n : 1; }
   // Close the current span and open the next one.
-  void next(const char* tag) {
+  void next(const char* tag, bool repeatable = true) {
     p.end(idx, s);
-    idx = idx >= 0 || p.on ? p.begin(tag, s) : -1;
+    idx = idx >= 0 || p.on ? p.begin(tag, s, repeatable) : -1;
   }
 };
 

@@ -82,8 +82,8 @@ struct mhsa_layer {
 namespace {
 // ProfScope over a layer's profiler.
 struct LayerProf : ProfScope {
-  LayerProf(mhsa_layer* L, const char* tag, hipStream_t s_, bool enabled = true)
-      : ProfScope(L->prof, tag, s_, enabled) {}
+  LayerProf(mhsa_layer* L, const char* tag, hipStream_t s_, bool enabled = true, bool repeatable = true)
+      : ProfScope(L->prof, tag, s_, enabled, repeatable) {}
 };
 }  // namespace
 
@@ -522,19 +522,19 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   }
   if (paired) {
     LayerProf ps(L, "gemm_qkv_pos", s, prof);
-    for (int r = prof ? L->prof.reps("gemm_qkv_pos") : 1; r > 0; --r)
+    for (int r = ps.reps(); r > 0; --r)
       HIPCHK(mhsa::gemm_pair(L->dt, L->dev[0].quantized, gq, gp, s));
   } else {
     {
       LayerProf ps(L, "gemm_qkv", s, prof);
-      for (int r = prof ? L->prof.reps("gemm_qkv") : 1; r > 0; --r)
+      for (int r = ps.reps(); r > 0; --r)
         if ((rc = project_qkv(L, x, (int)o.M, o.qkv, 3 * D, s, o.use_vt ? &o.vt : nullptr))) return rc;
     }
     if (!ready) {
       LayerProf ps(L, "gemm_pos", s, prof);
       mhsa::GemmParams g;
       if ((rc = pos_gemm(L, o, pos_emb, g))) return rc;
-      for (int r = prof ? L->prof.reps("gemm_pos") : 1; r > 0; --r)
+      for (int r = ps.reps(); r > 0; --r)
         HIPCHK(mhsa::gemm(L->dt, L->dev[4].quantized, g, s));
     }
   }
@@ -570,7 +570,7 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   auto key_bounds = [&](int b, int& lo, int& hi, int& qv) { offline_key_bounds(lens, T, b, lo, hi, qv); };
   {
     LayerProf ps(L, "attention", s, prof);
-    for (int r = prof ? L->prof.reps("attention") : 1; r > 0 && !rc; --r) {
+    for (int r = ps.reps(); r > 0 && !rc; --r) {
       bool fused = false;
       if (next && B <= mhsa::kMaxBatch) {
         mhsa::AttnParams af = a;
@@ -590,8 +590,9 @@ int32_t forward_impl(mhsa_layer* L, const void* x, int B, int T, const void* pos
   }
   if (rc) return rc;
   if (!out) return MHSA_OK;
-  LayerProf ps(L, "gemm_out", s, prof);
-  for (int r = prof ? L->prof.reps("gemm_out") : 1; r > 0 && !rc; --r)
+  // (an in-place residual form is not repeated: each pass would add again)
+  LayerProf ps(L, "gemm_out", s, prof, residual != out);
+  for (int r = ps.reps(); r > 0 && !rc; --r)
     rc = run_gemm(L, L->dt, L->dev[3], D, o.cx, D, (int)o.M, out, D, residual, D, s);
   return rc;
 }
@@ -942,7 +943,7 @@ int32_t mhsa_sublayer_forward(mhsa_layer* L, void* x, int32_t batch, int32_t seq
   if (int32_t rc = sublayer_norm(L, gamma, beta, (int64_t)batch * seq_len, &gd, &bd)) return rc;
   {
     LayerProf ps(L, "layer_norm", s);
-    for (int r = L->prof.reps("layer_norm"); r > 0; --r)
+    for (int r = ps.reps(); r > 0; --r)
       HIPCHK(mhsa::layer_norm(dtype_of(L), x, L->hbuf.p, gd, bd, eps, (int)((int64_t)batch * seq_len), L->D, s));
   }
   return forward_impl(L, L->hbuf.p, batch, seq_len, pos_emb, pos_len, ctx, lens, x, x, AttnDebug(), s);
@@ -981,13 +982,13 @@ int32_t mhsa_stack_sublayer_forward(mhsa_layer* const* layers, int32_t n_layers,
     LayerProf ps(L, "gemm_pos", s);
     mhsa::GemmParams g;
     if (int32_t rc = pos_gemm(L, lay[0], pos_emb, g)) return rc;
-    for (int r = L->prof.reps("gemm_pos"); r > 0; --r) HIPCHK(mhsa::gemm(L->dt, L->dev[4].quantized, g, s));
+    for (int r = ps.reps(); r > 0; --r) HIPCHK(mhsa::gemm(L->dt, L->dev[4].quantized, g, s));
   }
   for (int l = 0; l < n_layers; ++l) {
     mhsa_layer* L = layers[l];
     {
       LayerProf ps(L, "layer_norm", s);
-      for (int r = L->prof.reps("layer_norm"); r > 0; --r)
+      for (int r = ps.reps(); r > 0; --r)
         HIPCHK(mhsa::layer_norm(dtype_of(L), x, L->hbuf.p, gd[l], bd[l], eps, (int)M, L->D, s));
     }
     FusedNext nx;
@@ -1088,7 +1089,7 @@ int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, 
   // a bf16 layer projects its bf16 table in bf16 and widens the result
   if (L->pmemo_len != pos_len) {
     HIPCHK(L->pmemo.ensure(align_up((int64_t)pos_len * D * 4, 256)));
-    LayerProf ps(L, "gemm_pos", s);
+    LayerProf ps(L, "gemm_pos", s, true, false);
     if (L->dt == mhsa::kBF16) {
       HIPCHK(L->pmemo_bf16.ensure(align_up((int64_t)pos_len * D * 2, 256)));
       if ((rc = run_gemm(L, mhsa::kBF16, L->dev[4], D, pos_emb, D, pos_len, L->pmemo_bf16.p, D, nullptr, 0, s)))
@@ -1133,7 +1134,8 @@ int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, 
     fp.ring_len = R;
   }
   const bool one_launch = !S || (L->qkv_fused && mhsa::gemm_split_fused_ok(mhsa::kF32, fp));
-  LayerProf ps_kv(L, one_launch ? "gemm_qkv" : "gemm_q", s);
+  // (only the one-launch ring form is repeated: it rewrites the same rows)
+  LayerProf ps_kv(L, one_launch ? "gemm_qkv" : "gemm_q", s, true, S && one_launch);
   if (!S) {
     if (L->qkv_fused) {
       if ((rc = run_gemm(L, mhsa::kF32, L->sdev[0], 3 * D, x, D, (int)M, q, 3 * D, nullptr, 0, s))) return rc;
@@ -1147,10 +1149,10 @@ int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, 
     // K|V to the cache ring's rows of this chunk, and the chunk's input rows
     // copied into the input ring by the workgroups of the first column tile.
     if (one_launch) {
-      for (int r = L->prof.reps("gemm_qkv"); r > 0; --r) HIPCHK(mhsa::gemm(mhsa::kF32, L->sdev[0].quantized, fp, s));
+      for (int r = ps_kv.reps(); r > 0; --r) HIPCHK(mhsa::gemm(mhsa::kF32, L->sdev[0].quantized, fp, s));
     } else {
       if ((rc = run_gemm(L, mhsa::kF32, L->sdev[0], D, x, D, (int)M, q, D, nullptr, 0, s))) return rc;
-      ps_kv.next("gemm_kv");
+      ps_kv.next("gemm_kv", false);
       if (L->qkv_fused) {
         if ((rc = run_gemm(L, mhsa::kF32, L->sdev[1], 2 * D, x, D, (int)M, kv, 2 * D, nullptr, 0, s, T, R, slot, R)))
           return rc;
@@ -1161,7 +1163,7 @@ int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, 
                            R, slot, R)))
           return rc;
       }
-      ps_kv.next("ring_write");
+      ps_kv.next("ring_write", false);
       HIPCHK(mhsa::ring_write(mhsa::kF32, x, S->ring_h.p, B, T, D, R, D, slot, s));
     }
   }
@@ -1193,7 +1195,7 @@ int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, 
   a.L = Lk;
   a.qoff = C;
   set_ctx(a, ctx);
-  for (int r = L->prof.reps("attention"); r > 0 && !rc; --r)
+  for (int r = ps_kv.reps(); r > 0 && !rc; --r)
     rc = run_attention(
         L, mhsa::kF32, a, B,
         [&](int b, int& lo, int& hi, int& qv) {
@@ -1203,8 +1205,8 @@ int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, 
         },
         s);
   if (rc) return rc;
-  ps_kv.next("gemm_out");
-  for (int r = L->prof.reps("gemm_out"); r > 0 && !rc; --r)
+  ps_kv.next("gemm_out", residual != out);
+  for (int r = ps_kv.reps(); r > 0 && !rc; --r)
     rc = run_gemm(L, mhsa::kF32, L->sdev[3], D, cx, D, (int)M, out, D, residual, D, s);
   if (rc) return rc;
   if (S) {
@@ -1341,7 +1343,7 @@ int32_t mhsa_stack_step(mhsa_stack* K, void* x, const float* gamma, const float*
   for (int l = 0; l < n; ++l) {
     mhsa_layer* L = K->layers[l];
     {
-      LayerProf ps(L, "layer_norm", s);
+      LayerProf ps(L, "layer_norm", s, true, false);
       HIPCHK(mhsa::layer_norm(mhsa::kF32, x, K->h.p, g ? g + (size_t)2 * l * D : nullptr,
                               g ? g + (size_t)(2 * l + 1) * D : nullptr, eps, (int)M, D, s));
     }

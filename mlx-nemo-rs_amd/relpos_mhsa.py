@@ -49,7 +49,8 @@ EXPORTS = (
     "mhsa_block_attention", "mhsa_block_feed_forward", "mhsa_block_conv", "mhsa_block_forward",
     "mhsa_encoder_forward", "mhsa_encoder_create", "mhsa_encoder_destroy", "mhsa_encoder_load_cache",
     "mhsa_encoder_read_cache", "mhsa_encoder_fill", "mhsa_encoder_step",
-    "mhsa_ffn_debug_linear", "mhsa_conv_debug_linear",
+    "mhsa_ffn_profile_enable", "mhsa_ffn_profile_repeat", "mhsa_ffn_profile_reset", "mhsa_ffn_profile_count",
+    "mhsa_ffn_profile_entry", "mhsa_ffn_debug_linear", "mhsa_conv_debug_linear",
     "mhsa_debug_dequantize", "mhsa_debug_linear", "mhsa_debug_linear_f32", "mhsa_debug_layer_norm",
     "mhsa_debug_attention_forms", "mhsa_debug_offline_mask", "mhsa_debug_stream_mask", "mhsa_debug_rel_shift_index",
     "mhsa_debug_position_scores", "mhsa_debug_top_keys", "mhsa_profile_enable", "mhsa_profile_repeat",
@@ -179,6 +180,11 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_debug_attention_forms": (I, [P(ctypes.c_int64), I]),
         "mhsa_debug_layer_norm": (I, [VP, VP, I, P(ctypes.c_float), P(ctypes.c_float), F, VP, VP]),
         "mhsa_ffn_debug_linear": (I, [VP, I, I, VP, I, VP, VP]),
+        "mhsa_ffn_profile_enable": (I, [VP, I]),
+        "mhsa_ffn_profile_repeat": (I, [VP, ctypes.c_char_p, I]),
+        "mhsa_ffn_profile_reset": (I, [VP]),
+        "mhsa_ffn_profile_count": (I, [VP]),
+        "mhsa_ffn_profile_entry": (I, [VP, I, P(ctypes.c_char_p), P(ctypes.c_double), PI]),
         "mhsa_conv_debug_linear": (I, [VP, I, I, VP, I, VP, VP]),
         "mhsa_debug_offline_mask": (I, [I, I, P(Context), PI, VP, VP]),
         "mhsa_debug_stream_mask": (I, [I, I, I, P(StreamMask), VP, VP]),
@@ -393,8 +399,10 @@ def _tensor_list(weights: Dict[str, np.ndarray]):
     return (Tensor * max(len(tensors), 1))(*tensors), len(tensors), arrays
 
 
-class FeedForward:
+class FeedForward(_Profiled):
     """FeedForward (conformer.rs:2031-2088) backed by the HIP library."""
+
+    _PROFILE = "mhsa_ffn_profile_"
 
     def __init__(self, d_model: int, ff_dim: int, use_bias: bool):
         lib = library()
@@ -1053,6 +1061,13 @@ def debug_rel_shift_index(rows: int, total_len: int):
     return out
 
 
+class _View(_Profiled):
+    """A module handle owned by a ConformerBlock: its profiler only."""
+
+    def __init__(self, lib, handle, prefix: str):
+        self._lib, self._h, self._PROFILE = lib, ctypes.c_void_p(handle), prefix
+
+
 class ConformerBlock:
     """ConformerBlock (conformer.rs:1613-2028) backed by the HIP library:
     FF1 half-step, MHSA, convolution, FF2 half-step, norm_out."""
@@ -1088,6 +1103,15 @@ class ConformerBlock:
         arr_t, n, keep = _tensor_list(weights)
         bits, group = (quant.bits, quant.group_size) if quant else (0, 0)
         _check(self._lib.mhsa_block_load_weights(self._h, arr_t, n, prefix.encode(), 1 if strict else 0, bits, group))
+
+    def parts(self):
+        """Profiled views of the block's attention layer, conv module and both
+        FeedForwards (owned by the block)."""
+        lib = self._lib
+        return [_View(lib, lib.mhsa_block_attention(self._h), "mhsa_profile_"),
+                _View(lib, lib.mhsa_block_conv(self._h), "mhsa_conv_profile_"),
+                _View(lib, lib.mhsa_block_feed_forward(self._h, 1), "mhsa_ffn_profile_"),
+                _View(lib, lib.mhsa_block_feed_forward(self._h, 2), "mhsa_ffn_profile_")]
 
     def forward_(self, x, pos_emb, context: Optional[AttentionContext] = None, lengths: Optional[Sequence[int]] = None):
         """In place x <- block(x) (conformer.rs:1693-1875); lengths [B] build the

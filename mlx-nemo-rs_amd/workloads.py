@@ -19,13 +19,24 @@ Six configurations of the FastConformer attention sublayer:
                       biases N(0, 0.01), codes U{0..255}), B=4, T=1500, bf16,
                       valid lengths U{1000..1500}, seed 4
 
-and two of the block's ConvolutionModule (conformer.rs:2105-2437):
+two of the block's ConvolutionModule (conformer.rs:2105-2437):
 
 * ``conv_offline_bf16`` D=1024, K=9, BatchNorm, symmetric, B=8, T=375, bf16,
                       valid lengths U{188..375}, seed 5
 * ``conv_stream_f32``  D=1024, K=9, LayerNorm, causal, 16 sessions, 14-frame
                       chunks through the [16, 1024, 8] f32 conv cache, 50
                       steps, fp32, seed 6
+
+and two of the whole ConformerBlock (conformer.rs:1613-2028: FF1 half step,
+MHSA, conv, FF2 half step, norm_out) at the 0.6B shape (ff_dim 4096, conv
+kernel 9):
+
+* ``block_offline_bf16`` B=8, T=375, bf16, symmetric conv with BatchNorm,
+                      valid lengths U{188..375}, seed 7
+* ``block_stream_f32`` 16 sessions, 14-frame chunks against a 70-frame
+                      attention cache under [70, 13] chunked_limited, causal
+                      conv with LayerNorm and its [16, 1024, 8] cache, fills
+                      U{0..70}, 50 steps, fp32, seed 8
 
 Weights are Xavier-uniform U(+-sqrt(6 / 2D)), pos_bias_u/v ~ N(0, 0.02^2),
 inputs x ~ N(0, 1); every array comes from numpy's PCG64 with the stated
@@ -58,11 +69,13 @@ class Workload:
     cache_size: int = 0
     steps: int = 0
     fills: Optional[List[int]] = None
-    # "mhsa" (the attention sublayer) or "conv" (ConvolutionModule)
+    # "mhsa" (the attention sublayer), "conv" (ConvolutionModule) or
+    # "block" (the whole ConformerBlock)
     module: str = "mhsa"
     conv_kernel: int = 0
     conv_norm: str = "batch_norm"
     causal: bool = False
+    ff_dim: int = 0  # "block": FeedForward width
 
     @property
     def head_dim(self) -> int:
@@ -123,7 +136,32 @@ CONFIGS: Dict[str, Workload] = {
                                   module="conv", conv_kernel=9, conv_norm="batch_norm"),
     "conv_stream_f32": Workload("conv_stream_f32", 1024, 8, 16, 14, "float32", seed=6, use_bias=True, steps=50,
                                 module="conv", conv_kernel=9, conv_norm="layer_norm", causal=True),
+    "block_offline_bf16": Workload("block_offline_bf16", 1024, 8, 8, 375, "bfloat16", seed=7, use_bias=True,
+                                   module="block", conv_kernel=9, conv_norm="batch_norm", ff_dim=4096),
+    "block_stream_f32": Workload("block_stream_f32", 1024, 8, 16, 14, "float32", seed=8, use_bias=True,
+                                 cache_size=70, steps=50, context=(70, 13, "chunked_limited"), module="block",
+                                 conv_kernel=9, conv_norm="layer_norm", causal=True, ff_dim=4096),
 }
+
+BLOCK_NORMS = ("norm_feed_forward1", "norm_self_att", "norm_conv", "norm_feed_forward2", "norm_out")
+
+
+def make_block_weights(rng, d: int, h: int, f: int, k: int, norm: str = "batch_norm", prefix: str = "blk"):
+    """One ConformerBlock's tensors keyed like a checkpoint (conformer.rs:1977-2028):
+    feed_forward1/2 Xavier-uniform with biases N(0, 0.02), self_attn as
+    make_layer_weights with zero biases, conv as make_conv_weights, the five
+    LayerNorms weight U(0.8, 1.2), bias N(0, 0.05)."""
+    w: Dict[str, np.ndarray] = {}
+    for ff in ("feed_forward1", "feed_forward2"):
+        for name, (o, i) in (("linear1", (f, d)), ("linear2", (d, f))):
+            w[f"{prefix}.{ff}.{name}.weight"] = xavier(rng, o, i)
+            w[f"{prefix}.{ff}.{name}.bias"] = rng.normal(0, 0.02, o).astype(np.float32)
+    w.update(prefixed(make_layer_weights(rng, d, h, True, False), f"{prefix}.self_attn"))
+    w.update(make_conv_weights(rng, d, k, norm, False, True, f"{prefix}.conv"))
+    for n in BLOCK_NORMS:
+        w[f"{prefix}.{n}.weight"] = rng.uniform(0.8, 1.2, d).astype(np.float32)
+        w[f"{prefix}.{n}.bias"] = rng.normal(0, 0.05, d).astype(np.float32)
+    return w
 
 
 def make_conv_weights(rng, d: int, k: int, norm: str = "batch_norm", quantized: bool = False,
@@ -164,6 +202,21 @@ def instantiate(cfg: Workload, centred: bool = False):
     layers: list of per-layer weight dicts; x: float32 [B, T, D] (or the first
     chunk for streaming); extras: lengths / fills / per-step chunks."""
     rng = np.random.default_rng(cfg.seed)
+    if cfg.module == "block":
+        w = make_block_weights(rng, cfg.d_model, cfg.n_heads, cfg.ff_dim, cfg.conv_kernel, cfg.conv_norm)
+        extras = {}
+        if cfg.cache_size:
+            B, C, D = cfg.batch, cfg.cache_size, cfg.d_model
+            extras["fills"] = [int(v) for v in rng.integers(0, C + 1, size=B)]
+            cache = rng.standard_normal((1, B, C, D)).astype(np.float32)
+            for b, fl in enumerate(extras["fills"]):
+                cache[:, b, : C - fl] = 0.0
+            extras["cache"] = cache
+            extras["conv_cache"] = np.zeros((1, B, D, cfg.conv_kernel - 1), dtype=np.float32)
+            extras["chunks"] = rng.standard_normal((cfg.steps, B, cfg.seq_len, D)).astype(np.float32)
+            return [w], extras["chunks"][0], extras
+        extras["lengths"] = [int(v) for v in rng.integers(cfg.seq_len // 2, cfg.seq_len + 1, size=cfg.batch)]
+        return [w], rng.standard_normal((cfg.batch, cfg.seq_len, cfg.d_model)).astype(np.float32), extras
     if cfg.module == "conv":
         w = make_conv_weights(rng, cfg.d_model, cfg.conv_kernel, cfg.conv_norm, cfg.quantized, cfg.use_bias)
         extras = {}
@@ -266,3 +319,13 @@ def algorithmic_bytes(cfg: Workload) -> float:
         w = 5 * D * D * es
     pos_rows = cfg.pos_band or (2 * T - 1)
     return cfg.layers * (w + 2 * B * T * D * es + pos_rows * D * es)
+
+
+def block_flops(cfg: Workload, lengths=None, fills=None) -> float:
+    """Useful MFMA work of one ConformerBlock pass: both FeedForwards
+    (2 x 2 x 2 rows D F), the attention sublayer as algorithmic_flops counts
+    it (streaming: K/V of the cache already projected), and the conv module
+    as conv_flops counts it."""
+    rows = cfg.batch * cfg.seq_len
+    return 8.0 * rows * cfg.d_model * cfg.ff_dim + algorithmic_flops(cfg, lengths, fills) + conv_flops(cfg)
+

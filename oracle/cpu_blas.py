@@ -281,3 +281,71 @@ def conv_module(P, x, lengths=None, cache=None, causal=False):
         y = layer_norm(y) * P["norm_weight"] + P["norm_bias"]
     y = y * (np.float32(1.0) / (np.float32(1.0) + np.exp(-y)))
     return _linear(y, P["pointwise_conv2.weight"], P["pointwise_conv2.bias"]), new_cache
+
+
+# ---------------------------------------------------------------------------
+# ConformerBlock (conformer.rs:1693-1971)
+# ---------------------------------------------------------------------------
+
+def _bf16_values(a):
+    u = _f32(a).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32).view(np.float32)
+
+
+def block_params(weights, prefix: str = "blk", dtype_bf16: bool = False):
+    """float32 parameters of a ConformerBlock from checkpoint-style tensors
+    (at bf16 values for a bf16 model): both FeedForwards, the attention layer
+    (layer_params), the conv module (conv_params) and the five LayerNorms."""
+    bf = _bf16_values if dtype_bf16 else _f32
+    out = {}
+    for ff in ("feed_forward1", "feed_forward2"):
+        out[ff] = {n: (bf(weights[f"{prefix}.{ff}.{n}.weight"]), bf(weights[f"{prefix}.{ff}.{n}.bias"]))
+                   for n in ("linear1", "linear2")}
+    att = {k[len(prefix) + len(".self_attn."):]: v for k, v in weights.items() if k.startswith(f"{prefix}.self_attn.")}
+    out["attn"] = layer_params(att, dtype_bf16)
+    out["conv"] = conv_params(weights, dtype_bf16, f"{prefix}.conv")
+    out["norms"] = [(bf(weights[f"{prefix}.{n}.weight"]), bf(weights[f"{prefix}.{n}.bias"]))
+                    for n in ("norm_feed_forward1", "norm_self_att", "norm_conv", "norm_feed_forward2", "norm_out")]
+    return out
+
+
+def ffn(P, x):
+    """FeedForward::forward (conformer.rs:2066-2072): linear2(silu(linear1(x)))."""
+    h = _linear(x, *P["linear1"])
+    return _linear(h * (np.float32(1.0) / (np.float32(1.0) + np.exp(-h))), *P["linear2"])
+
+
+def _ln(x, nw):
+    return layer_norm(x) * nw[0] + nw[1]
+
+
+def block(P, n_heads, x, pos_emb, ctx=None, lengths=None, causal=False):
+    """ConformerBlock::forward (conformer.rs:1693-1875)."""
+    half = np.float32(0.5)
+    n = P["norms"]
+    x = x + half * ffn(P["feed_forward1"], _ln(x, n[0]))
+    x = x + forward(P["attn"], n_heads, _ln(x, n[1]), pos_emb, ctx, lengths)
+    x = x + conv_module(P["conv"], _ln(x, n[2]), lengths, None, causal)[0]
+    x = x + half * ffn(P["feed_forward2"], _ln(x, n[3]))
+    return _ln(x, n[4])
+
+
+class BlockStreamer:
+    """ConformerBlock::forward_with_cache (conformer.rs:1893-1971) for a batch
+    of sessions: the attention as Streamer (K/V re-projected over [cache; x]
+    every step) and the conv cache [B, D, K-1]."""
+
+    def __init__(self, P, n_heads, att_cache, conv_cache, pos_emb, ctx):
+        self.P = P
+        self.att = Streamer(P["attn"], n_heads, att_cache, pos_emb, ctx)
+        self.conv_cache = _f32(conv_cache)
+
+    def step(self, x, filled):
+        half = np.float32(0.5)
+        n = self.P["norms"]
+        x = x + half * ffn(self.P["feed_forward1"], _ln(x, n[0]))
+        x = x + self.att.step(_ln(x, n[1]), filled)
+        y, self.conv_cache = conv_module(self.P["conv"], _ln(x, n[2]), None, self.conv_cache, True)
+        x = x + y
+        x = x + half * ffn(self.P["feed_forward2"], _ln(x, n[3]))
+        return _ln(x, n[4])
