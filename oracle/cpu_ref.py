@@ -1,7 +1,8 @@
 """ctypes wrapper of the fp32 CPU restatement (oracle/cpu_ref.cpp).
 
-TEST INFRASTRUCTURE ONLY: used by tests/ to cross-check the numpy oracle and
-by bench.py's cpu_baseline leg as the timed CPU baseline.
+TEST INFRASTRUCTURE ONLY: used by tests/ to cross-check the numpy oracle.
+The timed CPU baseline of bench.py is the numpy + OpenBLAS restatement in
+oracle/cpu_blas.py, not this file.
 """
 import ctypes
 import os

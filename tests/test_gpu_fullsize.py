@@ -89,7 +89,8 @@ def test_local_window_full_size_against_oracle_windows():
         pos = O.bf16_round(O.RelPositionalEncoding(D, 5000, True).get_encoding(hi - lo))
         ref = O.mhsa_forward(p, xb[:, lo:hi], pos, ctx, None, O.BF16)[:, i0 - lo:i1 - lo]
         err = abs_err(got[:, i0:i1], ref)
-        print(f"xl_local_bf16 queries [{i0}, {i1}): max abs error {err:.3e}")
+        n_far = int(np.sum(np.abs(got[:, i0:i1] - ref) > BF16_TOL))
+        print(f"xl_local_bf16 queries [{i0}, {i1}): max abs error {err:.3e}, {n_far} of {ref.size} beyond {BF16_TOL}")
         assert err < BF16_TOL, (i0, i1, err)
 
 
@@ -124,7 +125,9 @@ def test_stack_u8_layer_full_shape_zero_mean():
     got = host(xd)
     ref = O.mhsa_sublayer(p, xb, pos, None, O.key_padding_mask(lengths, T), dtype=O.BF16)
     err = row_rel_err(got, ref)
-    print(f"u8 sublayer: max per-row error / row max {err:.3e}")
+    n_far = int(np.sum(np.abs(got - ref) > BF16_TOL))
+    print(f"u8 sublayer: max per-row error / row max {err:.3e}, max abs error {abs_err(got, ref):.3e}, "
+          f"{n_far} of {ref.size} outputs beyond {BF16_TOL} absolute")
     assert err < BF16_TOL
 
 
