@@ -7,7 +7,7 @@
 //
 // Kernels, by problem (gfx950, 256 CUs):
 //  * gemm_tile_kernel: bf16 projections with enough rows to fill the GPU
-//    (128x128, 192x192 or 256x256 tiles on 4 waves, direct-to-LDS operand
+//    (128x128, 192x128, 192x192, 192x256 or 256x256 tiles on 4 waves, direct-to-LDS operand
 //    streams, LDS-staged epilogue; described at its definition).
 //  * gemm_kpar_kernel: fp32 projections of few rows (the streaming chunk,
 //    one short utterance): persistent workgroups over 32 x 32 tiles, each
@@ -689,13 +689,15 @@ int split_count(const GemmParams& p) {
 // 192 x 192 tile pass at K = 1024 with every CU busy (measured: a 256 x 256
 // pass 1.45; 128 x 128 0.5 alone on a CU with four stages, 0.75 for a pass of
 // two per CU with two stages; 192 x 128 taken as 0.7, two thirds of the
-// MFMAs of a 192 x 192 pass plus its fixed prologue and epilogue).
+// MFMAs of a 192 x 192 pass plus its fixed prologue and epilogue; 192 x 256
+// taken as 1.3: a third more MFMAs than 192 x 192 at fewer LDS bytes each).
 template <int BM, int BN>
 double tile_cost(const GemmParams& p) {
   const int64_t tiles = m_tiles<BM>(p) * (p.N / BN);
   double c;
   if (BM == 128 && BN == 128) c = tiles <= 256 ? 0.5 : (double)((tiles + 511) / 512) * 0.75;
   else if (BM == 192 && BN == 128) c = (double)((tiles + 255) / 256) * 0.7;
+  else if (BM == 192 && BN == 256) c = (double)((tiles + 255) / 256) * 1.3;
   else c = (double)((tiles + 255) / 256) * (BM * BN == 256 * 256 ? 1.45 : 1.0);
   return c * p.K / 1024.0;
 }
@@ -725,9 +727,10 @@ bool tile_ok(const GemmParams& p) {
 // 128 x 128 at the tile shape with the lowest estimated time, below that
 // (short inputs, a short position table) as 64 x 64 tiles with four stages
 // (749 x 1024 x 1024: 6.6 us against 12 us for split-K and its reduce).
-// Stages: three (loads two ahead) for 192 x 192 and 192 x 128; four for a
-// 128 x 128 tile that has its CU to itself, two when two share one;
-// 256 x 256 fits two. Returns false when p does not take the tile kernel.
+// Stages: three (loads two ahead) for 192 x 192, 192 x 128 and the u8
+// 192 x 256; four for a 128 x 128 tile that has its CU to itself, two when
+// two share one; 256 x 256 and the dense 192 x 256 fit two. Returns false
+// when p does not take the tile kernel.
 bool tile_form(const GemmParams& p, TileForm& f) {
   if (!tile_ok(p) || p.N % 64) return false;
   if (p.N % 128 || m_tiles<128>(p) * (p.N / 128) < 96) {
@@ -740,6 +743,7 @@ bool tile_form(const GemmParams& p, TileForm& f) {
   if (p.N % 192 == 0 && tile_cost<192, 192>(p) < best) best = tile_cost<192, 192>(p), f = TileForm{192, 192, 3};
   if (p.N % 256 == 0 && tile_cost<256, 256>(p) < best) best = tile_cost<256, 256>(p), f = TileForm{256, 256, 2};
   if (tile_cost<192, 128>(p) < best) best = tile_cost<192, 128>(p), f = TileForm{192, 128, 3};
+  if (p.N % 256 == 0 && tile_cost<192, 256>(p) < best) best = tile_cost<192, 256>(p), f = TileForm{192, 256, 2};
   return true;
 }
 
@@ -750,6 +754,7 @@ bool dispatch_tile(const GemmParams& p, hipStream_t s, hipError_t& err) {
   if (f.bm == 64) err = launch_tile<64, 64, QUANT, 4>(p, s);
   else if (f.bm == 256) err = launch_tile<256, 256, QUANT, 2>(p, s);
   else if (f.bm == 192 && f.bn == 192) err = launch_tile<192, 192, QUANT, 3>(p, s);
+  else if (f.bm == 192 && f.bn == 256) err = launch_tile<192, 256, QUANT, QUANT ? 3 : 2>(p, s);
   else if (f.bm == 192) err = launch_tile<192, 128, QUANT, 3>(p, s);
   else if (f.ns == 4) err = launch_tile<128, 128, QUANT, 4>(p, s);
   else err = launch_tile<128, 128, QUANT, 2>(p, s);
@@ -856,6 +861,7 @@ template <bool QUANT>
 hipError_t dispatch_pair(const TileForm& f, const GemmParams& p1, const GemmParams& p2, hipStream_t s) {
   if (f.bm == 256) return launch_pair<256, 256, 2, QUANT>(p1, p2, s);
   if (f.bm == 192 && f.bn == 192) return launch_pair<192, 192, 3, QUANT>(p1, p2, s);
+  if (f.bm == 192 && f.bn == 256) return launch_pair<192, 256, QUANT ? 3 : 2, QUANT>(p1, p2, s);
   if (f.bm == 192) return launch_pair<192, 128, 3, QUANT>(p1, p2, s);
   if (f.ns == 4) return launch_pair<128, 128, 4, QUANT>(p1, p2, s);
   return launch_pair<128, 128, 2, QUANT>(p1, p2, s);
