@@ -228,17 +228,23 @@ int32_t mhsa_encoder_create(mhsa_block* const* blocks, int32_t n_layers, int32_t
   if (!out) return fail(MHSA_EINVAL, "null output pointer");
   *out = nullptr;
   if (!blocks || n_layers <= 0) return fail(MHSA_EINVAL, "null or empty block list");
-  std::unique_ptr<mhsa_encoder> e(new (std::nothrow) mhsa_encoder());
-  if (!e) return fail(MHSA_ENOMEM, "out of host memory");
+  // every block checked before anything is allocated
   for (int l = 0; l < n_layers; ++l) {
     mhsa_block* k = blocks[l];
-    if (!k) return fail(MHSA_EINVAL, "block %d is null", l);
+    if (!k) return fail(MHSA_EINVAL, "block %d is null", l);  // (block 0 first)
     if (k->D != blocks[0]->D || k->K != blocks[0]->K)
       return fail(MHSA_EINVAL, "block %d differs from block 0 in d_model or conv kernel size", l);
     if (!k->causal || k->K < 2)
       return fail(MHSA_EINVAL, "block %d: the streaming conv cache needs a causal convolution of kernel size >= 2", l);
     for (int j = 0; j < l; ++j)
       if (blocks[j] == k) return fail(MHSA_EINVAL, "block %d appears twice", l);
+  }
+  if (batch <= 0 || cache_size < 0 || chunk_len <= 0)
+    return fail(MHSA_EINVAL, "bad encoder shape: batch %d, cache_size %d, chunk_len %d", batch, cache_size, chunk_len);
+  std::unique_ptr<mhsa_encoder> e(new (std::nothrow) mhsa_encoder());
+  if (!e) return fail(MHSA_ENOMEM, "out of host memory");
+  for (int l = 0; l < n_layers; ++l) {
+    mhsa_block* k = blocks[l];
     mhsa_stack* st = nullptr;
     if (int32_t rc = mhsa_stack_create(&k->attn, 1, batch, cache_size, chunk_len, &st)) return rc;
     e->att.push_back(st);

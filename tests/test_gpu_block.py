@@ -111,6 +111,41 @@ def test_encoder_forward_equals_block_loop():
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("tag", ["linear1", "linear2", "pointwise_conv2", "gemm_out"])
+def test_profiler_repeat_issues_in_place_launches_once(tag):
+    """The event profiler issues the launches of its repeat tag n times per
+    event pair. The residual forms that update x in place (FeedForward
+    linear2, pointwise_conv2, the attention's output projection) are issued
+    once whatever the tag, and credited with one launch; others (linear1)
+    with n. Either way the block's output equals the unprofiled one."""
+    d, h, f, k, B, T, n, calls = 512, 4, 2048, 9, 2, 150, 4, 3
+    rng = np.random.default_rng(75)
+    w = block_weights(rng, d, h, f, k, "batch_norm", False)
+    blk = gpu_block(w, d, h, f, k, "batch_norm", False, O.BF16)
+    x = dev(rng.standard_normal((B, T, d)), O.BF16)
+    pos = dev(O.RelPositionalEncoding(d, 5000, True).get_encoding(T), O.BF16)
+    a, b = x.clone(), x.clone()
+    for _ in range(calls):
+        blk.forward_(a, pos, None, [150, 97])
+    parts = blk.parts()
+    for pt in parts:
+        pt.profile_reset()
+        pt.profile_repeat(tag, n)
+        pt.profile(True)
+    for _ in range(calls):
+        blk.forward_(b, pos, None, [150, 97])
+    torch.cuda.synchronize()
+    counts = [pt.profile_read() for pt in parts]
+    for pt in parts:
+        pt.profile(False)
+        pt.profile_repeat(None, 1)
+    assert torch.equal(a, b), tag
+    got = sum(c[tag][1] for c in counts if tag in c)
+    owners = sum(1 for c in counts if tag in c)  # FeedForward tags: both FeedForwards
+    expect = owners * calls * (n if tag == "linear1" else 1)
+    assert got == expect, (tag, got, expect)
+
+
 @pytest.mark.timeout(900)
 def test_streaming_encoder_24_steps_against_oracle():
     """Two cache-aware blocks (causal conv kernel 9 with LayerNorm, d_model
