@@ -857,19 +857,19 @@ def conformer_block(p: ConformerBlockParams, x, pos_emb, context: Optional[Atten
 
 
 def conformer_block_with_cache(p: ConformerBlockParams, x, pos_emb, att_cache, conv_cache, att_mask=None,
-                               pad_lengths=None, dtype: str = F32):
+                               pad_lengths=None, dtype: str = F32, pos_rows=None):
     """ConformerBlock::forward_with_cache (conformer.rs:1893-1971) on the
     streaming path's f32 activations x [B, T, D]: every op that meets them is
     f32 (the parameters hold their `dtype` values). The attention caches
-    its LayerNorm output h (attention.rs:579-586); `att_mask` as
-    mhsa_forward_with_cache takes it; `pad_lengths` [B] zero the conv's
+    its LayerNorm output h (attention.rs:579-586); `att_mask` and `pos_rows`
+    as mhsa_forward_with_cache takes them; `pad_lengths` [B] zero the conv's
     frames past them (pad_mask, conformer.rs:929-941). Returns (x,
     new_att_cache, new_conv_cache)."""
     x = np.asarray(x, dtype=np.float64)
     x = feed_forward_sublayer(p.ff1, x, *p.ff1_norm, dtype=dtype, act=F32)  # 1914-1919
     g, b = p.attn_norm
     h = layer_norm(x, None if g is None else to_dtype(g, dtype), None if b is None else to_dtype(b, dtype), 1e-5, F32)
-    a, new_att = mhsa_forward_with_cache(p.attn, h, pos_emb, att_cache, att_mask, dtype)  # 1924-1933
+    a, new_att = mhsa_forward_with_cache(p.attn, h, pos_emb, att_cache, att_mask, dtype, pos_rows=pos_rows)  # 1924-1933
     x = x + a
     x, new_conv = conv_sublayer(p.conv, x, *p.conv_norm, dtype=dtype, act=F32, lengths=pad_lengths,
                                 cache=conv_cache)  # 1936-1941

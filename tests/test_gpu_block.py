@@ -146,21 +146,40 @@ def test_profiler_repeat_issues_in_place_launches_once(tag):
     assert got == expect, (tag, got, expect)
 
 
+def _layer_pos_rows(blk, pos_d):
+    """The bf16 position rows the block's attention layer projects (its
+    streaming memo), through the layer's own GEMM."""
+    lib = M.library()
+    h = lib.mhsa_block_attention(blk._h)
+    rows = pos_d.numel() // pos_d.shape[-1]
+    out = torch.empty_like(pos_d)
+    M._check(lib.mhsa_debug_linear(h, M.LINEARS.index("linear_pos"), M._dptr(pos_d), rows, M._dptr(out),
+                                   M._stream_ptr()))
+    return host(out)[0]
+
+
 @pytest.mark.timeout(900)
-def test_streaming_encoder_24_steps_against_oracle():
+@pytest.mark.parametrize("dtype,steps", [(O.F32, 24), (O.BF16, 8)])
+def test_streaming_encoder_24_steps_against_oracle(dtype, steps):
     """Two cache-aware blocks (causal conv kernel 9 with LayerNorm, d_model
-    512, 4 heads, ff 2048) streamed 24 chunks of 14 frames for 3 sessions
-    with per-session fills (0, 33, 70) against a 70-frame cache under the
-    [70, 13] chunked_limited context, in fp32: every step's output against
-    the oracle's conformer_block_with_cache run per session on its own state
-    (end to end), and both caches read back at the end."""
+    512, 4 heads, ff 2048) streamed chunks of 14 frames for 3 sessions with
+    per-session fills (0, 33, 70) against a 70-frame cache under the
+    [70, 13] chunked_limited context: every step's output against the
+    oracle's conformer_block_with_cache run per session on its own state
+    (end to end), and both caches read back at the end. fp32 blocks for 24
+    steps; bf16 blocks for 8, where the streamed activations stay f32 and
+    every op is f32 on the bf16 parameter values (conformer.rs:845-849), and
+    the bf16 position rows the layer projects are handed to the oracle (the
+    GPU rounds its fp32 sum, the oracle the exact one: an element within
+    accumulation noise of a rounding boundary may differ by one ulp, which
+    test_streaming_bf16_layer_xl_shape checks on its own)."""
     d, h, f, k = 512, 4, 2048, 9
-    B, C, T, steps = 3, 70, 14, 24
+    B, C, T = 3, 70, 14
     ctx = ((70, 13), "chunked_limited")
     rng = np.random.default_rng(74)
     ws = [block_weights(rng, d, h, f, k, "layer_norm", False, prefix=f"l{i}") for i in range(2)]
     ps = [block_oracle(w, d, h, "layer_norm", True, prefix=f"l{i}") for i, w in enumerate(ws)]
-    blks = [gpu_block(w, d, h, f, k, "layer_norm", True, O.F32, prefix=f"l{i}") for i, w in enumerate(ws)]
+    blks = [gpu_block(w, d, h, f, k, "layer_norm", True, dtype, prefix=f"l{i}") for i, w in enumerate(ws)]
     enc = M.StreamingEncoder(blks, B, C, T)
     fills = [0, 33, 70]
     att = rng.standard_normal((2, B, C, d)) * 0.5
@@ -169,8 +188,9 @@ def test_streaming_encoder_24_steps_against_oracle():
     conv = rng.standard_normal((2, B, d, k - 1)) * 0.5
     enc.load_cache(dev(att, O.F32), dev(conv, O.F32), fills)
     state = [[(att[l, b:b + 1], conv[l, b:b + 1]) for l in range(2)] for b in range(B)]
-    pos = O.RelPositionalEncoding(d, 5000, True).get_encoding(C + T)
-    pos_d = dev(pos, O.F32)
+    pos = O.to_dtype(O.RelPositionalEncoding(d, 5000, True).get_encoding(C + T), dtype)
+    pos_d = dev(pos, dtype)
+    rows = [_layer_pos_rows(blk, pos_d) if dtype == O.BF16 else None for blk in blks]
     worst = 0.0
     for step in range(steps):
         x = rng.standard_normal((B, T, d))
@@ -182,7 +202,7 @@ def test_streaming_encoder_24_steps_against_oracle():
             y = x[b:b + 1].astype(np.float32).astype(np.float64)
             for l in range(2):
                 a_c, c_c = state[b][l]
-                y, a_c, c_c = O.conformer_block_with_cache(ps[l], y, pos, a_c, c_c, m, None, O.F32)
+                y, a_c, c_c = O.conformer_block_with_cache(ps[l], y, pos, a_c, c_c, m, None, dtype, rows[l])
                 state[b][l] = (a_c, c_c)
             e = row_rel_err(got[b:b + 1], y)
             worst = max(worst, e)
@@ -195,4 +215,5 @@ def test_streaming_encoder_24_steps_against_oracle():
         for l in range(2):
             assert row_rel_err(ch[l, b:b + 1], state[b][l][0]) < F32_TOL
             assert row_rel_err(np.swapaxes(tm[l, b:b + 1], 1, 2), np.swapaxes(state[b][l][1], 1, 2)) < F32_TOL
-    print(f"streaming encoder, 2 blocks x {steps} steps x {B} sessions: worst per-row error / row max {worst:.3e}")
+    print(f"streaming encoder ({dtype}), 2 blocks x {steps} steps x {B} sessions: worst per-row error / row max "
+          f"{worst:.3e}")
