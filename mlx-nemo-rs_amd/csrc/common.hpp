@@ -63,9 +63,19 @@ __device__ __forceinline__ floatx16 mma32(const bf16x8 a, const bf16x8 b, floatx
 }
 
 // Round an fp32 value to the storage type and back (identity for fp32).
+// bf16: one packed conversion with 0 as its low input leaves bf16(v) (round
+// to nearest even) in the high half, and the word read as fp32 is that
+// value; the element-wise form compiles to the conversion into the low half
+// and a shift. The s_nop gives an input that a transcendental instruction
+// (exp, rcp) has just written its wait state: the compiler does not look
+// into inline assembly for that hazard.
 template <typename T> __device__ __forceinline__ float round_to(float v);
 template <> __device__ __forceinline__ float round_to<float>(float v) { return v; }
-template <> __device__ __forceinline__ float round_to<bf16>(float v) { return (float)(bf16)v; }
+template <> __device__ __forceinline__ float round_to<bf16>(float v) {
+  float r;
+  asm("s_nop 0\n\tv_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(v));
+  return r;
+}
 
 template <typename T> __device__ __forceinline__ T from_float(float v) { return (T)v; }
 
