@@ -1,8 +1,8 @@
 """The CPU baseline: the reference's rel-pos MHSA op sequence in float32 numpy.
 
 TEST INFRASTRUCTURE ONLY: timed by the `cpu_baseline` leg of `bench.py`; the
-product never imports it. (The float64 oracle in `relpos_oracle.py` is the
-checker; this module is the same algorithm run for speed, not for parity.)
+product never imports it. (The float64 oracle in `relpos_oracle.py` is what
+parity is checked against; this module is the same algorithm run for speed.)
 
 The reference's CPU path is MLX's CPU backend (unavailable offline), where
 every matmul is a BLAS sgemm and the rest are elementwise kernels. This

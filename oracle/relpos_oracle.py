@@ -1,6 +1,6 @@
 """CPU oracle for the FastConformer rel-pos multi-head self-attention path.
 
-TEST INFRASTRUCTURE ONLY. This module is the checker: it may be imported by
+TEST INFRASTRUCTURE ONLY. This module is the oracle: it may be imported by
 `tests/`, by `__graft_entry__.smoke()` and by the `cpu_baseline` leg of
 `bench.py`, and by nothing else. The product (the HIP library under
 `mlx-nemo-rs_amd/`) never calls it and has no CPU fallback.
@@ -476,8 +476,8 @@ def mhsa_forward_with_cache(p: MhsaParams, x: np.ndarray, pos_emb: np.ndarray,
     activation promotes to f32 (MLX type promotion), so only the position
     rows -- a bf16 table through bf16 weights -- are rounded to bf16.
 
-    `pos_rows` [P, D], when given, replaces linear_pos(pos_emb): a checker
-    can then feed a kernel's own projected rows, pinned separately.
+    `pos_rows` [P, D], when given, replaces linear_pos(pos_emb): a test can
+    then feed a kernel's own projected rows, pinned separately.
     """
     x = np.asarray(x, dtype=np.float64)
     pos_emb = np.asarray(pos_emb, dtype=np.float64)
