@@ -217,3 +217,50 @@ def test_streaming_encoder_24_steps_against_oracle(dtype, steps):
             assert row_rel_err(np.swapaxes(tm[l, b:b + 1], 1, 2), np.swapaxes(state[b][l][1], 1, 2)) < F32_TOL
     print(f"streaming encoder ({dtype}), 2 blocks x {steps} steps x {B} sessions: worst per-row error / row max "
           f"{worst:.3e}")
+
+
+def test_streaming_encoder_valid_frames_against_oracle():
+    """Chunks whose sessions end early: per step and session a valid frame
+    count below the chunk (the last chunk of an utterance). The attention
+    hides every key from rows at or past it (the bool mask: those rows give 0
+    before linear_out, attention.rs:774-790) and the conv zeroes the GLU
+    frames past it (pad_mask, conformer.rs:929-941), per session here where
+    the reference uses session 0's count for all. Two fp32 blocks, 6 steps,
+    against the oracle per session."""
+    d, h, f, k = 512, 4, 2048, 9
+    B, C, T = 3, 70, 14
+    ctx = ((70, 13), "chunked_limited")
+    valids = [[14, 9, 1], [14, 14, 5], [7, 14, 14], [0, 3, 14], [14, 13, 2], [11, 14, 14]]
+    rng = np.random.default_rng(76)
+    ws = [block_weights(rng, d, h, f, k, "layer_norm", False, prefix=f"l{i}") for i in range(2)]
+    ps = [block_oracle(w, d, h, "layer_norm", True, prefix=f"l{i}") for i, w in enumerate(ws)]
+    blks = [gpu_block(w, d, h, f, k, "layer_norm", True, O.F32, prefix=f"l{i}") for i, w in enumerate(ws)]
+    enc = M.StreamingEncoder(blks, B, C, T)
+    fills = [0, 33, 70]
+    att = rng.standard_normal((2, B, C, d)) * 0.5
+    for b in range(B):
+        att[:, b, :C - fills[b]] = 0.0
+    conv = rng.standard_normal((2, B, d, k - 1)) * 0.5
+    enc.load_cache(dev(att, O.F32), dev(conv, O.F32), fills)
+    state = [[(att[l, b:b + 1], conv[l, b:b + 1]) for l in range(2)] for b in range(B)]
+    pos = O.RelPositionalEncoding(d, 5000, True).get_encoding(C + T)
+    pos_d = dev(pos, O.F32)
+    worst = 0.0
+    for step, valid in enumerate(valids):
+        x = rng.standard_normal((B, T, d))
+        xd = dev(x, O.F32)
+        enc.step_(xd, pos_d, M.StreamingMask(*ctx, None, valid), valid)
+        got = host(xd)
+        for b in range(B):
+            m = O.streaming_mask(ctx[0], ctx[1], C, fills[b], T, valid[b])
+            y = x[b:b + 1].astype(np.float32).astype(np.float64)
+            for l in range(2):
+                a_c, c_c = state[b][l]
+                y, a_c, c_c = O.conformer_block_with_cache(ps[l], y, pos, a_c, c_c, m, [valid[b]], O.F32)
+                state[b][l] = (a_c, c_c)
+            e = row_rel_err(got[b:b + 1], y)
+            worst = max(worst, e)
+            assert e < F32_TOL, (step, b, valid[b], e)
+            fills[b] = O.next_fill(fills[b], T, 0, C)
+        assert enc.fill() == fills
+    print(f"streaming encoder with valid frame counts: worst per-row error / row max {worst:.3e}")
