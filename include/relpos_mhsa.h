@@ -447,7 +447,7 @@ mhsa_conv* mhsa_block_conv(mhsa_block* block);
  * conformer.rs:1594-1615: keys past a length hidden from the attention,
  * clamped to >= 1; frames past it zeroed in the conv). MHSA_ENOTSUP for a
  * causal conv in a bf16 block (its f32 result promotes the rest of the
- * block). */
+ * block: mhsa_block_forward_to takes that case). */
 int32_t mhsa_block_forward(mhsa_block* block, void* x_inout, int32_t batch, int32_t seq_len, const void* pos_emb,
                            int32_t pos_len, const mhsa_context* ctx, const int32_t* lengths, void* hip_stream);
 /* The offline encoder's layer loop (conformer.rs:542-550): every block in
@@ -455,6 +455,31 @@ int32_t mhsa_block_forward(mhsa_block* block, void* x_inout, int32_t batch, int3
 int32_t mhsa_encoder_forward(mhsa_block* const* blocks, int32_t n_layers, void* x_inout, int32_t batch,
                              int32_t seq_len, const void* pos_emb, int32_t pos_len, const mhsa_context* ctx,
                              const int32_t* lengths, void* hip_stream);
+/* Dtype of forward's result on activations stored in x_dtype (MHSA_F32 or
+ * the block dtype): MHSA_F32 once they are f32 or the conv is causal, whose
+ * zero padding is an f32 array (conformer.rs:2250-2256), so that in a bf16
+ * block MLX promotes the depthwise conv and every later op to f32; else the
+ * block dtype. -1 for a null block or a dtype it cannot take. */
+int32_t mhsa_block_output_dtype(const mhsa_block* block, int32_t x_dtype);
+/* forward (conformer.rs:1693-1875) as the returned array of the reference's
+ * ConformerBlock::forward, whose dtype may differ from its input's: x
+ * [batch, seq_len, d_model] device in x_dtype, which is the block dtype or,
+ * in a bf16 block, MHSA_F32 (activations an earlier causal conv promoted:
+ * every op then runs in f32 on the parameters' bf16 values); out in
+ * mhsa_block_output_dtype(block, x_dtype). out may be x when the two dtypes
+ * agree, else they must not overlap; x is otherwise left unchanged. Other
+ * arguments as mhsa_block_forward. */
+int32_t mhsa_block_forward_to(mhsa_block* block, const void* x, int32_t x_dtype, int32_t batch, int32_t seq_len,
+                              const void* pos_emb, int32_t pos_len, const mhsa_context* ctx, const int32_t* lengths,
+                              void* out, void* hip_stream);
+/* The offline encoder's layer loop (conformer.rs:542-550) over
+ * mhsa_block_forward_to: block 0 reads x (x_dtype), the others run on out,
+ * which ends in the dtype mhsa_block_output_dtype gives when chained over
+ * the blocks (f32 after the first causal conv of a bf16 stack); x and out
+ * must not overlap unless no block changes the dtype. */
+int32_t mhsa_encoder_forward_to(mhsa_block* const* blocks, int32_t n_layers, const void* x, int32_t x_dtype,
+                                int32_t batch, int32_t seq_len, const void* pos_emb, int32_t pos_len,
+                                const mhsa_context* ctx, const int32_t* lengths, void* out, void* hip_stream);
 
 /* The streaming encoder's per-chunk loop over n_layers blocks
  * (ConformerEncoder::forward_streaming, conformer.rs:840-1047, with

@@ -11,6 +11,7 @@
 
 #include "host_common.hpp"
 #include "kernels.hpp"
+#include "sublayers.hpp"
 
 using mhsa::DType;
 
@@ -537,7 +538,56 @@ int32_t conv_impl(mhsa_conv* m, const void* x, int B, int T, DType act, const in
 
 int32_t check_conv(const mhsa_conv* m) { return m ? MHSA_OK : fail(MHSA_EINVAL, "null conv handle"); }
 
+// conv_norm's affine parameters on the device (null when neither is given),
+// rounded like the reference's cast of the norm to the module dtype and
+// uploaded when they change.
+int32_t conv_sublayer_norm(mhsa_conv* m, const float* gamma, const float* beta, const float** gd, const float** bd) {
+  const int D = m->D;
+  *gd = *bd = nullptr;
+  if (!gamma && !beta) return MHSA_OK;
+  std::vector<float> tmp(2 * D);
+  const bool bf = m->dt == mhsa::kBF16;
+  for (int i = 0; i < D; ++i) {
+    const float gv = gamma ? gamma[i] : 1.f, bv = beta ? beta[i] : 0.f;
+    tmp[i] = bf ? round_bf16(gv) : gv;
+    tmp[D + i] = bf ? round_bf16(bv) : bv;
+  }
+  if (tmp != m->ln_host) {
+    if (m->ln_dev.p) HIPCHK(hipDeviceSynchronize());  // earlier LayerNorm launches may still read them
+    HIPCHK(m->ln_dev.ensure(tmp.size() * 4));
+    HIPCHK(hipMemcpy(m->ln_dev.p, tmp.data(), tmp.size() * 4, hipMemcpyHostToDevice));
+    m->ln_host = tmp;
+  }
+  *gd = static_cast<const float*>(m->ln_dev.p);
+  *bd = *gd + D;
+  return MHSA_OK;
+}
+
 }  // namespace
+
+int32_t mhsa_conv_sublayer_to_f32(mhsa_conv* m, const void* x, DType x_dt, int B, int T, const int32_t* lens,
+                                  const float* gamma, const float* beta, float eps, float* out, hipStream_t s) {
+  if (int32_t rc = check_conv(m)) return rc;
+  if (!x || !out || B <= 0 || T <= 0) return fail(MHSA_EINVAL, "bad sublayer arguments");
+  if (!aligned16(x) || !aligned16(out)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  if (m->D > mhsa::kMaxLayerNormDim)
+    return fail(MHSA_ENOTSUP, "the sublayer's LayerNorm supports d_model <= %d (got %d)", mhsa::kMaxLayerNormDim, m->D);
+  if (x_dt != mhsa::kF32 && !(x_dt == m->dt && m->causal))
+    return fail(MHSA_EINVAL, "only f32 activations, or a causal module's own-dtype ones, give an f32 sublayer");
+  if (x_dt != mhsa::kF32 && x == out) return fail(MHSA_EINVAL, "the f32 output cannot overwrite bf16 input");
+  const float* gd;
+  const float* bd;
+  if (int32_t rc = conv_sublayer_norm(m, gamma, beta, &gd, &bd)) return rc;
+  const int D = m->D;
+  const int64_t rows = (int64_t)B * T;
+  HIPCHK(m->hbuf.ensure(align_up(rows * D * mhsa::dtype_size(x_dt), 256)));
+  // conv_norm in the activations' dtype (conformer.rs:1793); the residual x
+  // (conformer.rs:1814) then goes to out in f32, where the module adds to it
+  HIPCHK(mhsa::layer_norm(x_dt, x, m->hbuf.p, gd, bd, eps, (int)rows, D, s));
+  if (x_dt != mhsa::kF32) HIPCHK(mhsa::widen_bf16(x, out, rows * D, s));
+  else if (x != out) HIPCHK(hipMemcpyAsync(out, x, (size_t)rows * D * 4, hipMemcpyDeviceToDevice, s));
+  return conv_impl(m, m->hbuf.p, B, T, x_dt, lens, nullptr, out, out, s);
+}
 
 extern "C" {
 
@@ -717,25 +767,9 @@ int32_t mhsa_conv_sublayer_forward(mhsa_conv* m, void* x, int32_t batch, int32_t
                               "cannot hold in place: call mhsa_conv_forward and add the residual in f32");
   hipStream_t s = static_cast<hipStream_t>(hs);
   const int D = m->D;
-  const float* gd = nullptr;
-  const float* bd = nullptr;
-  if (gamma || beta) {
-    std::vector<float> tmp(2 * D);
-    const bool bf = m->dt == mhsa::kBF16;
-    for (int i = 0; i < D; ++i) {
-      const float gv = gamma ? gamma[i] : 1.f, bv = beta ? beta[i] : 0.f;
-      tmp[i] = bf ? round_bf16(gv) : gv;
-      tmp[D + i] = bf ? round_bf16(bv) : bv;
-    }
-    if (tmp != m->ln_host) {
-      if (m->ln_dev.p) HIPCHK(hipDeviceSynchronize());
-      HIPCHK(m->ln_dev.ensure(tmp.size() * 4));
-      HIPCHK(hipMemcpy(m->ln_dev.p, tmp.data(), tmp.size() * 4, hipMemcpyHostToDevice));
-      m->ln_host = tmp;
-    }
-    gd = static_cast<const float*>(m->ln_dev.p);
-    bd = gd + D;
-  }
+  const float* gd;
+  const float* bd;
+  if (int32_t rc = conv_sublayer_norm(m, gamma, beta, &gd, &bd)) return rc;
   const int64_t rows = (int64_t)batch * seq_len;
   HIPCHK(m->hbuf.ensure(align_up(rows * D * mhsa::dtype_size(act), 256)));
   // conv_norm (conformer.rs:1793, 1939), then x + conv(.) (conformer.rs:1814, 1941)

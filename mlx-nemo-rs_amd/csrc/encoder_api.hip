@@ -11,6 +11,7 @@
 
 #include "host_common.hpp"
 #include "kernels.hpp"
+#include "sublayers.hpp"
 
 using mhsa::DType;
 
@@ -32,6 +33,7 @@ struct mhsa_block {
   std::vector<float> nw[kNorms], nb[kNorms];  // LayerNorm weight / bias as loaded (fp32)
   DevBuf out_norm;                            // norm_out weight, bias in the block dtype's values
   std::vector<float> out_norm_host;           // what out_norm holds
+  DevBuf work;                                // bf16 activations before a causal conv promotes them
   ~mhsa_block() {
     mhsa_ffn_destroy(ff1);
     mhsa_ffn_destroy(ff2);
@@ -97,7 +99,7 @@ int32_t block_forward(mhsa_block* k, void* x, int B, int T, const void* pos_emb,
   if (!x || !pos_emb || B <= 0 || T <= 0) return fail(MHSA_EINVAL, "bad block arguments");
   if (k->causal && k->dt == mhsa::kBF16)
     return fail(MHSA_ENOTSUP, "a causal conv makes the rest of a bf16 block f32 (MLX promotion), which the bf16 "
-                              "input cannot hold in place");
+                              "input cannot hold in place: call mhsa_block_forward_to");
   const int rows = B * T;
   // conformer.rs:1703-1729, 1747-1780, 1790-1814, 1827-1851, 1862
   if (int32_t rc = mhsa_ffn_sublayer_forward(k->ff1, x, rows, k->nw[0].data(), k->nb[0].data(), kNormEps, s))
@@ -114,6 +116,88 @@ int32_t block_forward(mhsa_block* k, void* x, int B, int T, const void* pos_emb,
   const float* bd;
   if (int32_t rc = upload_out_norm(k, &gd, &bd)) return rc;
   HIPCHK(mhsa::layer_norm(k->dt, x, x, gd, bd, kNormEps, rows, k->D, s));
+  return MHSA_OK;
+}
+
+// The block's output dtype for activations stored in xdt: f32 once they are
+// f32 or the conv is causal (its f32 zero padding, conformer.rs:2250-2256,
+// promotes the depthwise conv and everything after it), else the block's.
+DType block_out_dtype(const mhsa_block* k, DType xdt) {
+  return xdt == mhsa::kF32 || k->causal ? mhsa::kF32 : k->dt;
+}
+
+// The block on activations made f32 before it (a bf16 block's ops then all
+// run in f32 on the parameters' bf16 values), in place on x:
+// conformer.rs:1703-1729, 1747-1780, 1790-1814, 1827-1851, 1862 as MLX
+// promotes them.
+int32_t block_forward_act32(mhsa_block* k, float* x, int B, int T, const void* pos_emb, int pos_len,
+                            const mhsa_context* ctx, const int32_t* lens, hipStream_t s) {
+  const int rows = B * T;
+  if (int32_t rc = mhsa_ffn_sublayer_forward_f32(k->ff1, x, rows, k->nw[0].data(), k->nb[0].data(), kNormEps, s))
+    return rc;
+  if (int32_t rc = mhsa_sublayer_forward_act32(k->attn, x, B, T, k->nw[1].data(), k->nb[1].data(), kNormEps,
+                                               pos_emb, pos_len, ctx, lens, s))
+    return rc;
+  if (int32_t rc = mhsa_conv_sublayer_to_f32(k->conv, x, mhsa::kF32, B, T, lens, k->nw[2].data(), k->nb[2].data(),
+                                             kNormEps, x, s))
+    return rc;
+  if (int32_t rc = mhsa_ffn_sublayer_forward_f32(k->ff2, x, rows, k->nw[3].data(), k->nb[3].data(), kNormEps, s))
+    return rc;
+  const float* gd;
+  const float* bd;
+  if (int32_t rc = upload_out_norm(k, &gd, &bd)) return rc;
+  HIPCHK(mhsa::layer_norm(mhsa::kF32, x, x, gd, bd, kNormEps, rows, k->D, s));
+  return MHSA_OK;
+}
+
+// forward from x (stored in xdt) to out (in block_out_dtype): in place where
+// the dtype holds, else through the block's bf16 copy of x up to the conv,
+// whose sublayer writes the f32 sum to out.
+int32_t block_forward_to(mhsa_block* k, const void* x, DType xdt, int B, int T, const void* pos_emb, int pos_len,
+                         const mhsa_context* ctx, const int32_t* lens, void* out, hipStream_t s) {
+  if (!x || !out || !pos_emb || B <= 0 || T <= 0) return fail(MHSA_EINVAL, "bad block arguments");
+  if (!aligned16(x) || !aligned16(out)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  if (xdt != k->dt && xdt != mhsa::kF32)
+    return fail(MHSA_EINVAL, "activations in dtype %d for a block of dtype %d", (int)xdt, (int)k->dt);
+  const DType odt = block_out_dtype(k, xdt);
+  const size_t in_bytes = (size_t)B * T * k->D * mhsa::dtype_size(xdt);
+  if (odt == xdt) {
+    if (out != x) HIPCHK(hipMemcpyAsync(out, x, in_bytes, hipMemcpyDeviceToDevice, s));
+    if (xdt == k->dt) return block_forward(k, out, B, T, pos_emb, pos_len, ctx, lens, s);
+    return block_forward_act32(k, static_cast<float*>(out), B, T, pos_emb, pos_len, ctx, lens, s);
+  }
+  // bf16 activations into a causal bf16 block: bf16 up to the conv's padding
+  const char* xb = static_cast<const char*>(x);
+  const char* ob = static_cast<const char*>(out);
+  if (xb < ob + (size_t)B * T * k->D * 4 && ob < xb + in_bytes)
+    return fail(MHSA_EINVAL, "x and the f32 output must not overlap");
+  if (x != k->work.p) {  // (the encoder loop may have put them there)
+    HIPCHK(k->work.ensure(align_up((int64_t)in_bytes, 256)));
+    HIPCHK(hipMemcpyAsync(k->work.p, x, in_bytes, hipMemcpyDeviceToDevice, s));
+  }
+  const int rows = B * T;
+  if (int32_t rc = mhsa_ffn_sublayer_forward(k->ff1, k->work.p, rows, k->nw[0].data(), k->nb[0].data(), kNormEps, s))
+    return rc;
+  if (int32_t rc = mhsa_sublayer_forward(k->attn, k->work.p, B, T, k->nw[1].data(), k->nb[1].data(), kNormEps,
+                                         pos_emb, pos_len, ctx, lens, s))
+    return rc;
+  float* o = static_cast<float*>(out);
+  if (int32_t rc = mhsa_conv_sublayer_to_f32(k->conv, k->work.p, xdt, B, T, lens, k->nw[2].data(), k->nb[2].data(),
+                                             kNormEps, o, s))
+    return rc;
+  if (int32_t rc = mhsa_ffn_sublayer_forward_f32(k->ff2, o, rows, k->nw[3].data(), k->nb[3].data(), kNormEps, s))
+    return rc;
+  const float* gd;
+  const float* bd;
+  if (int32_t rc = upload_out_norm(k, &gd, &bd)) return rc;
+  HIPCHK(mhsa::layer_norm(mhsa::kF32, o, o, gd, bd, kNormEps, rows, k->D, s));
+  return MHSA_OK;
+}
+
+int32_t dtype_code(int32_t d, DType* out) {
+  if (d == MHSA_F32) *out = mhsa::kF32;
+  else if (d == MHSA_BF16) *out = mhsa::kBF16;
+  else return fail(MHSA_EINVAL, "dtype %d is not f32 or bf16", d);
   return MHSA_OK;
 }
 
@@ -220,6 +304,68 @@ int32_t mhsa_encoder_forward(mhsa_block* const* blocks, int32_t n_layers, void* 
     if (int32_t rc = block_forward(blocks[l], x, batch, seq_len, pos_emb, pos_len, ctx, lengths,
                                    static_cast<hipStream_t>(hs)))
       return rc;
+  return MHSA_OK;
+}
+
+int32_t mhsa_block_output_dtype(const mhsa_block* k, int32_t x_dtype) {
+  DType xdt;
+  if (!k || (x_dtype != MHSA_F32 && x_dtype != MHSA_BF16)) return -1;
+  xdt = x_dtype == MHSA_F32 ? mhsa::kF32 : mhsa::kBF16;
+  if (xdt != k->dt && xdt != mhsa::kF32) return -1;
+  return block_out_dtype(k, xdt) == mhsa::kF32 ? MHSA_F32 : MHSA_BF16;
+}
+
+int32_t mhsa_block_forward_to(mhsa_block* k, const void* x, int32_t x_dtype, int32_t batch, int32_t seq_len,
+                              const void* pos_emb, int32_t pos_len, const mhsa_context* ctx, const int32_t* lengths,
+                              void* out, void* hs) {
+  if (int32_t rc = check_block(k)) return rc;
+  DType xdt;
+  if (int32_t rc = dtype_code(x_dtype, &xdt)) return rc;
+  return block_forward_to(k, x, xdt, batch, seq_len, pos_emb, pos_len, ctx, lengths, out,
+                          static_cast<hipStream_t>(hs));
+}
+
+int32_t mhsa_encoder_forward_to(mhsa_block* const* blocks, int32_t n_layers, const void* x, int32_t x_dtype,
+                                int32_t batch, int32_t seq_len, const void* pos_emb, int32_t pos_len,
+                                const mhsa_context* ctx, const int32_t* lengths, void* out, void* hs) {
+  if (!blocks || n_layers <= 0) return fail(MHSA_EINVAL, "null or empty block list");
+  DType xdt;
+  if (int32_t rc = dtype_code(x_dtype, &xdt)) return rc;
+  // every block checked, and the activations' dtype followed through the
+  // stack, before the first launch
+  DType dt = xdt;
+  for (int l = 0; l < n_layers; ++l) {
+    if (!blocks[l]) return fail(MHSA_EINVAL, "block %d is null", l);
+    if (blocks[l]->D != blocks[0]->D || blocks[l]->dt != blocks[0]->dt)
+      return fail(MHSA_EINVAL, "block %d differs from block 0 in d_model or dtype", l);
+    if (dt != blocks[l]->dt && dt != mhsa::kF32)
+      return fail(MHSA_EINVAL, "activations in dtype %d for a block of dtype %d", (int)dt, (int)blocks[l]->dt);
+    dt = block_out_dtype(blocks[l], dt);
+  }
+  // one pos_emb, context and padding for every layer (conformer.rs:542-550):
+  // the first block moves x to out, the others run on out
+  hipStream_t s = static_cast<hipStream_t>(hs);
+  if (int32_t rc = block_forward_to(blocks[0], x, xdt, batch, seq_len, pos_emb, pos_len, ctx, lengths, out, s))
+    return rc;
+  dt = block_out_dtype(blocks[0], xdt);
+  for (int l = 1; l < n_layers; ++l) {
+    const DType odt = block_out_dtype(blocks[l], dt);
+    if (odt != dt) {
+      // bf16 activations turning f32 here: out cannot hold both, so they
+      // move to the block's own bf16 copy (block_forward_to copies them)
+      // and the f32 result lands in out
+      const size_t bytes = (size_t)batch * seq_len * blocks[l]->D * 2;
+      HIPCHK(blocks[l]->work.ensure(align_up((int64_t)bytes, 256)));
+      HIPCHK(hipMemcpyAsync(blocks[l]->work.p, out, bytes, hipMemcpyDeviceToDevice, s));
+      if (int32_t rc = block_forward_to(blocks[l], blocks[l]->work.p, dt, batch, seq_len, pos_emb, pos_len, ctx,
+                                        lengths, out, s))
+        return rc;
+    } else if (int32_t rc = block_forward_to(blocks[l], out, dt, batch, seq_len, pos_emb, pos_len, ctx, lengths,
+                                             out, s)) {
+      return rc;
+    }
+    dt = odt;
+  }
   return MHSA_OK;
 }
 

@@ -24,6 +24,7 @@
 #include "../../include/relpos_mhsa.h"
 #include "host_common.hpp"
 #include "kernels.hpp"
+#include "sublayers.hpp"
 
 using mhsa::DType;
 
@@ -1070,8 +1071,11 @@ namespace {
 // One cache-aware step (S != null: the chunk against the stream's ring) or
 // the no-cache form (S == null: keys and values from x alone,
 // attention.rs:687-700), both in fp32 (prepare_stream says why).
+// lens (no cache only): the offline key padding, keys past lens[b] (clamped
+// to >= 1) hidden as offline_key_bounds hides them.
 int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, const void* pos_emb, int pos_len,
-                    const mhsa_stream_mask* mask, void* out, hipStream_t s, const void* residual = nullptr) {
+                    const mhsa_stream_mask* mask, void* out, hipStream_t s, const void* residual = nullptr,
+                    const int32_t* lens = nullptr) {
   if (!x || !pos_emb || !out) return fail(MHSA_EINVAL, "null tensor pointer");
   if (!aligned16(x) || !aligned16(pos_emb) || !aligned16(out))
     return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
@@ -1200,7 +1204,7 @@ int32_t stream_step(mhsa_layer* L, mhsa_stream* S, const void* x, int B, int T, 
         L, mhsa::kF32, a, B,
         [&](int b, int& lo, int& hi, int& qv) {
           lo = masked ? C - used[b] : 0;  // unfilled cache rows (conformer.rs:155-181)
-          hi = Lk;
+          hi = lens && !S ? std::min(std::max(lens[b], 1), T) : Lk;
           qv = masked && mask->valid_host ? std::min(std::max(mask->valid_host[b], 0), T) : T;
         },
         s);
@@ -1235,6 +1239,33 @@ int32_t mhsa_forward_uncached(mhsa_layer* L, const void* x, int32_t batch, int32
 }
 
 }  // extern "C"
+
+int32_t mhsa_sublayer_forward_act32(mhsa_layer* L, float* x, int B, int T, const float* gamma, const float* beta,
+                                    float eps, const void* pos_emb, int pos_len, const mhsa_context* ctx,
+                                    const int32_t* lens, hipStream_t s) {
+  if (int32_t rc = check_layer(L)) return rc;
+  if (!x || B <= 0 || T <= 0) return fail(MHSA_EINVAL, "bad sublayer arguments");
+  if (!aligned16(x)) return fail(MHSA_EINVAL, "device tensors must be 16-byte aligned");
+  const int64_t rows = (int64_t)B * T;
+  const float* gd = nullptr;
+  const float* bd = nullptr;
+  if (int32_t rc = sublayer_norm(L, gamma, beta, rows, &gd, &bd)) return rc;
+  HIPCHK(L->hbuf.ensure(align_up(rows * L->D * 4, 256)));  // the f32 LayerNorm output
+  {
+    LayerProf ps(L, "layer_norm", s);
+    for (int r = ps.reps(); r > 0; --r)
+      HIPCHK(mhsa::layer_norm(mhsa::kF32, x, L->hbuf.p, gd, bd, eps, (int)rows, L->D, s));
+  }
+  // forward projects its position rows on every call (attention.rs:511),
+  // so the streaming path's memo is not reused across calls
+  L->pmemo_len = -1;
+  mhsa_stream_mask m{};
+  if (ctx) {
+    m.present = 1;
+    m.ctx = *ctx;
+  }
+  return stream_step(L, nullptr, L->hbuf.p, B, T, pos_emb, pos_len, ctx ? &m : nullptr, x, s, x, lens);
+}
 
 struct mhsa_stack {
   std::vector<mhsa_layer*> layers;

@@ -47,7 +47,8 @@ EXPORTS = (
     "mhsa_pos_encoding",
     "mhsa_block_create", "mhsa_block_destroy", "mhsa_block_set_dtype", "mhsa_block_load_weights",
     "mhsa_block_attention", "mhsa_block_feed_forward", "mhsa_block_conv", "mhsa_block_forward",
-    "mhsa_encoder_forward", "mhsa_encoder_create", "mhsa_encoder_destroy", "mhsa_encoder_load_cache",
+    "mhsa_encoder_forward", "mhsa_block_output_dtype", "mhsa_block_forward_to", "mhsa_encoder_forward_to",
+    "mhsa_encoder_create", "mhsa_encoder_destroy", "mhsa_encoder_load_cache",
     "mhsa_encoder_read_cache", "mhsa_encoder_fill", "mhsa_encoder_step",
     "mhsa_ffn_profile_enable", "mhsa_ffn_profile_repeat", "mhsa_ffn_profile_reset", "mhsa_ffn_profile_count",
     "mhsa_ffn_profile_entry", "mhsa_ffn_debug_linear", "mhsa_conv_debug_linear",
@@ -168,6 +169,9 @@ def library(path: str = LIB_PATH) -> ctypes.CDLL:
         "mhsa_block_conv": (VP, [VP]),
         "mhsa_block_forward": (I, [VP, VP, I, I, VP, I, P(Context), PI, VP]),
         "mhsa_encoder_forward": (I, [P(VP), I, VP, I, I, VP, I, P(Context), PI, VP]),
+        "mhsa_block_output_dtype": (I, [VP, I]),
+        "mhsa_block_forward_to": (I, [VP, VP, I, I, I, VP, I, P(Context), PI, VP, VP]),
+        "mhsa_encoder_forward_to": (I, [P(VP), I, VP, I, I, I, VP, I, P(Context), PI, VP, VP]),
         "mhsa_encoder_create": (I, [P(VP), I, I, I, I, P(VP)]),
         "mhsa_encoder_destroy": (None, [VP]),
         "mhsa_encoder_load_cache": (I, [VP, VP, VP, PI, VP]),
@@ -1130,6 +1134,36 @@ class ConformerBlock:
                                             _stream_ptr()))
         return x
 
+    def output_dtype(self, x_dtype):
+        """Dtype of forward's result on activations in x_dtype: f32 once they
+        are f32 or the conv is causal (its f32 zero padding promotes a bf16
+        block, conformer.rs:2250-2256), else the block dtype."""
+        code = self._lib.mhsa_block_output_dtype(self._h, _dtype_code(x_dtype))
+        if code < 0:
+            raise MhsaError(MHSA_EINVAL, f"a {self.dtype} block cannot take {x_dtype} activations")
+        return _torch_dtype(code)
+
+    def forward(self, x, pos_emb, context: Optional[AttentionContext] = None,
+                lengths: Optional[Sequence[int]] = None):
+        """block(x) as a new tensor (conformer.rs:1693-1875) in
+        output_dtype(x.dtype): x in the block dtype or, in a bf16 block, f32
+        activations an earlier causal conv promoted."""
+        import torch
+        b, t, d = x.shape
+        pe = pos_emb.reshape(-1, d)
+        if not x.is_cuda or not x.is_contiguous() or not pe.is_cuda or not pe.is_contiguous():
+            raise MhsaError(MHSA_EINVAL, "expected contiguous GPU tensors")
+        if pe.dtype != _torch_dtype(self._dtype):
+            raise MhsaError(MHSA_EINVAL, f"pos_emb must be {self.dtype}")
+        if lengths is not None and len(lengths) != b:
+            raise MhsaError(MHSA_EINVAL, f"lengths must have {b} entries")
+        out = torch.empty((b, t, d), dtype=self.output_dtype(x.dtype), device=x.device)
+        ctx = context.c() if context is not None else None
+        _check(self._lib.mhsa_block_forward_to(self._h, _dptr(x), _dtype_code(x.dtype), b, t, _dptr(pe),
+                                               pe.shape[0], ctypes.byref(ctx) if ctx is not None else None,
+                                               _int_array(lengths), _dptr(out), _stream_ptr()))
+        return out
+
 
 def encoder_forward_(blocks: Sequence[ConformerBlock], x, pos_emb, context=None, lengths=None):
     """The offline encoder's layer loop over blocks (conformer.rs:542-550), in place."""
@@ -1144,6 +1178,30 @@ def encoder_forward_(blocks: Sequence[ConformerBlock], x, pos_emb, context=None,
                                                ctypes.byref(ctx) if ctx is not None else None,
                                                _int_array(lengths), _stream_ptr()))
     return x
+
+
+def encoder_forward(blocks: Sequence[ConformerBlock], x, pos_emb, context=None, lengths=None):
+    """The offline encoder's layer loop over blocks (conformer.rs:542-550) as
+    a new tensor, whose dtype follows the blocks' output_dtype (f32 after the
+    first causal conv of a bf16 stack)."""
+    import torch
+    blocks = list(blocks)
+    if not blocks:
+        raise MhsaError(MHSA_EINVAL, "the encoder needs at least one block")
+    b, t, d = x.shape
+    pe = pos_emb.reshape(-1, d)
+    if not x.is_cuda or not x.is_contiguous() or not pe.is_cuda or not pe.is_contiguous():
+        raise MhsaError(MHSA_EINVAL, "expected contiguous GPU tensors")
+    dt = x.dtype
+    for k in blocks:
+        dt = k.output_dtype(dt)
+    out = torch.empty((b, t, d), dtype=dt, device=x.device)
+    ctx = context.c() if context is not None else None
+    arr = (ctypes.c_void_p * len(blocks))(*[k._h.value for k in blocks])
+    _check(blocks[0]._lib.mhsa_encoder_forward_to(arr, len(blocks), _dptr(x), _dtype_code(x.dtype), b, t, _dptr(pe),
+                                                  pe.shape[0], ctypes.byref(ctx) if ctx is not None else None,
+                                                  _int_array(lengths), _dptr(out), _stream_ptr()))
+    return out
 
 
 class StreamingEncoder:

@@ -619,7 +619,10 @@ def layer_norm(x: np.ndarray, gamma=None, beta=None, eps: float = 1e-5,
 
 def mhsa_sublayer(p: MhsaParams, x, pos_emb, context=None, key_mask=None,
                   gamma=None, beta=None, dtype: str = F32, eps: float = 1e-5):
-    """x + MHSA(LayerNorm(x)) (conformer.rs:1747-1780)."""
+    """x + MHSA(LayerNorm(x)) (conformer.rs:1747-1780); the norm parameters
+    hold their `dtype` values (set_dtype casts the norms, conformer.rs:1656)."""
+    gamma = None if gamma is None else to_dtype(gamma, dtype)
+    beta = None if beta is None else to_dtype(beta, dtype)
     h = layer_norm(x, gamma, beta, eps, dtype)
     a = mhsa_forward(p, h, pos_emb, context, key_mask, dtype)
     return _rnd(np.asarray(x, dtype=np.float64) + a, dtype)
@@ -833,19 +836,32 @@ class ConformerBlockParams:
 
 
 def conformer_block(p: ConformerBlockParams, x, pos_emb, context: Optional[AttentionContext] = None,
-                    lengths=None, dtype: str = F32):
+                    lengths=None, dtype: str = F32, act: Optional[str] = None, pos_rows=None):
     """ConformerBlock::forward (conformer.rs:1693-1875) on x [B, T, D] in
     `dtype`: x + 0.5 FF1(LN(x)) (1703-1729), x + MHSA(LN(x)) with the key
     padding mask of `lengths` (1747-1780), x + conv(LN(x)) with frames past
     `lengths` zeroed (1790-1814), x + 0.5 FF2(LN(x)) (1827-1851), then
     norm_out (1862). `lengths` builds PaddingMask (conformer.rs:1594-1615):
     None when no frame is padding. A causal conv in a bf16 block promotes
-    the rest of the block to f32 (the conv's f32 padding), as MLX does."""
+    the rest of the block to f32 (the conv's f32 padding), as MLX does.
+
+    `act` is the dtype x is stored in (default `dtype`): F32 in a bf16 block
+    means activations an earlier block's causal conv promoted, so that every
+    op of this block runs in f32 on the bf16 parameter values -- the
+    attention as `forward` (attention.rs:446-573) computes it from an f32 x:
+    f32 projections, matrix_bd = q_v (f32) . linear_pos(pos_emb) (bf16) in
+    f32, the scale cast to f32 and the additive mask; the arithmetic of
+    mhsa_forward_with_cache without a cache, whose `pos_rows` it passes on
+    (a test can feed a kernel's own bf16 position rows)."""
     x = np.asarray(x, dtype=np.float64)
     t_ = x.shape[1]
     if lengths is not None and all(int(v) >= t_ for v in lengths):
         lengths = None  # PaddingMask::new gives None
     key_mask = key_padding_mask(lengths, t_) if lengths is not None else None
+    if (act or dtype) != dtype:
+        if act != F32:
+            raise ValueError("activations other than the block dtype are f32")
+        return _conformer_block_f32_activations(p, x, pos_emb, context, key_mask, lengths, dtype, pos_rows)
     x = feed_forward_sublayer(p.ff1, x, *p.ff1_norm, dtype=dtype)
     x = mhsa_sublayer(p.attn, x, pos_emb, context, key_mask, *p.attn_norm, dtype=dtype)
     x, _ = conv_sublayer(p.conv, x, *p.conv_norm, dtype=dtype, lengths=lengths)
@@ -854,6 +870,45 @@ def conformer_block(p: ConformerBlockParams, x, pos_emb, context: Optional[Atten
     g, b = p.out_norm
     return layer_norm(x, None if g is None else to_dtype(g, dtype), None if b is None else to_dtype(b, dtype),
                       1e-5, act)
+
+
+def _conformer_block_f32_activations(p: ConformerBlockParams, x, pos_emb, context, key_mask, lengths, dtype,
+                                     pos_rows=None):
+    """conformer_block on activations stored in f32 in a `dtype` block: each
+    sublayer as in the f32-activation forms above, the attention as
+    mhsa_forward_with_cache without a cache and with the offline additive
+    mask (attention.rs:533-543) over the whole query range."""
+    t_ = x.shape[1]
+
+    def norm(pair):
+        g, b = pair
+        return None if g is None else to_dtype(g, dtype), None if b is None else to_dtype(b, dtype)
+
+    x = feed_forward_sublayer(p.ff1, x, *p.ff1_norm, dtype=dtype, act=F32)  # 1703-1729
+    h = layer_norm(x, *norm(p.attn_norm), 1e-5, F32)
+    mask = _offline_mask(context, key_mask, 0, t_, t_)
+    if mask is not None:  # [B|1, T, T] as mhsa_forward_with_cache takes it
+        mask = np.broadcast_to(mask, np.broadcast_shapes(mask.shape, (1, 1, t_, t_)))
+        mask = mask.reshape(mask.shape[0], t_, t_)
+    a, _ = mhsa_forward_with_cache(p.attn, h, pos_emb, None, mask, dtype, pos_rows=pos_rows)  # 1747-1780
+    x = _rnd(x + a, F32)
+    x, _ = conv_sublayer(p.conv, x, *p.conv_norm, dtype=dtype, act=F32, lengths=lengths)  # 1790-1814
+    x = feed_forward_sublayer(p.ff2, x, *p.ff2_norm, dtype=dtype, act=F32)  # 1827-1851
+    return layer_norm(x, *norm(p.out_norm), 1e-5, F32)  # 1862
+
+
+def conformer_encoder(blocks, x, pos_emb, context: Optional[AttentionContext] = None, lengths=None,
+                      dtype: str = F32, pos_rows=None):
+    """The offline encoder's layer loop (conformer.rs:542-550): every block on
+    one pos_emb, context and padding, the activations turning f32 at the first
+    causal conv of a bf16 stack; `pos_rows` [blocks] as conformer_block takes
+    them. Returns (x, the dtype x ends in)."""
+    act = dtype
+    for i, p in enumerate(blocks):
+        x = conformer_block(p, x, pos_emb, context, lengths, dtype, act, None if pos_rows is None else pos_rows[i])
+        if p.conv.causal:
+            act = F32
+    return x, act
 
 
 def conformer_block_with_cache(p: ConformerBlockParams, x, pos_emb, att_cache, conv_cache, att_mask=None,

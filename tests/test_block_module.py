@@ -103,3 +103,50 @@ def test_encoder_checks_its_blocks():
     assert lib.mhsa_encoder_create(None, 1, 2, 8, 4, ctypes.byref(h)) == M.MHSA_EINVAL
     arr = (ctypes.c_void_p * 1)(causal._h.value)
     assert lib.mhsa_encoder_create(arr, 1, 2, 8, 4, None) == M.MHSA_EINVAL
+
+
+def test_forward_to_dtypes_and_argument_checks():
+    """mhsa_block_output_dtype: f32 once the activations are f32 or the conv
+    is causal (its f32 zero padding promotes a bf16 block,
+    conformer.rs:2250-2256), else the block dtype; bf16 activations into an
+    f32 block are not a case. mhsa_block_forward_to and
+    mhsa_encoder_forward_to reject bad arguments before any device work
+    (the addresses below are never dereferenced)."""
+    lib = M.library()
+    sym = M.ConformerBlock(D, H, F, K, "batch_norm", causal=False)
+    cau = M.ConformerBlock(D, H, F, K, "layer_norm", causal=True)
+    for blk in (sym, cau):
+        assert lib.mhsa_block_output_dtype(blk._h, M.F32) == M.F32
+        assert lib.mhsa_block_output_dtype(blk._h, M.BF16) == -1
+    sym.set_dtype("bfloat16")
+    cau.set_dtype("bfloat16")
+    assert lib.mhsa_block_output_dtype(sym._h, M.BF16) == M.BF16
+    assert lib.mhsa_block_output_dtype(cau._h, M.BF16) == M.F32
+    assert lib.mhsa_block_output_dtype(sym._h, M.F32) == M.F32
+    assert lib.mhsa_block_output_dtype(cau._h, M.F32) == M.F32
+    assert lib.mhsa_block_output_dtype(None, M.F32) == -1
+    assert lib.mhsa_block_output_dtype(sym._h, 7) == -1
+    import torch
+    assert cau.output_dtype(torch.bfloat16) == torch.float32 and sym.output_dtype("bfloat16") == torch.bfloat16
+
+    x, o, pe = ctypes.c_void_p(1 << 20), ctypes.c_void_p(2 << 20), ctypes.c_void_p(3 << 20)
+
+    def fwd(blk, xp, dt, out, b=2, t=8):
+        return lib.mhsa_block_forward_to(blk._h, xp, dt, b, t, pe, 2 * t - 1, None, None, out, None)
+
+    f32blk = M.ConformerBlock(D, H, F, K)
+    assert fwd(sym, x, 7, o) == M.MHSA_EINVAL  # not a dtype
+    assert fwd(f32blk, x, M.BF16, o) == M.MHSA_EINVAL  # bf16 activations in an f32 block
+    assert fwd(cau, x, M.BF16, x) == M.MHSA_EINVAL  # the f32 result over its bf16 input
+    assert b"overlap" in lib.mhsa_last_error()
+    assert fwd(cau, x, M.BF16, ctypes.c_void_p((1 << 20) + 2 * 8 * D)) == M.MHSA_EINVAL  # partly overlapping
+    assert fwd(cau, ctypes.c_void_p((1 << 20) + 8), M.BF16, o) == M.MHSA_EINVAL  # misaligned
+    assert fwd(sym, x, M.BF16, o, b=0) == M.MHSA_EINVAL
+    assert lib.mhsa_block_forward_to(None, x, M.F32, 2, 8, pe, 15, None, None, o, None) == M.MHSA_EINVAL
+    # the encoder checks its blocks and follows the dtype through them first
+    enc = lambda blocks, dt: lib.mhsa_encoder_forward_to((ctypes.c_void_p * len(blocks))(*[k._h.value for k in blocks]),
+                                                       len(blocks), x, dt, 2, 8, pe, 15, None, None, o, None)
+    assert enc([f32blk, cau], M.F32) == M.MHSA_EINVAL  # dtypes differ
+    assert b"differs from block 0" in lib.mhsa_last_error()
+    assert enc([cau, sym], 7) == M.MHSA_EINVAL
+    assert lib.mhsa_encoder_forward_to(None, 1, x, M.BF16, 2, 8, pe, 15, None, None, o, None) == M.MHSA_EINVAL

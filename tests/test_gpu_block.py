@@ -11,6 +11,8 @@ three ulps (0.03-0.05) from the oracle's; measured 265 (dense) and 1082 (u8)
 of 614400 outputs past 2e-2 absolute, largest 0.047 at row maxima ~4, and
 the check also bounds that count at 1%.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -92,6 +94,106 @@ def test_block_bf16_causal_conv_is_refused():
     with pytest.raises(M.MhsaError) as e:
         blk.forward_(x, pos)
     assert e.value.code == M.MHSA_ENOTSUP
+
+
+@pytest.mark.parametrize("quant", [False, True])
+def test_block_forward_to_bf16_causal_against_oracle(quant):
+    """A bf16 block with a causal conv (kernel 9, LayerNorm) on bf16 input:
+    FF1 and the MHSA sublayer in bf16, then the conv's f32 zero padding
+    promotes the depthwise conv and everything after it (conformer.rs:
+    2250-2256), so the block returns f32 (mhsa_block_forward_to). 0.6B
+    shape at B=3, T=200 with lengths (200, 131, 57), dense or affine u8
+    projections, against conformer_block; the bf16 sublayers' roundings
+    carry into the f32 result, so the bound is the bf16 block's. x is left
+    as it was."""
+    d, h, f, k, B, T = 1024, 8, 4096, 9, 3, 200
+    rng = np.random.default_rng(80 + quant)
+    w = block_weights(rng, d, h, f, k, "layer_norm", quant)
+    p = block_oracle(w, d, h, "layer_norm", True)
+    lengths = [200, 131, 57]
+    x = O.to_dtype(rng.standard_normal((B, T, d)), O.BF16)
+    pos = O.to_dtype(O.RelPositionalEncoding(d, 5000, True).get_encoding(T), O.BF16)
+    blk = gpu_block(w, d, h, f, k, "layer_norm", True, O.BF16)
+    assert blk.output_dtype(torch.bfloat16) == torch.float32
+    xd = dev(x, O.BF16)
+    x0 = xd.clone()
+    out = blk.forward(xd, dev(pos, O.BF16), None, lengths)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32 and torch.equal(xd, x0)
+    got = host(out)
+    ref = O.conformer_block(p, x, pos, None, lengths, O.BF16)
+    assert not np.array_equal(ref, O.bf16_round(ref))  # the oracle's result is f32 too
+    err = row_rel_err(got, ref)
+    n_far = int(np.sum(np.abs(got - ref) > BF16_TOL))
+    print(f"bf16 causal block quant={quant}: max |err| {np.max(np.abs(got - ref)):.3e}, per-row error / row max "
+          f"{err:.3e}, {n_far} of {got.size} outputs beyond {BF16_TOL}")
+    assert err < BF16_TOL
+    assert n_far <= 1e-2 * got.size
+
+
+@pytest.mark.parametrize("ctx,quant", [(None, False), (((100, 8), "regular"), True),
+                                       (((160, 15), "chunked_limited"), False)])
+def test_block_forward_to_f32_activations_against_oracle(ctx, quant):
+    """A bf16 block on f32 activations (what every block after the first
+    causal conv of a bf16 encoder receives): every op in f32 on the bf16
+    parameter values, the attention as the offline forward computes it from
+    an f32 x -- key padding (lengths 180, 97), the context, matrix_bd in
+    f32 over the layer's bf16 position rows (handed to the oracle, as in the
+    streaming tests) -- against conformer_block(act=f32) at the f32 bound.
+    In place (out = x). (Each window reaches key 0 from every row: a row
+    that sees no key is NaN in the reference.)"""
+    d, h, f, k, B, T = 512, 4, 2048, 9, 2, 180
+    rng = np.random.default_rng(83 + quant)
+    w = block_weights(rng, d, h, f, k, "layer_norm", quant)
+    p = block_oracle(w, d, h, "layer_norm", True)
+    lengths = [180, 97]
+    context = M.AttentionContext.new(*ctx) if ctx else None
+    octx = O.AttentionContext.new(*ctx) if ctx else None
+    x = rng.standard_normal((B, T, d)).astype(np.float32).astype(np.float64)
+    pos = O.to_dtype(O.RelPositionalEncoding(d, 5000, True).get_encoding(T), O.BF16)
+    blk = gpu_block(w, d, h, f, k, "layer_norm", True, O.BF16)
+    pos_d = dev(pos, O.BF16)
+    xd = dev(x, O.F32)
+    assert blk.output_dtype(torch.float32) == torch.float32
+    lib = M.library()
+    M._check(lib.mhsa_block_forward_to(blk._h, M._dptr(xd), M.F32, B, T, M._dptr(pos_d), pos_d.shape[1],
+                                       ctypes.byref(context.c()) if context else None, M._int_array(lengths),
+                                       M._dptr(xd), M._stream_ptr()))
+    got = host(xd)
+    ref = O.conformer_block(p, x, pos, octx, lengths, O.BF16, act=O.F32, pos_rows=_layer_pos_rows(blk, pos_d))
+    err = row_rel_err(got, ref)
+    print(f"bf16 block on f32 activations ctx={ctx} quant={quant}: per-row error / row max {err:.3e}")
+    assert err < F32_TOL
+
+
+def test_encoder_forward_to_promotes_like_the_block_loop():
+    """mhsa_encoder_forward_to over bf16 blocks (symmetric, causal, causal):
+    bf16 activations through the first, f32 from the second's conv on (the
+    loop moves them out of the output buffer before the promotion), equal
+    bit for bit to chaining ConformerBlock.forward, and against the oracle's
+    conformer_encoder with each layer's bf16 position rows."""
+    d, h, f, k, B, T = 512, 4, 2048, 9, 2, 150
+    rng = np.random.default_rng(86)
+    kinds = [("batch_norm", False), ("layer_norm", True), ("layer_norm", True)]
+    ws = [block_weights(rng, d, h, f, k, nrm, False, prefix=f"l{i}") for i, (nrm, _) in enumerate(kinds)]
+    ps = [block_oracle(w, d, h, nrm, c, prefix=f"l{i}") for i, (w, (nrm, c)) in enumerate(zip(ws, kinds))]
+    blks = [gpu_block(w, d, h, f, k, nrm, c, O.BF16, prefix=f"l{i}") for i, (w, (nrm, c)) in enumerate(zip(ws, kinds))]
+    x = O.to_dtype(rng.standard_normal((B, T, d)), O.BF16)
+    pos = O.to_dtype(O.RelPositionalEncoding(d, 5000, True).get_encoding(T), O.BF16)
+    xd, pos_d = dev(x, O.BF16), dev(pos, O.BF16)
+    lengths = [150, 97]
+    y = xd
+    for blk in blks:
+        y = blk.forward(y, pos_d, None, lengths)
+    out = M.encoder_forward(blks, xd, pos_d, None, lengths)
+    torch.cuda.synchronize()
+    assert out.dtype == torch.float32 and torch.equal(out, y)
+    rows = [_layer_pos_rows(blk, pos_d) for blk in blks]
+    ref, act = O.conformer_encoder(ps, x, pos, None, lengths, O.BF16, pos_rows=rows)
+    assert act == O.F32
+    err = row_rel_err(host(out), ref)
+    print(f"encoder (bf16: symmetric, causal, causal): per-row error / row max {err:.3e}")
+    assert err < BF16_TOL
 
 
 def test_encoder_forward_equals_block_loop():

@@ -950,3 +950,68 @@ def test_conformer_block_streaming_equals_offline_chunked():
         y, att, conv = O.conformer_block_with_cache(p, seq[:, c * T:(c + 1) * T], pos, att, conv, m, None, O.F32)
         assert np.max(np.abs(y - whole[:, c * T:(c + 1) * T])) < 1e-10, c
         fill = O.next_fill(fill, T, 0, C)
+
+
+def _bf16_cast_block(p):
+    """The block's parameters as set_dtype(bf16) leaves them: every dense
+    weight, bias and norm parameter rounded to bf16 (the block's own dtype
+    stays f32 here)."""
+    r = lambda a: None if a is None else O.bf16_round(np.asarray(a, dtype=np.float64))
+    lin = lambda l: O.LinearLayer(r(l.weight), r(l.bias))
+    ffn = lambda f: O.FeedForwardParams(lin(f.linear1), lin(f.linear2))
+    a = p.attn
+    attn = O.MhsaParams(a.d_model, a.n_heads, lin(a.linear_q), lin(a.linear_k), lin(a.linear_v), lin(a.linear_out),
+                        lin(a.linear_pos), r(a.pos_bias_u), r(a.pos_bias_v))
+    c = p.conv
+    conv = O.ConvModuleParams(lin(c.pointwise_conv1), r(c.depthwise_weight), r(c.depthwise_bias),
+                              lin(c.pointwise_conv2), c.norm, r(c.norm_weight), r(c.norm_bias), r(c.running_mean),
+                              r(c.running_var), c.causal)
+    nrm = lambda pair: (r(pair[0]), r(pair[1]))
+    return O.ConformerBlockParams(ffn(p.ff1), nrm(p.ff1_norm), attn, nrm(p.attn_norm), conv, nrm(p.conv_norm),
+                                  ffn(p.ff2), nrm(p.ff2_norm), nrm(p.out_norm))
+
+
+@pytest.mark.parametrize("causal,ctx,lengths", [(True, None, [9, 6]), (False, ((3, 2), "regular"), None),
+                                                (True, ((8, 1), "chunked_limited"), [9, 1])])
+def test_conformer_block_f32_activations_is_the_f32_block_on_bf16_parameters(causal, ctx, lengths):
+    """A bf16 block on activations an earlier causal conv made f32 runs every
+    op in f32 on the bf16 parameter values (MLX promotion). With the conv's
+    norm a LayerNorm (BatchNorm's rsqrt term stays bf16) and linear_pos the
+    identity over a bf16 table (so its rows are exact in either dtype), that
+    is the f32 block on bf16-rounded parameters, equal in every output (the
+    two store the same f32 roundings), while the all-bf16 block is 1e-2
+    off. (The contexts keep key
+    0 in every row's window: a row that sees no key is NaN in the
+    reference.)"""
+    d, h, f, k, T = 16, 2, 32, 5, 9
+    p = _block_params(d, h, f, k, 56, causal=causal)
+    p.attn.linear_pos = O.LinearLayer(np.eye(d), None)
+    x = np.random.default_rng(57).standard_normal((2, T, d)).astype(np.float32).astype(np.float64)
+    pos = O.bf16_round(O.RelPositionalEncoding(d, 64, False).get_encoding(T))
+    context = O.AttentionContext.new(*ctx) if ctx else None
+    got = O.conformer_block(p, x, pos, context, lengths, O.BF16, act=O.F32)
+    ref = O.conformer_block(_bf16_cast_block(p), x, pos, context, lengths, O.F32)
+    scale = np.max(np.abs(ref))
+    assert np.array_equal(got, ref)
+    assert np.max(np.abs(O.conformer_block(p, O.bf16_round(x), pos, context, lengths, O.BF16) - got)) / scale > 1e-3
+
+
+def test_conformer_encoder_promotes_after_the_first_causal_conv():
+    """conformer_encoder: a bf16 stack keeps bf16 activations through
+    symmetric blocks and turns f32 at the first causal one; every later
+    block then takes f32 activations (conformer.rs:542-550 calls each block
+    on the previous block's returned array)."""
+    d, h, f, k, T = 16, 2, 32, 5, 7
+    ps = [_block_params(d, h, f, k, 60 + 5 * i, causal=c) for i, c in enumerate((False, True, True))]
+    x = O.bf16_round(np.random.default_rng(61).standard_normal((1, T, d)))
+    pos = O.bf16_round(O.RelPositionalEncoding(d, 64, False).get_encoding(T))
+    out, act = O.conformer_encoder(ps, x, pos, None, None, O.BF16)
+    assert act == O.F32
+    y0 = O.conformer_block(ps[0], x, pos, None, None, O.BF16)
+    assert np.array_equal(y0, O.bf16_round(y0))  # still bf16 after the symmetric block
+    y1 = O.conformer_block(ps[1], y0, pos, None, None, O.BF16)
+    assert not np.array_equal(y1, O.bf16_round(y1))  # f32 after the causal one
+    y2 = O.conformer_block(ps[2], y1, pos, None, None, O.BF16, act=O.F32)
+    assert np.array_equal(out, y2)
+    # an f32 stack never changes dtype
+    assert O.conformer_encoder(ps, x, pos, None, None, O.F32)[1] == O.F32
