@@ -161,16 +161,18 @@ int32_t block_forward_to(mhsa_block* k, const void* x, DType xdt, int B, int T, 
     return fail(MHSA_EINVAL, "activations in dtype %d for a block of dtype %d", (int)xdt, (int)k->dt);
   const DType odt = block_out_dtype(k, xdt);
   const size_t in_bytes = (size_t)B * T * k->D * mhsa::dtype_size(xdt);
+  const size_t out_bytes = (size_t)B * T * k->D * mhsa::dtype_size(odt);
+  const char* xb = static_cast<const char*>(x);
+  const char* ob = static_cast<const char*>(out);
+  if (out != x && xb < ob + out_bytes && ob < xb + in_bytes)
+    return fail(MHSA_EINVAL, "x and out must be the same buffer or not overlap");
   if (odt == xdt) {
     if (out != x) HIPCHK(hipMemcpyAsync(out, x, in_bytes, hipMemcpyDeviceToDevice, s));
     if (xdt == k->dt) return block_forward(k, out, B, T, pos_emb, pos_len, ctx, lens, s);
     return block_forward_act32(k, static_cast<float*>(out), B, T, pos_emb, pos_len, ctx, lens, s);
   }
   // bf16 activations into a causal bf16 block: bf16 up to the conv's padding
-  const char* xb = static_cast<const char*>(x);
-  const char* ob = static_cast<const char*>(out);
-  if (xb < ob + (size_t)B * T * k->D * 4 && ob < xb + in_bytes)
-    return fail(MHSA_EINVAL, "x and the f32 output must not overlap");
+  if (out == x) return fail(MHSA_EINVAL, "the f32 output cannot overwrite its bf16 input (x and out must not overlap)");
   if (x != k->work.p) {  // (the encoder loop may have put them there)
     HIPCHK(k->work.ensure(align_up((int64_t)in_bytes, 256)));
     HIPCHK(hipMemcpyAsync(k->work.p, x, in_bytes, hipMemcpyDeviceToDevice, s));

@@ -140,6 +140,7 @@ def test_forward_to_dtypes_and_argument_checks():
     assert fwd(cau, x, M.BF16, x) == M.MHSA_EINVAL  # the f32 result over its bf16 input
     assert b"overlap" in lib.mhsa_last_error()
     assert fwd(cau, x, M.BF16, ctypes.c_void_p((1 << 20) + 2 * 8 * D)) == M.MHSA_EINVAL  # partly overlapping
+    assert fwd(sym, x, M.BF16, ctypes.c_void_p((1 << 20) + 2 * 8 * D)) == M.MHSA_EINVAL  # the same, one dtype
     assert fwd(cau, ctypes.c_void_p((1 << 20) + 8), M.BF16, o) == M.MHSA_EINVAL  # misaligned
     assert fwd(sym, x, M.BF16, o, b=0) == M.MHSA_EINVAL
     assert lib.mhsa_block_forward_to(None, x, M.F32, 2, 8, pe, 15, None, None, o, None) == M.MHSA_EINVAL
