@@ -22,6 +22,7 @@
 // skipped, so a +-w local window costs O(T w) instead of O(T^2).
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -746,9 +747,12 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
   __syncthreads();
   if (jfirst < jend) carry = pack(band_tile(rrw));
 
-  int buf = 0;
   bool have_carry = true;  // carry holds band tile 0 of the current key tile
-  for (int j0 = jfirst; j0 < jend; j0 += NK, buf ^= 1) {
+  // Key tile j0 from LDS buffer BUF::value, a literal in each of the loop's
+  // two calls below, so that the buffer's base folds into the immediate
+  // offsets of the K and V^T fragment reads.
+  auto key_tile = [&](int j0, auto BUF) {
+    constexpr int buf = decltype(BUF)::value;
     const bool more = j0 + NK < jend;
     // the next key tile and its 64 new ring rows (last read before the
     // previous barrier; awaited at the next one), issued one load per MFMA
@@ -776,7 +780,7 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
         rrw += NK;
         have_carry = false;
         __syncthreads();
-        continue;
+        return;
       }
     }
     // after a skipped tile, band tile 0 from its ring rows (present since
@@ -786,13 +790,16 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
       have_carry = true;
     }
 
-    // Band tiles first, each stored to the remap strip as soon as it is
-    // done (rel_shift: strip column n of query column c pairs with key
-    // j0 + n - 31 + c), so few accumulators are live at once.
+    // Band tiles first, then the score MFMAs, and the band tiles are stored
+    // to the remap strip (rel_shift: strip column n of query column c pairs
+    // with key j0 + n - 31 + c) while the score chains finish: the band
+    // chains' last results are ready by then, and the strip writes' latency
+    // runs beside the score MFMAs (xl_stack_u8 attention 3% faster than
+    // storing each band tile as soon as its chain ends).
     put(carry, 0);
+    floatx16 bt[NU];
     {
       // band tiles 1 .. NU as interleaved MFMA chains
-      floatx16 bt[NU];
       const char* rbt[NU];
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
@@ -817,10 +824,6 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
         if (st < C::KDMA + C::VDMA) dma_kv(st, jn, buf ^ 1);
         __builtin_amdgcn_sched_barrier(0);
       }
-#pragma unroll
-      for (int u = 0; u + 1 < NU; ++u) put(pack(bt[u]), u + 1);
-      carry = pack(bt[NU - 1]);
-      put(carry, NU);
     }
     rrw += NK;
 
@@ -848,6 +851,11 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    // the band tiles to the strip, their chains done while the score MFMAs ran
+#pragma unroll
+    for (int u = 0; u + 1 < NU; ++u) put(pack(bt[u]), u + 1);
+    carry = pack(bt[NU - 1]);
+    put(carry, NU);
     __builtin_amdgcn_wave_barrier();
 
     // x = q_u k + bd for this lane's keys jl(u, r) = 32u + 16(r / 8) + 8hh + r % 8:
@@ -967,6 +975,10 @@ __device__ __forceinline__ void attn_bf16_body(const AttnParams& p, int nb, int 
     }
 
     __syncthreads();  // waits for this wave's loads of the next tile first
+  };
+  for (int j0 = jfirst; j0 < jend; j0 += 2 * NK) {
+    key_tile(j0, std::integral_constant<int, 0>{});
+    if (j0 + NK < jend) key_tile(j0 + NK, std::integral_constant<int, 1>{});
   }
 
   const float l_tot = sum_xor32(l_run);
