@@ -224,6 +224,27 @@ __device__ __forceinline__ void gemm_tile_body(const GemmParams& p, int block, c
   };
 
   const int nk = p.K / 64;
+  // The residual's 16-byte runs this lane adds in the epilogue (its stores
+  // of 8 columns of C, below), loaded ahead of the operand stream: they are
+  // in registers when the k-loop ends instead of being fetched after it
+  // (an output GEMM with a residual measured 9% faster). They are the
+  // oldest loads in flight, so only the wait for the first stages covers
+  // them; every later wait count stays exact.
+  constexpr int CPR = C::WN / 8, RIT = (C::WM * CPR + 63) / 64;
+  constexpr bool RPRE = RIT <= 12;
+  const int row0 = m0 + wm * C::WM, col0 = n0 + wn * C::WN;
+  bf16x8 rpre[RPRE ? RIT : 1];
+  if constexpr (RPRE) {
+    if (p.R) {
+#pragma unroll
+      for (int it = 0; it < RIT; ++it) {
+        const int id = it * 64 + lane, r = id / CPR, c = id % CPR;
+        if (((C::WM * CPR) % 64 == 0 || id < C::WM * CPR) && row0 + r < m_end)
+          rpre[it] = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.R) + (int64_t)(row0 + r) * p.ldr +
+                                                       col0 + c * 8);
+      }
+    }
+  }
 #pragma unroll
   for (int st = 0; st < C::DIST; ++st) issue(min(st, nk - 1), st);
   if constexpr (QUANT) {
@@ -331,7 +352,6 @@ __device__ __forceinline__ void gemm_tile_body(const GemmParams& p, int block, c
   // wave: measured 6.2 against 2.5 us for the epilogue of a V block)
   __syncthreads();
   char* st = smem + w * C::REG;
-  const int row0 = m0 + wm * C::WM, col0 = n0 + wn * C::WN;
   // columns [col0, col0 + ncn) go to C, the rest of the block to V^T
   const int ncn = p.vt ? min(max(p.vt_col0 - col0, 0), C::WN) : C::WN;
   const bool vtw = ncn < C::WN;
@@ -362,9 +382,9 @@ __device__ __forceinline__ void gemm_tile_body(const GemmParams& p, int block, c
             *reinterpret_cast<bf16*>(stv + (j * 32 + 8 * q + 4 * (lane >> 5) + e) * C::OPT + (i * 32 + (lane & 31)) * 2) =
                 (bf16)acc[j][i][4 * q + e];
   }
-  constexpr int CPR = C::WN / 8;
   // 8 columns [col, col + 8) of block row r to C, with the bias and residual
-  auto store_c = [&](int r, int col, bf16x8 v) {
+  // (rv: the residual run, when prefetched)
+  auto store_c = [&](int r, int col, bf16x8 v, const bf16x8* rvp = nullptr) {
     const int row = row0 + r;
     if (p.bias || p.R || p.act) {
       float f[8];
@@ -384,7 +404,8 @@ __device__ __forceinline__ void gemm_tile_body(const GemmParams& p, int block, c
         for (int e = 0; e < 8; ++e) f[e] = silu_value<bf16>(f[e]);
       }
       if (p.R) {
-        const bf16x8 rv = *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.R) + (int64_t)row * p.ldr + col);
+        const bf16x8 rv =
+            rvp ? *rvp : *reinterpret_cast<const bf16x8*>(reinterpret_cast<const bf16*>(p.R) + (int64_t)row * p.ldr + col);
 #pragma unroll
         for (int e = 0; e < 8; ++e) f[e] = round_to<bf16>((float)rv[e] + p.res_scale * f[e]);
       }
@@ -400,7 +421,8 @@ __device__ __forceinline__ void gemm_tile_body(const GemmParams& p, int block, c
       const int r = id / CPR, c = id % CPR;
       if ((C::WM * CPR) % 64 && id >= C::WM * CPR) break;
       if (c * 8 >= ncn || row0 + r >= m_end) continue;
-      store_c(r, col0 + c * 8, *reinterpret_cast<const bf16x8*>(st + r * C::OP + c * 16));
+      store_c(r, col0 + c * 8, *reinterpret_cast<const bf16x8*>(st + r * C::OP + c * 16),
+              RPRE && p.R ? &rpre[RPRE ? it : 0] : nullptr);
     }
   } else if (ncn > 0) {
     // the C columns of a block staged only transposed: consecutive lanes on
