@@ -259,16 +259,36 @@ __device__ __forceinline__ void gemm_tile_body(const GemmParams& p, int block, c
       }
     }
   }
+  if constexpr (QUANT && C::DIST == 2) {
+    // each stage's scale sets right after its codes, and a wait for stage 0
+    // and its scales only: behind stage 1's codes then come set 1's scales
+    // and stage 2's codes, the count every later wait assumes (a 192x192 u8
+    // Q/K/V tile's prologue measured 3.1 us waiting for everything)
+    // (the empty asm statements keep the issue order the counts rely on)
+    issue(0, 0);
+    asm volatile("" ::: "memory");
+    sbload(0, 0);
+    asm volatile("" ::: "memory");
+    issue(min(1, nk - 1), 1);
+    asm volatile("" ::: "memory");
+    sbload(min(1, nk - 1), 1);
+    asm volatile("" ::: "memory");
+    constexpr int vm = C::NA + C::NB + C::TN;
+    static_assert(vm < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((vm & 15) | ((vm >> 4) << 14) | (7 << 4));  // lgkmcnt(0)
+    asm volatile("s_barrier" ::: "memory");
+  } else if constexpr (QUANT) {
 #pragma unroll
-  for (int st = 0; st < C::DIST; ++st) issue(min(st, nk - 1), st);
-  if constexpr (QUANT) {
-    // the loop's wait counts take the two scale sets as the last loads
-    // issued here, so this wait is for all of them
+    for (int st = 0; st < C::DIST; ++st) issue(min(st, nk - 1), st);
+    // with loads three or more stages ahead the loop's wait counts take the
+    // two scale sets as the last loads issued here, so this wait is for all
     sbload(0, 0);
     sbload(min(1, nk - 1), 1);
     __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) lgkmcnt(0): stage 0 landed
     __syncthreads();
   } else {
+#pragma unroll
+    for (int st = 0; st < C::DIST; ++st) issue(min(st, nk - 1), st);
     // stage 0 landed; the later stages' loads may stay in flight (the
     // xl_offline_bf16 step measured 2-3% faster than waiting for all)
     constexpr int vm = (C::DIST - 1) * (C::NA + C::NB);
