@@ -168,6 +168,34 @@ def test_feed_forward_dequant(dtype, f32_act, rows):
         exact(ff.debug_linear(which, unit_rows(rows, k, tdt)), expect(ref, rows), f"{name} rows={rows}")
 
 
+def test_projection_dequant_u8_two_stages():
+    """A 192-row u8 tile with only two k-stages: d_model 128 at 40000 rows
+    takes 192x128 tiles (three LDS stages, loads two ahead), whose prologue
+    waits for stage 0 and its scales with stage 1's codes and scales still in
+    flight; the loop's first wait must then cover them."""
+    d, rows = 128, 40000
+    rng = np.random.default_rng(128)
+    w = quant_layer(rng, d, 2)
+    layer = gpu_layer(w, d, 2, O.BF16)
+    x = unit_rows(rows, d, torch.bfloat16)
+    for name in LINEARS:
+        exact(layer.debug_linear(name, x), expect(deq(w, name, O.BF16), rows), f"{name} d_model={d} rows={rows}")
+
+
+def test_feed_forward_dequant_u8_one_stage():
+    """linear1 of a d_model-64 FeedForward (K = 64: one k-stage, so every
+    later load is a reload of it) at 40000 rows: 192x256 u8 tiles, three
+    stages."""
+    d, f, rows = 64, 256, 40000
+    rng = np.random.default_rng(64)
+    w = ffn_u8(rng, d, f)
+    ff = M.FeedForward(d, f, False)
+    ff.load_weights(w, "ff")
+    ff.set_dtype(O.BF16)
+    ref = O.dequantize(w["ff.linear1.weight"], w["ff.linear1.scales"], w["ff.linear1.biases"], 8, 64, O.BF16)
+    exact(ff.debug_linear(0, unit_rows(rows, d, torch.bfloat16)), expect(ref, rows), f"linear1 d_model={d} rows={rows}")
+
+
 @pytest.mark.parametrize("dtype,f32_act,rows", [(O.BF16, False, 3000), (O.BF16, True, 224), (O.F32, False, 1024)])
 def test_conv_pointwise_dequant(dtype, f32_act, rows):
     """ConvolutionModule's pointwise_conv1 [2048, 1024] and pointwise_conv2
