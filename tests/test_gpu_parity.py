@@ -189,6 +189,27 @@ def test_position_scores_bf16_match_rel_shift(d_model, n_heads, B, T):
                            f"at {np.argwhere(bad)[:3].tolist()}")
 
 
+@pytest.mark.parametrize("d_model,rows", [(128, 40000), (256, 40000)])
+def test_dense_projection_unit_rows_return_the_weights(d_model, rows):
+    """Unit rows (row r = e_{r mod K}) through the dense bf16 projections
+    return the bf16 weights exactly: each output is one product 1 * w. At
+    d_model 128 and 40000 rows the GEMM takes 192-row tiles with two k-stages
+    (three LDS stages), whose prologue waits for stage 0 only with stage 1's
+    loads in flight; at 256 it takes 192x256 tiles with four."""
+    rng = np.random.default_rng(d_model + rows)
+    w = W.make_layer_weights(rng, d_model, 2, False, False)
+    layer = gpu_layer(w, d_model, 2, False, O.BF16)
+    x = torch.zeros((rows, d_model), dtype=torch.bfloat16, device="cuda")
+    idx = torch.arange(rows, device="cuda")
+    x[idx, idx % d_model] = 1
+    for name in ("linear_q", "linear_k", "linear_v", "linear_out", "linear_pos"):
+        wb = torch.from_numpy(np.ascontiguousarray(w[f"{name}.weight"], dtype=np.float32)).bfloat16().float().numpy()
+        ref = wb.T[np.arange(rows) % d_model]
+        got = layer.debug_linear(name, x).float().cpu().numpy().reshape(ref.shape)
+        bad = got != ref
+        assert not bad.any(), f"{name}: {int(bad.sum())} of {bad.size} outputs differ, first at {np.argwhere(bad)[0]}"
+
+
 @pytest.mark.parametrize("quantized", [False, True])
 def test_paired_projections_equal_separate_launches(quantized):
     """At the xl_offline_bf16 shape (D=1024, B=8, T=375) the forward runs the
