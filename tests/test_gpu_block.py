@@ -84,6 +84,35 @@ def test_block_offline_against_oracle(dtype, quant, norm, causal):
         assert n_far <= 1e-2 * got.size
 
 
+@pytest.mark.parametrize("dtype,quant", [(O.BF16, False), (O.F32, True)])
+def test_block_offline_large_shape_against_oracle(dtype, quant):
+    """The FastConformer large shape (d_model 512, 8 heads of 64, ff 2048,
+    conv kernel 9): the d_k = 64 attention forms, the GEMMs at 512 and 2048
+    columns and the 512-wide LayerNorms inside one block, at B=4, T=250 with
+    key/frame padding (lengths 250, 199, 120, 33), against conformer_block."""
+    d, h, f, k, B, T = 512, 8, 2048, 9, 4, 250
+    rng = np.random.default_rng(512 + quant)
+    w = block_weights(rng, d, h, f, k, "batch_norm", quant)
+    p = block_oracle(w, d, h, "batch_norm", False)
+    lengths = [250, 199, 120, 33]
+    x = O.to_dtype(rng.standard_normal((B, T, d)), dtype)
+    pos = O.to_dtype(O.RelPositionalEncoding(d, 5000, True).get_encoding(T), dtype)
+    blk = gpu_block(w, d, h, f, k, "batch_norm", False, dtype)
+    xd = dev(x, dtype)
+    blk.forward_(xd, dev(pos, dtype), None, lengths)
+    got = host(xd)
+    ref = O.conformer_block(p, x, pos, None, lengths, dtype)
+    err = row_rel_err(got, ref)
+    if dtype == O.F32:
+        print(f"large block f32 quant={quant}: max per-row error / row max {err:.3e}")
+        assert err < F32_TOL
+    else:
+        n_far = int(np.sum(np.abs(got - ref) > BF16_TOL))
+        print(f"large block bf16: per-row error / row max {err:.3e}, {n_far} of {got.size} outputs beyond {BF16_TOL}")
+        assert err < BF16_TOL
+        assert n_far <= 1e-2 * got.size
+
+
 def test_block_bf16_causal_conv_is_refused():
     d, h, f, k = 256, 2, 512, 4
     rng = np.random.default_rng(72)
